@@ -1,0 +1,429 @@
+#!/usr/bin/env python3
+"""Benchmark of the hot path on one MI355X, in the driver's JSON-line format.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+A step is one call of the public entry point on inputs already resident in
+HBM. The default workload is BASELINE config 3, the bf16 GEMM 4096^3
+(``helion_mlir_utils.matmul``), whose TFLOP/s is ``value``; the same run also
+measures config 2's softmax and RMSNorm (bf16, [32768, 4096]) in HBM GB/s and
+reports them under ``components``. Other workloads (``--workload``) exist for
+profiling one kernel at a time: gemm, gemm_f32c, gemm_prepacked, linear,
+softmax, softmax_f32, rmsnorm, rmsnorm_f32, bmm, bmm_bf16, matmul_f32.
+
+Timing: W untimed steps, then K steps bracketed by ``torch.cuda.synchronize()``
+and HIP events recorded on the stream the kernels run on (torch's current
+stream, which the library launches on). ``roofline.achieved`` is the
+algorithmic work per launch of the dominant kernel over its average launch
+time; ``roofline.traffic`` is the HBM bytes per launch measured with
+rocprofv3 counters (``profiles/traffic.json``), or null when not measured.
+``cpu_baseline`` times the CPU oracle (``oracle/restate.py``, numpy) on the
+host cores on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+from pathlib import Path
+import platform
+import sys
+import time
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "helion-mlir-xsmm_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "bf16 GEMM TFLOP/s (4096³) + softmax/RMSNorm HBM GB/s, % of MI355X roofline"
+# MI355X published peaks: dense bf16 MFMA, dense f32 MFMA, HBM3E.
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_F32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def _blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+
+        counts = [info.get("num_threads", 1) for info in threadpool_info() if info.get("user_api") == "blas"]
+        if counts:
+            return int(max(counts))
+    except Exception:  # noqa: BLE001 - only for reporting
+        pass
+    return len(os.sched_getaffinity(0))
+
+
+class Workload:
+    """One benchmarked entry point: ``step()`` runs it once on resident inputs."""
+
+    name: str
+    description: str
+    unit: str  # "TFLOP/s" or "GB/s"
+    bound: str  # "mfma" or "hbm"
+    peak: float
+    work: float  # algorithmic flops or bytes per step
+    dtype: str
+    kernel: str  # the dominant kernel's name (rocprof)
+    launches_per_step: int = 1
+    config: dict
+
+    def step(self) -> object:
+        raise NotImplementedError
+
+    def cpu_baseline(self) -> dict:
+        raise NotImplementedError
+
+
+def _time_cpu(fn, work_per_call: float, budget_s: float = 10.0, max_reps: int = 50) -> tuple[float, int]:
+    """(throughput in work units per second, reps) of ``fn`` after one warm-up,
+    repeated until ``budget_s`` seconds of CPU work or ``max_reps``."""
+    fn()
+    reps, start = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        elapsed = time.perf_counter() - start
+        if elapsed >= budget_s or reps >= max_reps:
+            return work_per_call * reps / elapsed, reps
+
+
+class Gemm(Workload):
+    def __init__(self, device, out_dtype_name: str = "bf16", prepacked: bool = False) -> None:
+        import torch
+
+        import helion_mlir_utils as U
+        import hmx_workloads as W
+
+        cfg = W.config3()
+        self.cpu_a, self.cpu_b = cfg["a"], cfg["b"]
+        self.a, self.b = cfg["a"].to(device), cfg["b"].to(device)
+        self.out_dtype = torch.bfloat16 if out_dtype_name == "bf16" else torch.float32
+        self.U = U
+        self.prepacked = U.pack_b_blocked_vnni(self.b) if prepacked else None
+        m = n = k = 4096
+        self.name = "gemm_prepacked" if prepacked else ("gemm" if out_dtype_name == "bf16" else "gemm_f32c")
+        self.description = "bf16 GEMM 4096^3 (config 3)" + (", B pre-packed (pack_b_blocked_vnni)" if prepacked else "")
+        self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_BF16_TFLOPS
+        self.work = 2.0 * m * n * k
+        self.dtype = "bf16"
+        self.kernel = "gemm_bf16_kernel"
+        self.config = {"workload": self.description, "m": m, "n": n, "k": k, "a": "bf16 row-major",
+                       "b": "bf16 row-major" if not prepacked else "bf16 [N/32,K/32,16,32,2]",
+                       "c": out_dtype_name, "seed": 2, "values": "U[-1,1]"}
+
+    def step(self):
+        if self.prepacked is not None:
+            return self.U.matmul_prepacked_b(self.a, self.prepacked, 4096)
+        return self.U.matmul(self.a, self.b, out_dtype=self.out_dtype)
+
+    def cpu_baseline(self) -> dict:
+        from oracle import restate as R
+
+        a = self.cpu_a.float().numpy()
+        b = self.cpu_b.float().numpy()
+        rate, reps = _time_cpu(lambda: R.matmul(a, b, out="bf16"), self.work)
+        return {"value": rate / 1e12, "unit": "TFLOP/s", "cores": _blas_threads(), "kind": "port",
+                "sample": f"oracle.restate.matmul on the full 4096^3 problem (f32 accumulate, bf16 out), "
+                          f"{reps} reps, {_cpu_model()}"}
+
+
+class Linear(Workload):
+    def __init__(self, device) -> None:
+        import torch
+        import torch.nn.functional as F
+
+        import helion_mlir_utils as U
+        import hmx_workloads as W
+
+        cfg = W.config4()
+        self.cpu = cfg
+        x, w, b = (cfg[k].to(device) for k in ("x", "w", "b"))
+        layer = torch.nn.Linear(4096, 11008, device=device, dtype=torch.bfloat16)
+        with torch.no_grad():
+            layer.weight.copy_(w)
+            layer.bias.copy_(b)
+        self.x, self.layer, self.U, self.F = x, layer, U, F
+        self.cache = None
+        self.name = "linear"
+        self.description = "fused linear SiLU(X @ W^T + b), 8192 x 11008 x 4096 (config 4)"
+        self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_BF16_TFLOPS
+        self.work = 2.0 * 8192 * 11008 * 4096
+        self.dtype = "bf16"
+        self.kernel = "gemm_bf16_kernel"
+        self.config = {"workload": self.description, "m": 8192, "n": 11008, "k": 4096, "seed": 3}
+
+    def step(self):
+        import torch
+
+        with torch.no_grad():
+            y, self.cache = self.U.linear(self.x, self.layer, self.F.silu, cache=self.cache)
+        return y
+
+    def cpu_baseline(self) -> dict:
+        from oracle import restate as R
+
+        rows = 1024
+        x = self.cpu["x"][:rows].float().numpy()
+        w = self.cpu["w"].float().numpy()
+        b = self.cpu["b"].float().numpy()
+        work = 2.0 * rows * 11008 * 4096
+        rate, reps = _time_cpu(lambda: R.matmul(x, w, False, True, b, act="silu", out="bf16"), work)
+        return {"value": rate / 1e12, "unit": "TFLOP/s", "cores": _blas_threads(), "kind": "port",
+                "sample": f"oracle.restate.matmul on the first {rows} of 8192 rows, {reps} reps, {_cpu_model()}"}
+
+
+class RowOp(Workload):
+    def __init__(self, device, op: str, dtype_name: str) -> None:
+        import torch
+
+        import helion_mlir_utils as U
+        import hmx_workloads as W
+
+        dtype = torch.bfloat16 if dtype_name == "bf16" else torch.float32
+        cfg = W.config2(dtype)
+        self.cpu = cfg
+        self.x, self.w, self.eps = cfg["x"].to(device), cfg["weight"].to(device), cfg["eps"]
+        self.U, self.op = U, op
+        m, n = map(int, self.x.shape)
+        esz = self.x.element_size()
+        self.name = op + ("" if dtype_name == "bf16" else "_f32")
+        self.description = f"row {op} [{m}, {n}] {dtype_name} (config 2)"
+        self.unit, self.bound, self.peak = "GB/s", "hbm", PEAK_HBM_GBS
+        self.work = 2.0 * m * n * esz + (n * esz if op == "rmsnorm" else 0)  # one read + one write
+        self.dtype = dtype_name
+        self.kernel = "softmax_cached" if op == "softmax" else "rmsnorm_cached"
+        self.config = {"workload": self.description, "m": m, "n": n, "seed": 1, "values": "N(0, std 2)"}
+        if op == "rmsnorm":
+            self.config["eps"] = self.eps
+
+    def step(self):
+        if self.op == "softmax":
+            return self.U.softmax(self.x)
+        return self.U.rms_norm(self.x, self.w, self.eps)
+
+    def cpu_baseline(self) -> dict:
+        from oracle import restate as R
+
+        rows = 4096
+        x = self.cpu["x"][:rows].float().numpy()
+        w = self.cpu["weight"].float().numpy()
+        out = self.dtype
+        fn = (lambda: R.softmax(x, out)) if self.op == "softmax" else (lambda: R.rms_norm(x, w, self.eps, out))
+        work = self.work * rows / self.x.shape[0]
+        rate, reps = _time_cpu(fn, work)
+        return {"value": rate / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"oracle.restate.{self.op if self.op == 'softmax' else 'rms_norm'} on the first "
+                          f"{rows} of {self.x.shape[0]} rows, {reps} reps, {_cpu_model()}"}
+
+
+class Bmm(Workload):
+    def __init__(self, device, dtype_name: str) -> None:
+        import torch
+
+        import helion_mlir_utils as U
+        import hmx_workloads as W
+
+        dtype = torch.float32 if dtype_name == "f32" else torch.bfloat16
+        cfg = W.config5(dtype)
+        self.cpu = cfg
+        self.a, self.b = cfg["a"].to(device), cfg["b"].to(device)
+        self.U = U
+        self.plan = U.gemm_plan(dtype, 256, 256, 65536, batch=16)
+        self.name = "bmm" if dtype_name == "f32" else "bmm_bf16"
+        self.description = (f"split-K bmm [16,256,65536] @ [16,65536,256] {dtype_name}-in, f32 out, "
+                            f"S={self.plan['splits']} (config 5)")
+        if dtype_name == "f32":
+            self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_F32_TFLOPS
+            self.kernel = "gemm_f32_kernel"
+        else:
+            self.unit, self.bound, self.peak = "GB/s", "hbm", PEAK_HBM_GBS
+            self.kernel = "gemm_bf16_kernel"
+        self.flops = 2.0 * 16 * 256 * 256 * 65536
+        esz = 4 if dtype_name == "f32" else 2
+        self.bytes = 16 * (256 * 65536 * 2) * esz + 16 * 256 * 256 * 4
+        self.work = self.flops if self.unit == "TFLOP/s" else self.bytes
+        self.dtype = dtype_name
+        self.launches_per_step = 2  # the split GEMM and the fixed-order reduction
+        self.config = {"workload": self.description, "batch": 16, "m": 256, "n": 256, "k": 65536,
+                       "splits": self.plan["splits"], "seed": 4, "values": "U[-1,1]"}
+
+    def step(self):
+        import torch
+
+        return self.U.bmm(self.a, self.b, out_dtype=torch.float32)
+
+    def cpu_baseline(self) -> dict:
+        from oracle import restate as R
+
+        a = self.cpu["a"][:1].float().numpy()
+        b = self.cpu["b"][:1].float().numpy()
+        s = self.plan["splits"]
+        work = self.work / 16
+        rate, reps = _time_cpu(lambda: R.split_k_bmm(a, b, s), work, max_reps=20)
+        scale = 1e12 if self.unit == "TFLOP/s" else 1e9
+        return {"value": rate / scale, "unit": self.unit, "cores": _blas_threads(), "kind": "port",
+                "sample": f"oracle.restate.split_k_bmm of 1 of 16 batch slices, S={s}, {reps} reps, {_cpu_model()}"}
+
+
+class MatmulF32(Workload):
+    def __init__(self, device) -> None:
+        import helion_mlir_utils as U
+        import hmx_workloads as W
+
+        cfg = W.config1()
+        self.cpu = cfg
+        self.a, self.b = cfg["a"].to(device), cfg["b"].to(device)
+        self.U = U
+        self.name = "matmul_f32"
+        self.description = "f32 matmul 512^3 (config 1)"
+        self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_F32_TFLOPS
+        self.work = 2.0 * 512**3
+        self.dtype = "f32"
+        self.kernel = "gemm_f32_kernel"
+        self.config = {"workload": self.description, "m": 512, "n": 512, "k": 512, "seed": 0,
+                       "block_sizes": [64, 64, 64]}
+
+    def step(self):
+        return self.U.matmul(self.a, self.b, block_sizes=[64, 64, 64])
+
+    def cpu_baseline(self) -> dict:
+        from oracle import restate as R
+
+        a, b = self.cpu["a"].numpy(), self.cpu["b"].numpy()
+        rate, reps = _time_cpu(lambda: R.matmul(a, b), self.work, budget_s=5.0, max_reps=2000)
+        return {"value": rate / 1e12, "unit": "TFLOP/s", "cores": _blas_threads(), "kind": "port",
+                "sample": f"oracle.restate.matmul 512^3 f32, {reps} reps, {_cpu_model()}"}
+
+
+def make(name: str, device) -> Workload:
+    return {
+        "gemm": lambda: Gemm(device),
+        "gemm_f32c": lambda: Gemm(device, "f32"),
+        "gemm_prepacked": lambda: Gemm(device, prepacked=True),
+        "linear": lambda: Linear(device),
+        "softmax": lambda: RowOp(device, "softmax", "bf16"),
+        "softmax_f32": lambda: RowOp(device, "softmax", "f32"),
+        "rmsnorm": lambda: RowOp(device, "rmsnorm", "bf16"),
+        "rmsnorm_f32": lambda: RowOp(device, "rmsnorm", "f32"),
+        "bmm": lambda: Bmm(device, "f32"),
+        "bmm_bf16": lambda: Bmm(device, "bf16"),
+        "matmul_f32": lambda: MatmulF32(device),
+    }[name]()
+
+
+def measure(w: Workload, steps: int, warmup: int) -> dict:
+    """Step time (ms) over ``steps`` timed steps with HIP events."""
+    import torch
+
+    for _ in range(warmup):
+        w.step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        w.step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    scale = 1e12 if w.unit == "TFLOP/s" else 1e9
+    value = w.work / (ms * 1e-3) / scale
+    return {"ms": ms, "value": value, "frac": value / w.peak}
+
+
+def traffic_of(name: str) -> float | None:
+    """HBM bytes per launch of the workload's dominant kernel, from the
+    rocprofv3 FETCH_SIZE/WRITE_SIZE runs recorded in profiles/traffic.json."""
+    path = ROOT / "profiles" / "traffic.json"
+    try:
+        entry = json.loads(path.read_text()).get(name)
+    except (OSError, ValueError):
+        return None
+    if not entry or entry.get("bytes_per_launch") is None:
+        return None
+    return float(entry["bytes_per_launch"])
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--workload", default="gemm")
+    parser.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
+    parser.add_argument("--no-components", action="store_true", help="skip the softmax/RMSNorm lines")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (every box here has one GPU; "
+              "the sharded design is described in DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    device = torch.device("cuda", 0)
+    print(f"bench: workload={args.workload} steps={args.steps} warmup={args.warmup}", file=sys.stderr, flush=True)
+    w = make(args.workload, device)
+    result = measure(w, args.steps, args.warmup)
+    print(f"bench: {w.name} {result['ms']:.4f} ms/step {result['value']:.1f} {w.unit}", file=sys.stderr, flush=True)
+
+    per_launch_ms = result["ms"]  # one dominant launch per step (bmm: includes its reduction launch)
+    achieved = w.work / (per_launch_ms * 1e-3) / (1e12 if w.unit == "TFLOP/s" else 1e9)
+    roofline = {
+        "bound": w.bound,
+        "achieved": round(achieved, 2),
+        "peak": w.peak,
+        "unit": w.unit,
+        "frac": round(achieved / w.peak, 4),
+        "traffic": traffic_of(w.name),
+        "kernel": w.kernel,
+        "launch_ms": round(per_launch_ms, 5),
+    }
+    line = {
+        "metric": METRIC,
+        "value": round(result["value"], 2),
+        "unit": w.unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(result["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": w.dtype,
+        "data": "synthetic (seeded, BASELINE config distributions)",
+        "config": w.config,
+        "roofline": roofline,
+    }
+    if args.workload == "gemm" and not args.no_components:
+        components = {}
+        for name in ("softmax", "rmsnorm"):
+            cw = make(name, device)
+            r = measure(cw, args.steps, args.warmup)
+            components[name + "_bf16"] = {
+                "value": round(r["value"], 1), "unit": "GB/s", "frac": round(r["frac"], 4),
+                "ms_per_step": round(r["ms"], 5), "traffic": traffic_of(cw.name), "config": cw.config,
+            }
+            print(f"bench: {name} {r['ms']:.4f} ms/step {r['value']:.1f} GB/s", file=sys.stderr, flush=True)
+            del cw
+        line["components"] = components
+    if not args.no_cpu_baseline:
+        print("bench: timing the CPU oracle baseline", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = w.cpu_baseline()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,866 @@
+// GEMM kernels for gfx950: bf16 x bf16 -> f32 on v_mfma_f32_32x32x16_bf16 and
+// f32 x f32 -> f32 on v_mfma_f32_32x32x2_f32, with the epilogue
+// act(((A @ B) + bias) * scale + shift) fused before the single rounding to C,
+// batch slices on grid z and deterministic split-K on grid y.
+//
+// bf16 kernel. A workgroup of 4 waves (2 x 2) owns a BM x BN output tile;
+// each wave owns a (BM/2) x (BN/2) block of 32 x 32 MFMA fragments. Both
+// operand tiles live in LDS K-contiguous (`[rows][BK + 8]` bf16, the 8-element
+// pad makes the 16-byte fragment reads conflict-free), double-buffered: the
+// next K tile's global loads are issued into registers before the MFMAs of
+// the current one and written to the other LDS buffer after them, so one
+// barrier per K tile suffices. Operands that are not K-contiguous in HBM
+// (row-major B, transposed A, panel layouts) are transposed in registers on
+// the way (8 x 8 bf16 blocks through v_perm_b32); VNNI-pair layouts regroup
+// their K pairs with no data movement at all.
+//
+// f32 kernel. Same structure with BK = 32 and the f32 MFMA, whose operands
+// are one value per lane: LDS keeps each operand in its HBM orientation and
+// fragments are gathered with 4-byte (or 16-byte, when K-contiguous) reads.
+#include <type_traits>
+
+#include "hmx_device.hpp"
+
+namespace hmx {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// Operand layouts (A: rows are M, B: rows are N; both indexed (row, k)).
+enum : int {
+  L_KCONTIG = 0,      // row * ld + k
+  L_RCONTIG = 1,      // k * ld + row
+  L_VNNI_PANELS = 2,  // [R/P, Kp/2, P, 2]
+  L_BLOCKED_VNNI = 3, // [R/32, Kp/32, 16, 32, 2]
+  L_PANELS = 4,       // [R/P, Kp, P]
+  L_BLOCKED = 5,      // [R/32, Kp/32, 32, 32]
+};
+
+// How a layout's 16-byte vectors run: along K, along rows, or 4 rows x 2 K.
+template <int L>
+constexpr int vec_kind() {
+  return L == L_KCONTIG ? 0 : (L == L_VNNI_PANELS || L == L_BLOCKED_VNNI) ? 2 : 1;
+}
+
+struct Operand {
+  const void* p;   // this batch slice
+  int64_t ld;      // line stride (row-major layouts)
+  int64_t rows;    // logical extent along rows (M or N)
+  int64_t panel;   // panel width (panel layouts)
+  int64_t kpad;    // padded K (packed layouts)
+  bool vec;        // 16-byte loads allowed (alignment of base and lines)
+};
+
+template <int L>
+__device__ __forceinline__ int64_t offset_of(const Operand& o, int64_t r, int64_t k) {
+  if constexpr (L == L_KCONTIG) return r * o.ld + k;
+  if constexpr (L == L_RCONTIG) return k * o.ld + r;
+  if constexpr (L == L_VNNI_PANELS)
+    return (((r / o.panel) * (o.kpad >> 1) + (k >> 1)) * o.panel + (r % o.panel)) * 2 + (k & 1);
+  if constexpr (L == L_BLOCKED_VNNI)
+    return ((((r >> 5) * (o.kpad >> 5) + (k >> 5)) * 16 + ((k & 31) >> 1)) * 32 + (r & 31)) * 2 +
+           (k & 1);
+  if constexpr (L == L_PANELS) return ((r / o.panel) * o.kpad + k) * o.panel + (r % o.panel);
+  if constexpr (L == L_BLOCKED)
+    return (((r >> 5) * (o.kpad >> 5) + (k >> 5)) * 32 + (k & 31)) * 32 + (r & 31);
+  return 0;
+}
+
+__device__ __forceinline__ uint32_t lo_pair(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x05040100u);  // {x.lo16, y.lo16}
+}
+__device__ __forceinline__ uint32_t hi_pair(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x07060302u);  // {x.hi16, y.hi16}
+}
+__device__ __forceinline__ uint32_t dw(const uint4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// ---------------------------------------------------------------------------
+// bf16 operand tile loader: global (layout L) -> registers -> LDS [BR][BK+8].
+template <int BR, int BK, int NT, int L, bool GUARD>
+struct Bf16Loader {
+  static constexpr int KIND = vec_kind<L>();
+  static constexpr int PITCH = BK + 8;
+  // KIND 0: one 16-byte vector (8 K) per item; KIND 1: an 8-row x 8-K block;
+  // KIND 2: a 4-row x 8-K block.
+  static constexpr int ITEMS = KIND == 0 ? BR * BK / 8 : KIND == 1 ? BR * BK / 64 : BR * BK / 32;
+  static constexpr int PER_THREAD = (ITEMS + NT - 1) / NT;
+  static constexpr int REGS = KIND == 0 ? 1 : KIND == 1 ? 8 : 4;
+  static_assert(ITEMS % NT == 0 || ITEMS < NT, "tile not divisible among threads");
+  uint4 r[PER_THREAD][REGS];
+
+  // Scalar fallback: 8 consecutive elements starting at (row, k) stepping
+  // along `dr`/`dk`, zero outside [0, rows) x [0, k_end).
+  __device__ __forceinline__ static uint4 gather8(const Operand& o, int64_t row, int64_t k,
+                                                  int dr, int dk, int64_t k_end) {
+    const uint16_t* p = (const uint16_t*)o.p;
+    uint32_t h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t rr = row + e * dr, kk = k + e * dk;
+      h[e] = (rr < o.rows && kk < k_end) ? p[offset_of<L>(o, rr, kk)] : 0u;
+    }
+    return make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                      h[6] | (h[7] << 16));
+  }
+
+  __device__ __forceinline__ void load(const Operand& o, int64_t r0, int64_t k0, int64_t k_end,
+                                       int tid) {
+    const uint16_t* p = (const uint16_t*)o.p;
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int item = i * NT + tid;
+      if (ITEMS < NT && item >= ITEMS) break;
+      if constexpr (KIND == 0) {
+        const int64_t row = r0 + item / (BK / 8);
+        const int64_t k = k0 + (item % (BK / 8)) * 8;
+        if (!GUARD || (o.vec && row < o.rows && k + 8 <= k_end))
+          r[i][0] = *(const uint4*)(p + offset_of<L>(o, row, k));
+        else
+          r[i][0] = gather8(o, row, k, 0, 1, k_end);
+      } else if constexpr (KIND == 1) {
+        const int64_t k = k0 + (item % (BK / 8)) * 8;
+        const int64_t row = r0 + (item / (BK / 8)) * 8;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          if (!GUARD || (o.vec && row + 8 <= o.rows && k + kk < k_end))
+            r[i][kk] = *(const uint4*)(p + offset_of<L>(o, row, k + kk));
+          else
+            r[i][kk] = gather8(o, row, k + kk, 1, 0, k_end);
+        }
+      } else {
+        const int64_t k = k0 + (item % (BK / 8)) * 8;
+        const int64_t row = r0 + (item / (BK / 8)) * 4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (!GUARD || (o.vec && row + 4 <= o.rows && k + 2 * q + 2 <= k_end)) {
+            r[i][q] = *(const uint4*)(p + offset_of<L>(o, row, k + 2 * q));
+          } else {
+            uint32_t w[4];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              const int64_t rr = row + d, kk = k + 2 * q;
+              const uint32_t lo = (rr < o.rows && kk < k_end) ? p[offset_of<L>(o, rr, kk)] : 0u;
+              const uint32_t hi =
+                  (rr < o.rows && kk + 1 < k_end) ? p[offset_of<L>(o, rr, kk + 1)] : 0u;
+              w[d] = lo | (hi << 16);
+            }
+            r[i][q] = make_uint4(w[0], w[1], w[2], w[3]);
+          }
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(uint16_t* lds, int tid) const {
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int item = i * NT + tid;
+      if (ITEMS < NT && item >= ITEMS) break;
+      const int kcol = (item % (BK / 8)) * 8;
+      if constexpr (KIND == 0) {
+        const int row = item / (BK / 8);
+        *(uint4*)(lds + row * PITCH + kcol) = r[i][0];
+      } else if constexpr (KIND == 1) {
+        const int row = (item / (BK / 8)) * 8;
+        // 8 x 8 transpose: output row j holds K pairs (2d, 2d+1) of column j.
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          uint4 o;
+          if (j & 1) {
+            o.x = hi_pair(dw(r[i][0], j >> 1), dw(r[i][1], j >> 1));
+            o.y = hi_pair(dw(r[i][2], j >> 1), dw(r[i][3], j >> 1));
+            o.z = hi_pair(dw(r[i][4], j >> 1), dw(r[i][5], j >> 1));
+            o.w = hi_pair(dw(r[i][6], j >> 1), dw(r[i][7], j >> 1));
+          } else {
+            o.x = lo_pair(dw(r[i][0], j >> 1), dw(r[i][1], j >> 1));
+            o.y = lo_pair(dw(r[i][2], j >> 1), dw(r[i][3], j >> 1));
+            o.z = lo_pair(dw(r[i][4], j >> 1), dw(r[i][5], j >> 1));
+            o.w = lo_pair(dw(r[i][6], j >> 1), dw(r[i][7], j >> 1));
+          }
+          *(uint4*)(lds + (row + j) * PITCH + kcol) = o;
+        }
+      } else {
+        const int row = (item / (BK / 8)) * 4;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint4 o = make_uint4(dw(r[i][0], d), dw(r[i][1], d), dw(r[i][2], d), dw(r[i][3], d));
+          *(uint4*)(lds + (row + d) * PITCH + kcol) = o;
+        }
+      }
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+struct GemmArgs {
+  Operand a, b;
+  int64_t stride_a, stride_b;  // batch strides (elements)
+  void* c;
+  int64_t ldc, stride_c, stride_split;
+  int c_dtype;
+  int64_t m, n, k, k_chunk;
+  const void* bias;
+  const void* scale;
+  const void* shift;
+  int vec_dtype;
+  int act;
+  float act_arg;
+  int tiles_m, tiles_n;
+};
+
+// blockIdx.x -> (tile_m, tile_n). Consecutive workgroups are dealt to the 8
+// XCDs in turn; renumbering them so that each XCD gets one contiguous range,
+// then walking that range in groups of kGroupM tile rows, makes the tiles
+// that share A rows and B columns run on the same XCD and its L2.
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+  constexpr int kXcds = 8, kGroupM = 4;
+  const int nb = tiles_m * tiles_n;
+  int bid = blockIdx.x;
+  if (nb % kXcds == 0) bid = (bid % kXcds) * (nb / kXcds) + bid / kXcds;
+  const int per_group = kGroupM * tiles_n;
+  const int group = bid / per_group;
+  const int first_m = group * kGroupM;
+  const int gm = min(kGroupM, tiles_m - first_m);
+  const int in_group = bid % per_group;
+  tm = first_m + in_group % gm;
+  tn = in_group / gm;
+}
+
+__device__ __forceinline__ void column_vectors(const GemmArgs& g, int64_t col, bool in,
+                                               float& bias, float& scale, float& shift) {
+  bias = (g.bias && in) ? load_any(g.bias, g.vec_dtype, col) : 0.f;
+  scale = (g.scale && in) ? load_any(g.scale, g.vec_dtype, col) : 1.f;
+  shift = (g.shift && in) ? load_any(g.shift, g.vec_dtype, col) : 0.f;
+}
+
+
+// Epilogue, staged through LDS (free once the K loop is done). Each wave owns
+// a region of 32 x (WN + 8) f32; for each of its FM fragment rows it writes
+// the accumulators there (element e of lane l of a 32 x 32 fragment is row
+// 8*(e/4) + 4*(l/32) + e%4, column l % 32), then reads them back four
+// columns per lane to apply bias, scale, shift and the activation and store
+// C with 8- or 16-byte coalesced writes.
+template <int WN>
+constexpr int epi_pitch() { return WN + 8; }
+
+template <int FM, int FN, int WM, int WN, bool GUARD>
+__device__ __forceinline__ void epilogue(const GemmArgs& g, float* lds, int split, int batch,
+                                         int64_t m0, int64_t n0, int wm, int wn, int wave,
+                                         int lane, const f32x16_t (&acc)[FM][FN]) {
+  constexpr int P = epi_pitch<WN>();
+  float* ep = lds + wave * 32 * P;
+  const int64_t off = split * g.stride_split + batch * g.stride_c;
+  const bool bf16 = g.c_dtype == HMX_DTYPE_BF16;
+  const bool vec_ok = (g.ldc % 4 == 0) &&
+                      ((((uintptr_t)g.c) & (bf16 ? 7 : 15)) == 0) && (off % 4 == 0);
+  const int64_t col0 = n0 + wn * WN;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        ep[(8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * P + j * 32 + (lane & 31)] = acc[i][j][e];
+    __syncthreads();
+    const int64_t row0 = m0 + wm * WM + i * 32;
+    for (int idx = lane; idx < 32 * (WN / 4); idx += 64) {
+      const int r = idx / (WN / 4), cq = (idx % (WN / 4)) * 4;
+      const int64_t row = row0 + r, col = col0 + cq;
+      if (GUARD && row >= g.m) continue;
+      const float4 q = *(const float4*)(ep + r * P + cq);
+      float v[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const bool in = !GUARD || col + t < g.n;
+        float bias, scale, shift;
+        column_vectors(g, col + t, in, bias, scale, shift);
+        v[t] = apply_activation(g.act, (v[t] + bias) * scale + shift, g.act_arg);
+      }
+      const int64_t o = off + row * g.ldc + col;
+      if ((!GUARD || col + 4 <= g.n) && vec_ok) {
+        if (bf16)
+          *(uint2*)((uint16_t*)g.c + o) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        else
+          *(float4*)((float*)g.c + o) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if (GUARD && col + t >= g.n) break;
+          if (bf16)
+            ((uint16_t*)g.c)[o + t] = (uint16_t)f32_to_bf16_bits(v[t]);
+          else
+            ((float*)g.c)[o + t] = v[t];
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int BM_, int BN_, int BK_>
+struct Bf16Cfg {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_;
+  static constexpr int NT = 256;           // 4 waves, 2 x 2
+  static constexpr int WM = BM / 2, WN = BN / 2;
+  static constexpr int FM = WM / 32, FN = WN / 32;
+  static constexpr int PITCH = BK + 8;
+  static constexpr int LDS_ELEMS = 2 * (BM + BN) * PITCH;
+};
+
+template <class Cfg, int LA, int LB, bool GUARD>
+__global__ __launch_bounds__(Cfg::NT, 1) void gemm_bf16_kernel(GemmArgs g) {
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, NT = Cfg::NT, PITCH = Cfg::PITCH;
+  constexpr int FM = Cfg::FM, FN = Cfg::FN;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[Cfg::LDS_ELEMS];
+  // Stage s holds A at lds + s * STAGE and B right after it.
+  constexpr int STAGE = (BM + BN) * PITCH;
+
+  int tm, tn;
+  tile_coords(g.tiles_m, g.tiles_n, tm, tn);
+  const int split = blockIdx.y, batch = blockIdx.z;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t k_begin = (int64_t)split * g.k_chunk;
+  const int64_t k_end = min(g.k, k_begin + g.k_chunk);
+
+  Operand a = g.a, b = g.b;
+  a.p = (const uint16_t*)a.p + batch * g.stride_a;
+  b.p = (const uint16_t*)b.p + batch * g.stride_b;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  Bf16Loader<BM, BK, NT, LA, GUARD> la;
+  Bf16Loader<BN, BK, NT, LB, GUARD> lb;
+
+  f32x16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int ktiles = (int)((k_end - k_begin + BK - 1) / BK);
+  if (ktiles > 0) {
+    la.load(a, m0, k_begin, k_end, tid);
+    lb.load(b, n0, k_begin, k_end, tid);
+    la.store(lds, tid);
+    lb.store(lds + BM * PITCH, tid);
+  }
+  __syncthreads();
+
+  // Fragment read offsets: row lane % 32 of the fragment, K half lane / 32.
+  const int frag_row = lane & 31, frag_k = (lane >> 5) * 8;
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int cur = kt & 1;
+    // Prefetch the next K tile (the last iteration re-reads its own, in
+    // bounds): unconditional, so the staging registers stay registers.
+    const int64_t kn = k_begin + (int64_t)min(kt + 1, ktiles - 1) * BK;
+    la.load(a, m0, kn, k_end, tid);
+    lb.load(b, n0, kn, k_end, tid);
+    const uint16_t* As = lds + cur * STAGE + (wm * Cfg::WM + frag_row) * PITCH + frag_k;
+    const uint16_t* Bs = lds + cur * STAGE + BM * PITCH + (wn * Cfg::WN + frag_row) * PITCH + frag_k;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      bf16x8_t af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[i] = *(const bf16x8_t*)(As + i * 32 * PITCH + ks * 16);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bfr[j] = *(const bf16x8_t*)(Bs + j * 32 * PITCH + ks * 16);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+    la.store(lds + (cur ^ 1) * STAGE, tid);
+    lb.store(lds + (cur ^ 1) * STAGE + BM * PITCH, tid);
+    __syncthreads();
+  }
+
+  static_assert(4 * 32 * epi_pitch<Cfg::WN>() * 4 <= Cfg::LDS_ELEMS * 2, "epilogue does not fit LDS");
+  epilogue<FM, FN, Cfg::WM, Cfg::WN, GUARD>(g, (float*)lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
+}
+
+// ---------------------------------------------------------------------------
+// f32 kernel.
+template <int BM_, int BN_, int BK_>
+struct F32Cfg {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_;
+  static constexpr int NT = 256;
+  static constexpr int WM = BM / 2, WN = BN / 2;
+  static constexpr int FM = WM / 32, FN = WN / 32;
+};
+
+// LDS image of an f32 operand tile in its HBM orientation: K-contiguous
+// `[BR][BK + 4]` or row-contiguous `[BK][BR + 8]` (pads against bank
+// conflicts of the fragment reads).
+template <int BR, int BK, int NT, int L, bool GUARD>
+struct F32Loader {
+  static constexpr bool KC = L == L_KCONTIG;
+  static constexpr int PITCH = KC ? BK + 4 : BR + 8;
+  static constexpr int ELEMS = KC ? BR * PITCH : BK * PITCH;
+  static constexpr int ITEMS = BR * BK / 4;
+  static constexpr int PER_THREAD = ITEMS / NT;
+  static_assert(ITEMS % NT == 0, "tile not divisible among threads");
+  uint4 r[PER_THREAD];
+
+  __device__ __forceinline__ void load(const Operand& o, int64_t r0, int64_t k0, int64_t k_end,
+                                       int tid) {
+    const float* p = (const float*)o.p;
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int item = i * NT + tid;
+      int64_t row, k;
+      if constexpr (KC) {
+        row = r0 + item / (BK / 4);
+        k = k0 + (item % (BK / 4)) * 4;
+      } else {
+        k = k0 + item / (BR / 4);
+        row = r0 + (item % (BR / 4)) * 4;
+      }
+      const bool fits = KC ? (row < o.rows && k + 4 <= k_end) : (row + 4 <= o.rows && k < k_end);
+      if (!GUARD || (o.vec && fits)) {
+        r[i] = *(const uint4*)(p + offset_of<L>(o, row, k));
+      } else {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t rr = KC ? row : row + e, kk = KC ? k + e : k;
+          v[e] = (rr < o.rows && kk < k_end) ? p[offset_of<L>(o, rr, kk)] : 0.f;
+        }
+        r[i] = Elem<float>::pack(v);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float* lds, int tid) const {
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int item = i * NT + tid;
+      if constexpr (KC)
+        *(uint4*)(lds + (item / (BK / 4)) * PITCH + (item % (BK / 4)) * 4) = r[i];
+      else
+        *(uint4*)(lds + (item / (BR / 4)) * PITCH + (item % (BR / 4)) * 4) = r[i];
+    }
+  }
+
+  // The 4 values lane group g feeds MFMAs s = 0..3 of K step k8: K index
+  // k8 + 4g + s, row `row` of the tile.
+  __device__ __forceinline__ static void frag(const float* lds, int row, int k, float (&v)[4]) {
+    if constexpr (KC) {
+      const float4 q = *(const float4*)(lds + row * PITCH + k);
+      v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) v[s] = lds[(k + s) * PITCH + row];
+    }
+  }
+};
+
+template <class Cfg, int LAY_A, int LAY_B, bool GUARD>
+__global__ __launch_bounds__(Cfg::NT, 1) void gemm_f32_kernel(GemmArgs g) {
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, NT = Cfg::NT;
+  constexpr int FM = Cfg::FM, FN = Cfg::FN;
+  using LA = F32Loader<BM, BK, NT, LAY_A, GUARD>;
+  using LB = F32Loader<BN, BK, NT, LAY_B, GUARD>;
+  __shared__ __attribute__((aligned(16))) float lds[2 * (LA::ELEMS + LB::ELEMS)];
+  constexpr int STAGE = LA::ELEMS + LB::ELEMS;
+
+  int tm, tn;
+  tile_coords(g.tiles_m, g.tiles_n, tm, tn);
+  const int split = blockIdx.y, batch = blockIdx.z;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t k_begin = (int64_t)split * g.k_chunk;
+  const int64_t k_end = min(g.k, k_begin + g.k_chunk);
+
+  Operand a = g.a, b = g.b;
+  a.p = (const float*)a.p + batch * g.stride_a;
+  b.p = (const float*)b.p + batch * g.stride_b;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  LA la;
+  LB lb;
+  f32x16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int ktiles = (int)((k_end - k_begin + BK - 1) / BK);
+  if (ktiles > 0) {
+    la.load(a, m0, k_begin, k_end, tid);
+    lb.load(b, n0, k_begin, k_end, tid);
+    la.store(lds, tid);
+    lb.store(lds + LA::ELEMS, tid);
+  }
+  __syncthreads();
+
+  const int frag_row = lane & 31, frag_k = (lane >> 5) * 4;
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int cur = kt & 1;
+    // Prefetch the next K tile (the last iteration re-reads its own, in
+    // bounds): unconditional, so the staging registers stay registers.
+    const int64_t kn = k_begin + (int64_t)min(kt + 1, ktiles - 1) * BK;
+    la.load(a, m0, kn, k_end, tid);
+    lb.load(b, n0, kn, k_end, tid);
+#pragma unroll
+    for (int k8 = 0; k8 < BK; k8 += 8) {
+      float av[FM][4], bv[FN][4];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) LA::frag(lds + cur * STAGE, wm * Cfg::WM + i * 32 + frag_row, k8 + frag_k, av[i]);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) LB::frag(lds + cur * STAGE + LA::ELEMS, wn * Cfg::WN + j * 32 + frag_row, k8 + frag_k, bv[j]);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][s], bv[j][s], acc[i][j], 0, 0, 0);
+    }
+    la.store(lds + (cur ^ 1) * STAGE, tid);
+    lb.store(lds + (cur ^ 1) * STAGE + LA::ELEMS, tid);
+    __syncthreads();
+  }
+
+  static_assert(4 * 32 * epi_pitch<Cfg::WN>() <= 2 * STAGE, "epilogue does not fit LDS");
+  epilogue<FM, FN, Cfg::WM, Cfg::WN, GUARD>(g, lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Split-K reduction: out[b, i, j] = epilogue(sum_s ws[s, b, i, j]) with s in
+// increasing order, so the result never depends on scheduling.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws,
+                                                            int splits, int64_t batch,
+                                                            GemmArgs g) {
+  const int64_t mn = g.m * g.n;
+  const int64_t total = batch * mn;
+  const int64_t split_stride = batch * mn;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    float s = 0.f;
+    for (int sp = 0; sp < splits; ++sp) s += ws[sp * split_stride + idx];
+    const int64_t b = idx / mn, rem = idx % mn;
+    const int64_t row = rem / g.n, col = rem % g.n;
+    float bias, scale, shift;
+    column_vectors(g, col, true, bias, scale, shift);
+    const float v = apply_activation(g.act, (s + bias) * scale + shift, g.act_arg);
+    const int64_t off = b * g.stride_c + row * g.ldc + col;
+    if (g.c_dtype == HMX_DTYPE_BF16)
+      ((uint16_t*)g.c)[off] = (uint16_t)f32_to_bf16_bits(v);
+    else
+      ((float*)g.c)[off] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side: tile table, planning, dispatch.
+
+struct TileChoice {
+  int bm, bn, bk;
+};
+
+// Instantiated workgroup tiles, largest first.
+constexpr TileChoice kBf16Tiles[] = {{256, 256, 64}, {128, 128, 64}};
+constexpr TileChoice kF32Tiles[] = {{128, 128, 32}};
+constexpr int kCus = 256;  // MI355X compute units
+
+int layout_code(int b_layout) {
+  switch (b_layout) {
+    case HMX_B_ROW: return L_RCONTIG;
+    case HMX_B_TRANS: return L_KCONTIG;
+    case HMX_B_VNNI_PANELS: return L_VNNI_PANELS;
+    case HMX_B_BLOCKED_VNNI: return L_BLOCKED_VNNI;
+    case HMX_B_PANELS: return L_PANELS;
+    case HMX_B_BLOCKED: return L_BLOCKED;
+  }
+  return -1;
+}
+
+struct Plan {
+  TileChoice tile;
+  int splits;
+  int64_t k_chunk;
+  int64_t workspace_bytes;
+};
+
+int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int b_layout,
+              int splits, int64_t max_ws, int tile_m, int tile_n, int tile_k, Plan& plan) {
+  const bool bf16 = ab_dtype == HMX_DTYPE_BF16;
+  const TileChoice* table = bf16 ? kBf16Tiles : kF32Tiles;
+  const int count = bf16 ? (int)(sizeof(kBf16Tiles) / sizeof(TileChoice))
+                         : (int)(sizeof(kF32Tiles) / sizeof(TileChoice));
+  // Packed B layouts are instantiated for the first tile only.
+  const bool packed = b_layout != HMX_B_ROW && b_layout != HMX_B_TRANS;
+  int pick = -1;
+  if (tile_m > 0 || tile_n > 0 || tile_k > 0) {
+    for (int i = 0; i < count && pick < 0; ++i) {
+      if ((tile_m <= 0 || table[i].bm <= tile_m) && (tile_n <= 0 || table[i].bn <= tile_n) &&
+          (tile_k <= 0 || table[i].bk <= tile_k))
+        pick = i;
+    }
+    if (pick < 0) pick = count - 1;
+  } else {
+    // The largest tile that still gives every CU a workgroup; else the smallest.
+    pick = count - 1;
+    for (int i = 0; i < count; ++i) {
+      const int64_t tiles = ceil_div(m, table[i].bm) * ceil_div(n, table[i].bn) * batch;
+      if (tiles >= kCus) { pick = i; break; }
+    }
+  }
+  if (packed && bf16) pick = 0;
+  plan.tile = table[pick];
+  const int64_t tiles = ceil_div(m, plan.tile.bm) * ceil_div(n, plan.tile.bn) * batch;
+  const int64_t kt = ceil_div(k, plan.tile.bk);
+  if (splits == 0) {
+    // Split K while the grid holds fewer than 4 workgroups per CU, each chunk
+    // keeps at least 8 K tiles, and the partials (written and read again as
+    // f32) stay within a quarter of the operand traffic.
+    splits = 1;
+    const int64_t operand_bytes = batch * (m + n) * k * (bf16 ? 2 : 4);
+    for (;;) {
+      const int s2 = splits * 2;
+      if (tiles * splits >= 4 * kCus || kt / s2 < 8) break;
+      const int64_t need = (int64_t)s2 * batch * m * n * 4;
+      if ((max_ws >= 0 && need > max_ws) || 2 * need > operand_bytes / 4) break;
+      splits = s2;
+    }
+  }
+  if (splits < 1) splits = 1;
+  if (splits > 1) {
+    // Whole K tiles per chunk; no empty chunks.
+    plan.k_chunk = ceil_div(kt, splits) * plan.tile.bk;
+    splits = (int)ceil_div(k, plan.k_chunk);
+  } else {
+    plan.k_chunk = k;
+  }
+  plan.splits = splits;
+  plan.workspace_bytes = splits > 1 ? (int64_t)splits * batch * m * n * 4 : 0;
+  return HMX_OK;
+}
+
+template <int V>
+using IntC = std::integral_constant<int, V>;
+
+template <class Cfg, int LA, int LB>
+void launch_bf16(const GemmArgs& g, bool guard, dim3 grid, hipStream_t s) {
+  if (guard)
+    gemm_bf16_kernel<Cfg, LA, LB, true><<<grid, Cfg::NT, 0, s>>>(g);
+  else
+    gemm_bf16_kernel<Cfg, LA, LB, false><<<grid, Cfg::NT, 0, s>>>(g);
+}
+
+template <class Cfg>
+void dispatch_bf16(const GemmArgs& g, int la, int lb, bool guard, dim3 grid, hipStream_t s) {
+  if (la == L_KCONTIG) {
+    switch (lb) {
+      case L_KCONTIG: launch_bf16<Cfg, L_KCONTIG, L_KCONTIG>(g, guard, grid, s); break;
+      case L_RCONTIG: launch_bf16<Cfg, L_KCONTIG, L_RCONTIG>(g, guard, grid, s); break;
+      default:
+        if constexpr (Cfg::BM == kBf16Tiles[0].bm && Cfg::BN == kBf16Tiles[0].bn) {
+          switch (lb) {
+            case L_VNNI_PANELS: launch_bf16<Cfg, L_KCONTIG, L_VNNI_PANELS>(g, guard, grid, s); break;
+            case L_BLOCKED_VNNI: launch_bf16<Cfg, L_KCONTIG, L_BLOCKED_VNNI>(g, guard, grid, s); break;
+            case L_PANELS: launch_bf16<Cfg, L_KCONTIG, L_PANELS>(g, guard, grid, s); break;
+            case L_BLOCKED: launch_bf16<Cfg, L_KCONTIG, L_BLOCKED>(g, guard, grid, s); break;
+          }
+        }
+    }
+  } else {
+    if (lb == L_KCONTIG)
+      launch_bf16<Cfg, L_RCONTIG, L_KCONTIG>(g, guard, grid, s);
+    else
+      launch_bf16<Cfg, L_RCONTIG, L_RCONTIG>(g, guard, grid, s);
+  }
+}
+
+template <class Cfg, int LA, int LB>
+void launch_f32(const GemmArgs& g, bool guard, dim3 grid, hipStream_t s) {
+  if (guard)
+    gemm_f32_kernel<Cfg, LA, LB, true><<<grid, Cfg::NT, 0, s>>>(g);
+  else
+    gemm_f32_kernel<Cfg, LA, LB, false><<<grid, Cfg::NT, 0, s>>>(g);
+}
+
+template <class Cfg>
+void dispatch_f32(const GemmArgs& g, int la, int lb, bool guard, dim3 grid, hipStream_t s) {
+  if (la == L_KCONTIG) {
+    switch (lb) {
+      case L_KCONTIG: launch_f32<Cfg, L_KCONTIG, L_KCONTIG>(g, guard, grid, s); break;
+      case L_RCONTIG: launch_f32<Cfg, L_KCONTIG, L_RCONTIG>(g, guard, grid, s); break;
+      case L_BLOCKED: launch_f32<Cfg, L_KCONTIG, L_BLOCKED>(g, guard, grid, s); break;
+      case L_PANELS: launch_f32<Cfg, L_KCONTIG, L_PANELS>(g, guard, grid, s); break;
+    }
+  } else {
+    if (lb == L_KCONTIG)
+      launch_f32<Cfg, L_RCONTIG, L_KCONTIG>(g, guard, grid, s);
+    else
+      launch_f32<Cfg, L_RCONTIG, L_RCONTIG>(g, guard, grid, s);
+  }
+}
+
+}  // namespace
+}  // namespace hmx
+
+using namespace hmx;
+
+extern "C" {
+
+int hmx_gemm_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int trans_a,
+                  int b_layout, int splits, int64_t max_workspace_bytes, int tile_m,
+                  int tile_n, int tile_k, int* out_splits, int* out_tile_m, int* out_tile_n,
+                  int* out_tile_k, int64_t* out_workspace_bytes) {
+  (void)trans_a;
+  HMX_REQUIRE(valid_dtype(ab_dtype), "gemm_plan: unknown dtype %d", ab_dtype);
+  HMX_REQUIRE(layout_code(b_layout) >= 0, "gemm_plan: unknown B layout %d", b_layout);
+  HMX_REQUIRE(m >= 0 && n >= 0 && k >= 0 && batch >= 1, "gemm_plan: invalid shape");
+  HMX_REQUIRE(splits >= 0, "gemm_plan: negative splits");
+  Plan plan;
+  int st = make_plan(ab_dtype, m, n, k, batch, b_layout, splits, max_workspace_bytes, tile_m,
+                     tile_n, tile_k, plan);
+  if (st != HMX_OK) return st;
+  if (out_splits) *out_splits = plan.splits;
+  if (out_tile_m) *out_tile_m = plan.tile.bm;
+  if (out_tile_n) *out_tile_n = plan.tile.bn;
+  if (out_tile_k) *out_tile_k = plan.tile.bk;
+  if (out_workspace_bytes) *out_workspace_bytes = plan.workspace_bytes;
+  return HMX_OK;
+}
+
+int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
+             const void* b, int64_t ldb, int b_layout, int64_t b_panel, int64_t b_kpad,
+             void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int64_t batch,
+             int64_t stride_a, int64_t stride_b, int64_t stride_c, const void* bias,
+             const void* scale, const void* shift, int vec_dtype, int epilogue,
+             float epilogue_arg, int splits, void* workspace, int64_t workspace_bytes,
+             int tile_m, int tile_n, int tile_k, void* stream) {
+  HMX_REQUIRE(valid_dtype(ab_dtype) && valid_dtype(c_dtype), "gemm: unknown dtype");
+  HMX_REQUIRE((bias == nullptr && scale == nullptr && shift == nullptr) || valid_dtype(vec_dtype),
+              "gemm: unknown vector dtype %d", vec_dtype);
+  HMX_REQUIRE(valid_activation(epilogue), "gemm: unknown epilogue %d", epilogue);
+  const int lb = layout_code(b_layout);
+  HMX_REQUIRE(lb >= 0, "gemm: unknown B layout %d", b_layout);
+  HMX_REQUIRE(ab_dtype == HMX_DTYPE_BF16 || lb == L_KCONTIG || lb == L_RCONTIG ||
+                  lb == L_BLOCKED || lb == L_PANELS,
+              "gemm: VNNI layouts pair bf16 values; f32 B takes row-major, blocked or panel layouts");
+  HMX_REQUIRE(!trans_a || lb == L_KCONTIG || lb == L_RCONTIG,
+              "gemm: packed B layouts take a row-major A");
+  HMX_REQUIRE(m >= 0 && n >= 0 && k >= 0 && batch >= 1, "gemm: invalid shape [%lld, %lld, %lld] x %lld",
+              (long long)m, (long long)n, (long long)k, (long long)batch);
+  HMX_REQUIRE(a && b && c, "gemm: null operand");
+  HMX_REQUIRE(splits >= 0, "gemm: negative splits");
+  const bool packed = lb != L_KCONTIG && lb != L_RCONTIG;
+  if (!packed) {
+    HMX_REQUIRE(lda >= (trans_a ? m : k) && lda >= 1, "gemm: lda %lld too small", (long long)lda);
+    HMX_REQUIRE(ldb >= (lb == L_KCONTIG ? k : n) && ldb >= 1, "gemm: ldb %lld too small", (long long)ldb);
+  } else {
+    HMX_REQUIRE(b_kpad >= k && b_kpad % (lb == L_VNNI_PANELS ? 2 : 1) == 0,
+                "gemm: packed K extent %lld does not cover K %lld", (long long)b_kpad, (long long)k);
+    if (lb == L_BLOCKED_VNNI || lb == L_BLOCKED)
+      HMX_REQUIRE(b_kpad % 32 == 0, "gemm: blocked K extent %lld is not a multiple of 32", (long long)b_kpad);
+    if (lb == L_VNNI_PANELS || lb == L_PANELS)
+      HMX_REQUIRE(b_panel >= 8 && b_panel % (lb == L_VNNI_PANELS ? 4 : 8) == 0,
+                  "gemm: panel width %lld unsupported", (long long)b_panel);
+  }
+  HMX_REQUIRE(ldc >= n && ldc >= 1, "gemm: ldc %lld too small", (long long)ldc);
+  if (m == 0 || n == 0) return HMX_OK;
+
+  Plan plan;
+  make_plan(ab_dtype, m, n, k, batch, b_layout, splits, workspace ? workspace_bytes : 0,
+            tile_m, tile_n, tile_k, plan);
+  if (plan.splits > 1) {
+    HMX_REQUIRE(workspace != nullptr && workspace_bytes >= plan.workspace_bytes,
+                "gemm: split-K needs %lld workspace bytes, got %lld",
+                (long long)plan.workspace_bytes, (long long)workspace_bytes);
+  }
+  const int64_t tiles_m = ceil_div(m, plan.tile.bm), tiles_n = ceil_div(n, plan.tile.bn);
+  HMX_REQUIRE(tiles_m * tiles_n < ((int64_t)1 << 31) && batch < 65536 && plan.splits < 65536,
+              "gemm: grid too large");
+
+  const int64_t esz = dtype_bytes(ab_dtype);
+  const int64_t vec_elems = 16 / esz;
+  GemmArgs g{};
+  const int la = trans_a ? L_RCONTIG : L_KCONTIG;
+  g.a = Operand{a, lda, m, 0, 0, aligned16(a) && lda % vec_elems == 0 &&
+                                     (batch == 1 || stride_a % vec_elems == 0)};
+  const int64_t b_rows = packed ? (lb == L_BLOCKED_VNNI || lb == L_BLOCKED ? ceil_div(n, 32) * 32
+                                                                           : ceil_div(n, b_panel) * b_panel)
+                                : n;
+  g.b = Operand{b, ldb, b_rows, b_panel, b_kpad,
+                aligned16(b) && (packed || ldb % vec_elems == 0) &&
+                    (batch == 1 || stride_b % vec_elems == 0)};
+  // Packed layouts read zeros (their padding) past N up to the padded extent;
+  // columns past N are never stored.
+  g.stride_a = stride_a;
+  g.stride_b = stride_b;
+  g.m = m;
+  g.n = n;
+  g.k = k;
+  g.k_chunk = plan.k_chunk;
+  g.tiles_m = (int)tiles_m;
+  g.tiles_n = (int)tiles_n;
+  g.bias = bias;
+  g.scale = scale;
+  g.shift = shift;
+  g.vec_dtype = vec_dtype;
+  g.act = epilogue;
+  g.act_arg = epilogue_arg;
+  if (plan.splits > 1) {
+    g.c = workspace;
+    g.c_dtype = HMX_DTYPE_F32;
+    g.ldc = n;
+    g.stride_c = m * n;
+    g.stride_split = batch * m * n;
+    g.bias = g.scale = g.shift = nullptr;
+    g.act = HMX_EPI_IDENTITY;
+  } else {
+    g.c = c;
+    g.c_dtype = c_dtype;
+    g.ldc = ldc;
+    g.stride_c = stride_c;
+    g.stride_split = 0;
+  }
+
+  const bool whole = m % plan.tile.bm == 0 && n % plan.tile.bn == 0 &&
+                     plan.k_chunk % plan.tile.bk == 0 && k % plan.tile.bk == 0;
+  const bool guard = !(whole && g.a.vec && g.b.vec);
+  const dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)plan.splits, (unsigned)batch);
+  auto s = (hipStream_t)stream;
+  if (ab_dtype == HMX_DTYPE_BF16) {
+    const TileChoice t = plan.tile;
+    if (t.bm == 256)
+      dispatch_bf16<Bf16Cfg<256, 256, 64>>(g, la, lb, guard, grid, s);
+    else
+      dispatch_bf16<Bf16Cfg<128, 128, 64>>(g, la, lb, guard, grid, s);
+  } else {
+    dispatch_f32<F32Cfg<128, 128, 32>>(g, la, lb, guard, grid, s);
+  }
+  int st = check_launch("gemm");
+  if (st != HMX_OK || plan.splits <= 1) return st;
+
+  GemmArgs r = g;
+  r.c = c;
+  r.c_dtype = c_dtype;
+  r.ldc = ldc;
+  r.stride_c = stride_c;
+  r.bias = bias;
+  r.scale = scale;
+  r.shift = shift;
+  r.act = epilogue;
+  const int64_t total = batch * m * n;
+  const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(total, 256), 16384);
+  splitk_reduce_kernel<<<blocks, 256, 0, s>>>((const float*)workspace, plan.splits, batch, r);
+  return check_launch("gemm split-K reduce");
+}
+
+}  // extern "C"

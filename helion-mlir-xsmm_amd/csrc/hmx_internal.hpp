@@ -1,0 +1,37 @@
+// Host-side plumbing shared by libhmx's translation units: the per-thread
+// error message, argument checks and launch-error capture.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "hmx.h"
+
+namespace hmx {
+
+// Records the calling thread's error message and returns `status`.
+int set_error(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+// The HIP error of the last launch on this thread, as an hmx status.
+int check_launch(const char* what);
+
+inline bool valid_dtype(int dtype) {
+  return dtype == HMX_DTYPE_F32 || dtype == HMX_DTYPE_BF16;
+}
+inline int64_t dtype_bytes(int dtype) { return dtype == HMX_DTYPE_BF16 ? 2 : 4; }
+inline bool valid_activation(int code) {
+  return code >= HMX_EPI_IDENTITY && code <= HMX_EPI_LEAKY_RELU;
+}
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace hmx
+
+#define HMX_REQUIRE(cond, ...)                                   \
+  do {                                                           \
+    if (!(cond)) return ::hmx::set_error(HMX_ERR_INVALID, __VA_ARGS__); \
+  } while (0)

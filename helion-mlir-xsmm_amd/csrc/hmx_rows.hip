@@ -1,0 +1,632 @@
+// Memory-bound row kernels for gfx950: softmax, RMSNorm, GroupNorm/LayerNorm,
+// row sums, row dots, gemv, column sums and elementwise ops.
+//
+// One wave64 owns one row (or one (row, group) unit). A row of up to
+// 64 * kMaxPerLane elements is read once from HBM with 16-byte loads
+// (`global_load_dwordx4`) into registers, reduced with xor butterflies across
+// the wave, and written once: one HBM read and one write per element, the
+// floor for these ops. Longer rows stream through the same code in chunks
+// (extra reads from L2/HBM). Four waves share a 256-thread workgroup, so a
+// [32768, 4096] input launches 8192 workgroups (32 per CU).
+#include <type_traits>
+#include <utility>
+
+#include "hmx_device.hpp"
+
+namespace hmx {
+namespace {
+
+constexpr int kRowsPerBlock = 4;
+constexpr int kBlock = kRowsPerBlock * kWave;
+// f32 values a lane keeps of a cached row: 64 VGPRs.
+constexpr int kMaxPerLane = 64;
+
+// ---------------------------------------------------------------------------
+// Row access. A lane's j-th vector of a row covers columns
+// [(j * 64 + lane) * EPV, ... + EPV): for each j the wave reads one contiguous
+// 64 * EPV run, so every load instruction is fully coalesced.
+template <typename T, int EPV, int VPL>
+__device__ __forceinline__ void load_row(const T* __restrict__ p, int64_t n, int lane,
+                                         float (&v)[VPL * EPV], float fill) {
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int64_t col = ((int64_t)j * kWave + lane) * EPV;
+    if constexpr (EPV > 1) {
+      if (col + EPV <= n) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(p + col);
+        Elem<T>::unpack(raw, &v[j * EPV]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPV; ++e)
+          v[j * EPV + e] = (col + e < n) ? Elem<T>::load(p + col + e) : fill;
+      }
+    } else {
+      v[j] = col < n ? Elem<T>::load(p + col) : fill;
+    }
+  }
+}
+
+template <typename T, int EPV, int VPL>
+__device__ __forceinline__ void store_row(T* __restrict__ p, int64_t n, int lane,
+                                          const float (&v)[VPL * EPV]) {
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int64_t col = ((int64_t)j * kWave + lane) * EPV;
+    if constexpr (EPV > 1) {
+      if (col + EPV <= n) {
+        *reinterpret_cast<uint4*>(p + col) = Elem<T>::pack(&v[j * EPV]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPV; ++e)
+          if (col + e < n) Elem<T>::store(p + col + e, v[j * EPV + e]);
+      }
+    } else {
+      if (col < n) Elem<T>::store(p + col, v[j]);
+    }
+  }
+}
+
+// Column of element e of a lane's j-th vector.
+template <int EPV>
+__device__ __forceinline__ int64_t col_of(int j, int lane, int e) {
+  return ((int64_t)j * kWave + lane) * EPV + e;
+}
+
+// Streaming access for rows longer than the register cache: chunk c of a row
+// is the c-th run of 64 * EPV columns.
+template <typename T, int EPV>
+__device__ __forceinline__ void load_chunk(const T* __restrict__ p, int64_t n, int64_t col,
+                                           float (&v)[EPV], float fill) {
+  if constexpr (EPV > 1) {
+    if (col + EPV <= n) {
+      Elem<T>::unpack(*reinterpret_cast<const uint4*>(p + col), v);
+      return;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) v[e] = (col + e < n) ? Elem<T>::load(p + col + e) : fill;
+}
+
+template <typename T, int EPV>
+__device__ __forceinline__ void store_chunk(T* __restrict__ p, int64_t n, int64_t col,
+                                            const float (&v)[EPV]) {
+  if constexpr (EPV > 1) {
+    if (col + EPV <= n) {
+      *reinterpret_cast<uint4*>(p + col) = Elem<T>::pack(v);
+      return;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < EPV; ++e)
+    if (col + e < n) Elem<T>::store(p + col + e, v[e]);
+}
+
+// EPV consecutive f32 values (zero past n), as 16-byte loads where they fit.
+template <int EPV>
+__device__ __forceinline__ void load_f32_run(const float* __restrict__ p, int64_t n,
+                                             int64_t col, float (&u)[EPV]) {
+  if constexpr (EPV % 4 == 0) {
+    if (col + EPV <= n) {
+#pragma unroll
+      for (int q = 0; q < EPV / 4; ++q)
+        Elem<float>::unpack(*reinterpret_cast<const uint4*>(p + col + 4 * q), &u[4 * q]);
+      return;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) u[e] = (col + e < n) ? p[col + e] : 0.f;
+}
+
+__device__ __forceinline__ int64_t unit_index() {
+  return (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+}
+
+// ---------------------------------------------------------------------------
+// Softmax: max, sum of exp(x - max), then exp(x - max) * (1 / sum), as
+// helion_mlir_utils/normalization.py:47-72 computes it (f32 inside, one
+// rounding), with the row held in registers between the passes.
+template <typename T, int EPV, int VPL>
+__global__ __launch_bounds__(kBlock) void softmax_cached(const T* x,
+                                                         T* y, int64_t m,
+                                                         int64_t n) {
+  const int64_t row = unit_index();
+  if (row >= m) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  float v[VPL * EPV];
+  load_row<T, EPV, VPL>(x + row * n, n, lane, v, -INFINITY);
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < VPL * EPV; ++i) mx = fmaxf(mx, v[i]);
+  mx = wave_max(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL * EPV; ++i) {
+    v[i] = fast_exp(v[i] - mx);
+    if (col_of<EPV>(i / EPV, lane, i % EPV) < n) sum += v[i];
+  }
+  sum = wave_sum(sum);
+  const float inv = 1.f / sum;
+#pragma unroll
+  for (int i = 0; i < VPL * EPV; ++i) v[i] *= inv;
+  store_row<T, EPV, VPL>(y + row * n, n, lane, v);
+}
+
+template <typename T, int EPV>
+__global__ __launch_bounds__(kBlock) void softmax_stream(const T* x,
+                                                         T* y, int64_t m,
+                                                         int64_t n) {
+  const int64_t row = unit_index();
+  if (row >= m) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const T* xr = x + row * n;
+  T* yr = y + row * n;
+  const int64_t step = (int64_t)kWave * EPV;
+  float v[EPV];
+  float mx = -INFINITY;
+  for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
+    load_chunk<T, EPV>(xr, n, col, v, -INFINITY);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) mx = fmaxf(mx, v[e]);
+  }
+  mx = wave_max(mx);
+  float sum = 0.f;
+  for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
+    load_chunk<T, EPV>(xr, n, col, v, -INFINITY);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e)
+      if (col + e < n) sum += fast_exp(v[e] - mx);
+  }
+  const float inv = 1.f / wave_sum(sum);
+  for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
+    load_chunk<T, EPV>(xr, n, col, v, 0.f);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) v[e] = fast_exp(v[e] - mx) * inv;
+    store_chunk<T, EPV>(yr, n, col, v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm: x * rsqrt(mean(x^2) + eps) * w in f32, rounded once.
+template <typename T, int EPV, int VPL>
+__global__ __launch_bounds__(kBlock) void rmsnorm_cached(const T* x,
+                                                         const void* __restrict__ w,
+                                                         int w_dtype, T* y,
+                                                         int64_t m, int64_t n, float eps) {
+  const int64_t row = unit_index();
+  if (row >= m) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  float v[VPL * EPV];
+  load_row<T, EPV, VPL>(x + row * n, n, lane, v, 0.f);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL * EPV; ++i) ss += v[i] * v[i];
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / (float)n + eps);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      const int64_t col = col_of<EPV>(j, lane, e);
+      const float wv = (w != nullptr && col < n) ? load_any(w, w_dtype, col) : 1.f;
+      v[j * EPV + e] = v[j * EPV + e] * r * wv;
+    }
+  }
+  store_row<T, EPV, VPL>(y + row * n, n, lane, v);
+}
+
+template <typename T, int EPV>
+__global__ __launch_bounds__(kBlock) void rmsnorm_stream(const T* x,
+                                                         const void* __restrict__ w,
+                                                         int w_dtype, T* y,
+                                                         int64_t m, int64_t n, float eps) {
+  const int64_t row = unit_index();
+  if (row >= m) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const T* xr = x + row * n;
+  T* yr = y + row * n;
+  const int64_t step = (int64_t)kWave * EPV;
+  float v[EPV];
+  float ss = 0.f;
+  for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
+    load_chunk<T, EPV>(xr, n, col, v, 0.f);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) ss += v[e] * v[e];
+  }
+  const float r = rsqrtf(wave_sum(ss) / (float)n + eps);
+  for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
+    load_chunk<T, EPV>(xr, n, col, v, 0.f);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      const float wv = (w != nullptr && col + e < n) ? load_any(w, w_dtype, col + e) : 1.f;
+      v[e] = v[e] * r * wv;
+    }
+    store_chunk<T, EPV>(yr, n, col, v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GroupNorm over units of `gs` elements (row r, group g at r * G * gs + g * gs):
+// mean, centered variance, ((x - mean) * rsqrt(var + eps)) * w + b, then the
+// extra operand and activation; normalization.py:113-122.
+struct GroupNormArgs {
+  const void* w;
+  const void* b;
+  const void* extra;
+  int vec_dtype;
+  int64_t units;
+  int64_t groups;
+  int64_t gs;
+  float eps;
+  int extra_op;
+  int act;
+  float act_arg;
+};
+
+__device__ __forceinline__ float group_norm_out(const GroupNormArgs& a, float centered,
+                                                float r, int64_t ch) {
+  float yv = centered * r * (a.w ? load_any(a.w, a.vec_dtype, ch) : 1.f);
+  if (a.b) yv += load_any(a.b, a.vec_dtype, ch);
+  if (a.extra_op == HMX_EXTRA_ADD) yv += load_any(a.extra, a.vec_dtype, ch);
+  if (a.extra_op == HMX_EXTRA_MUL) yv *= load_any(a.extra, a.vec_dtype, ch);
+  return apply_activation(a.act, yv, a.act_arg);
+}
+
+template <typename T, int EPV, int VPL>
+__global__ __launch_bounds__(kBlock) void group_norm_cached(const T* x,
+                                                            T* y,
+                                                            GroupNormArgs a) {
+  const int64_t unit = unit_index();
+  if (unit >= a.units) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t g = unit % a.groups;
+  const int64_t n = a.gs;
+  float v[VPL * EPV];
+  load_row<T, EPV, VPL>(x + unit * n, n, lane, v, 0.f);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL * EPV; ++i) s += v[i];
+  const float mean = wave_sum(s) / (float)n;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL * EPV; ++i) {
+    const float c = v[i] - mean;
+    if (col_of<EPV>(i / EPV, lane, i % EPV) < n) q += c * c;
+  }
+  const float r = rsqrtf(wave_sum(q) / (float)n + a.eps);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      const int64_t col = col_of<EPV>(j, lane, e);
+      if (col < n) v[j * EPV + e] = group_norm_out(a, v[j * EPV + e] - mean, r, g * n + col);
+    }
+  }
+  store_row<T, EPV, VPL>(y + unit * n, n, lane, v);
+}
+
+template <typename T, int EPV>
+__global__ __launch_bounds__(kBlock) void group_norm_stream(const T* x,
+                                                            T* y,
+                                                            GroupNormArgs a) {
+  const int64_t unit = unit_index();
+  if (unit >= a.units) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t g = unit % a.groups;
+  const int64_t n = a.gs;
+  const T* xr = x + unit * n;
+  T* yr = y + unit * n;
+  const int64_t step = (int64_t)kWave * EPV;
+  float v[EPV];
+  float s = 0.f;
+  for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
+    load_chunk<T, EPV>(xr, n, col, v, 0.f);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) s += v[e];
+  }
+  const float mean = wave_sum(s) / (float)n;
+  float q = 0.f;
+  for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
+    load_chunk<T, EPV>(xr, n, col, v, 0.f);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e)
+      if (col + e < n) q += (v[e] - mean) * (v[e] - mean);
+  }
+  const float r = rsqrtf(wave_sum(q) / (float)n + a.eps);
+  for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
+    load_chunk<T, EPV>(xr, n, col, v, 0.f);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e)
+      if (col + e < n) v[e] = group_norm_out(a, v[e] - mean, r, g * n + col + e);
+    store_chunk<T, EPV>(yr, n, col, v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Row reductions read each element once: streaming is their natural form.
+// mode 0: sum x; mode 1: sum x * v (v f32); mode 2: sum x * v (v of type T).
+template <typename T, int EPV, int MODE>
+__global__ __launch_bounds__(kBlock) void row_reduce(const T* x,
+                                                     const void* __restrict__ vec,
+                                                     T* y, int64_t m,
+                                                     int64_t n, int act, float act_arg) {
+  const int64_t row = unit_index();
+  if (row >= m) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const T* xr = x + row * n;
+  const int64_t step = (int64_t)kWave * EPV;
+  float v[EPV];
+  float s = 0.f;
+  for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
+    load_chunk<T, EPV>(xr, n, col, v, 0.f);
+    if constexpr (MODE == 0) {
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) s += v[e];
+    } else if constexpr (MODE == 1) {
+      float u[EPV];
+      load_f32_run<EPV>((const float*)vec, n, col, u);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) s += v[e] * u[e];
+    } else {
+      float u[EPV];
+      load_chunk<T, EPV>((const T*)vec, n, col, u, 0.f);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) s += v[e] * u[e];
+    }
+  }
+  s = wave_sum(s);
+  if (lane == 0) Elem<T>::store(y + row, apply_activation(act, s, act_arg));
+}
+
+// Column sums: one thread per column walks all rows (each row read by a wave
+// as one contiguous run); f32 accumulation in row order.
+template <typename T>
+__global__ __launch_bounds__(256) void column_sum_kernel(const T* x,
+                                                         float* __restrict__ y, int64_t m,
+                                                         int64_t n) {
+  const int64_t col = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (col >= n) return;
+  float s = 0.f;
+  for (int64_t r = 0; r < m; ++r) s += Elem<T>::load(x + r * n + col);
+  y[col] = s + 0.f;
+}
+
+// Elementwise ops over 16-byte vectors (EPV elements), scalar tail.
+template <typename T, int EPV>
+__global__ __launch_bounds__(256) void elementwise_kernel(const T* x,
+                                                          T* y, int64_t numel,
+                                                          int op, float arg) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x * EPV;
+  for (int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * EPV; i < numel;
+       i += stride) {
+    float v[EPV];
+    load_chunk<T, EPV>(x, numel, i, v, 0.f);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      if (op == HMX_ELT_RELU)
+        v[e] = apply_activation(HMX_EPI_RELU, v[e], 0.f);
+      else if (op == HMX_ELT_LEAKY_RELU)
+        v[e] = v[e] > 0.f ? v[e] : v[e] * arg;
+      else
+        v[e] = v[e] * arg;
+    }
+    store_chunk<T, EPV>(y, numel, i, v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch.
+
+// The smallest vectors-per-lane that holds an n-element row in registers, or
+// 0 if the row needs the streaming kernel.
+int pick_vpl(int64_t n, int epv) {
+  for (int vpl = 1; vpl * epv <= kMaxPerLane; vpl *= 2)
+    if ((int64_t)kWave * vpl * epv >= n) return vpl;
+  return 0;
+}
+
+template <int V>
+using IntC = std::integral_constant<int, V>;
+
+// Calls f(IntC<VPL>) for the runtime vpl (a power of two, VPL * EPV <= 64).
+template <int EPV, typename F>
+void with_vpl(int vpl, F&& f) {
+  switch (vpl) {
+    case 1: f(IntC<1>{}); break;
+    case 2: f(IntC<2>{}); break;
+    case 4: f(IntC<4>{}); break;
+    case 8: f(IntC<8>{}); break;
+    case 16: if constexpr (16 * EPV <= kMaxPerLane) f(IntC<16>{}); break;
+    case 32: if constexpr (32 * EPV <= kMaxPerLane) f(IntC<32>{}); break;
+    case 64: if constexpr (64 * EPV <= kMaxPerLane) f(IntC<64>{}); break;
+  }
+}
+
+// Calls f(T*, IntC<EPV>) for the dtype and whether 16-byte vectors apply.
+template <typename F>
+void with_type(int dtype, bool vec, F&& f) {
+  if (dtype == HMX_DTYPE_BF16) {
+    if (vec) f((uint16_t*)nullptr, IntC<8>{});
+    else f((uint16_t*)nullptr, IntC<1>{});
+  } else {
+    if (vec) f((float*)nullptr, IntC<4>{});
+    else f((float*)nullptr, IntC<1>{});
+  }
+}
+
+// Whether rows of `n` elements starting at `p` (and `q`) keep 16-byte alignment.
+bool rows_vectorizable(const void* p, const void* q, int64_t n, int dtype) {
+  const int64_t epv = 16 / dtype_bytes(dtype);
+  return aligned16(p) && aligned16(q) && n % epv == 0;
+}
+
+dim3 unit_grid(int64_t units) { return dim3((unsigned)ceil_div(units, kRowsPerBlock)); }
+
+}  // namespace
+}  // namespace hmx
+
+using namespace hmx;
+
+extern "C" {
+
+int hmx_softmax_rows(int dtype, const void* x, void* y, int64_t m, int64_t n,
+                     void* stream) {
+  HMX_REQUIRE(valid_dtype(dtype), "softmax: unknown dtype %d", dtype);
+  HMX_REQUIRE(m >= 0 && n >= 1, "softmax: invalid shape [%lld, %lld]", (long long)m,
+              (long long)n);
+  HMX_REQUIRE(x && y, "softmax: null operand");
+  HMX_REQUIRE(m <= ((int64_t)1 << 31) * kRowsPerBlock, "softmax: too many rows");
+  if (m == 0) return HMX_OK;
+  auto s = (hipStream_t)stream;
+  with_type(dtype, rows_vectorizable(x, y, n, dtype), [&](auto tp, auto epv_c) {
+    using T = std::remove_pointer_t<decltype(tp)>;
+    constexpr int EPV = decltype(epv_c)::value;
+    const int vpl = pick_vpl(n, EPV);
+    if (vpl == 0) {
+      softmax_stream<T, EPV><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, (T*)y, m, n);
+    } else {
+      with_vpl<EPV>(vpl, [&](auto vpl_c) {
+        softmax_cached<T, EPV, decltype(vpl_c)::value>
+            <<<unit_grid(m), kBlock, 0, s>>>((const T*)x, (T*)y, m, n);
+      });
+    }
+  });
+  return check_launch("softmax");
+}
+
+int hmx_rmsnorm_rows(int dtype, const void* x, const void* w, int w_dtype, void* y,
+                     int64_t m, int64_t n, float eps, void* stream) {
+  HMX_REQUIRE(valid_dtype(dtype) && (w == nullptr || valid_dtype(w_dtype)),
+              "rms_norm: unknown dtype");
+  HMX_REQUIRE(m >= 0 && n >= 1, "rms_norm: invalid shape [%lld, %lld]", (long long)m,
+              (long long)n);
+  HMX_REQUIRE(x && y, "rms_norm: null operand");
+  HMX_REQUIRE(m <= ((int64_t)1 << 31) * kRowsPerBlock, "rms_norm: too many rows");
+  if (m == 0) return HMX_OK;
+  auto s = (hipStream_t)stream;
+  with_type(dtype, rows_vectorizable(x, y, n, dtype), [&](auto tp, auto epv_c) {
+    using T = std::remove_pointer_t<decltype(tp)>;
+    constexpr int EPV = decltype(epv_c)::value;
+    const int vpl = pick_vpl(n, EPV);
+    if (vpl == 0) {
+      rmsnorm_stream<T, EPV>
+          <<<unit_grid(m), kBlock, 0, s>>>((const T*)x, w, w_dtype, (T*)y, m, n, eps);
+    } else {
+      with_vpl<EPV>(vpl, [&](auto vpl_c) {
+        rmsnorm_cached<T, EPV, decltype(vpl_c)::value>
+            <<<unit_grid(m), kBlock, 0, s>>>((const T*)x, w, w_dtype, (T*)y, m, n, eps);
+      });
+    }
+  });
+  return check_launch("rms_norm");
+}
+
+int hmx_group_norm_rows(int dtype, const void* x, const void* w, const void* b,
+                        const void* extra, int vec_dtype, void* y, int64_t m,
+                        int64_t groups, int64_t group_size, float eps, int extra_op,
+                        int activation, float activation_arg, void* stream) {
+  HMX_REQUIRE(valid_dtype(dtype) && valid_dtype(vec_dtype), "group_norm: unknown dtype");
+  HMX_REQUIRE(m >= 0 && groups >= 1 && group_size >= 1, "group_norm: invalid shape");
+  HMX_REQUIRE(x && y, "group_norm: null operand");
+  HMX_REQUIRE(extra_op >= HMX_EXTRA_NONE && extra_op <= HMX_EXTRA_MUL,
+              "group_norm: unknown extra op %d", extra_op);
+  HMX_REQUIRE(extra_op == HMX_EXTRA_NONE || extra != nullptr,
+              "group_norm: extra op without an extra operand");
+  HMX_REQUIRE(valid_activation(activation), "group_norm: unknown activation %d", activation);
+  const int64_t units = m * groups;
+  HMX_REQUIRE(units <= ((int64_t)1 << 31) * kRowsPerBlock, "group_norm: too many rows");
+  if (units == 0) return HMX_OK;
+  GroupNormArgs a{w, b, extra, vec_dtype, units, groups, group_size, eps,
+                  extra_op, activation, activation_arg};
+  auto s = (hipStream_t)stream;
+  with_type(dtype, rows_vectorizable(x, y, group_size, dtype), [&](auto tp, auto epv_c) {
+    using T = std::remove_pointer_t<decltype(tp)>;
+    constexpr int EPV = decltype(epv_c)::value;
+    const int vpl = pick_vpl(group_size, EPV);
+    if (vpl == 0) {
+      group_norm_stream<T, EPV><<<unit_grid(units), kBlock, 0, s>>>((const T*)x, (T*)y, a);
+    } else {
+      with_vpl<EPV>(vpl, [&](auto vpl_c) {
+        group_norm_cached<T, EPV, decltype(vpl_c)::value>
+            <<<unit_grid(units), kBlock, 0, s>>>((const T*)x, (T*)y, a);
+      });
+    }
+  });
+  return check_launch("group_norm");
+}
+
+static int row_reduce_launch(const char* name, int mode, int dtype, const void* x,
+                             const void* vec, void* y, int64_t m, int64_t n, int act,
+                             float act_arg, void* stream) {
+  HMX_REQUIRE(valid_dtype(dtype), "%s: unknown dtype %d", name, dtype);
+  HMX_REQUIRE(m >= 0 && n >= 0, "%s: invalid shape", name);
+  HMX_REQUIRE(x && y && (mode == 0 || vec), "%s: null operand", name);
+  HMX_REQUIRE(valid_activation(act), "%s: unknown activation %d", name, act);
+  HMX_REQUIRE(m <= ((int64_t)1 << 31) * kRowsPerBlock, "%s: too many rows", name);
+  if (m == 0) return HMX_OK;
+  auto s = (hipStream_t)stream;
+  bool vec_ok = rows_vectorizable(x, x, n, dtype);
+  if (mode != 0) vec_ok = vec_ok && aligned16(vec);
+  with_type(dtype, vec_ok, [&](auto tp, auto epv_c) {
+    using T = std::remove_pointer_t<decltype(tp)>;
+    constexpr int EPV = decltype(epv_c)::value;
+    if (mode == 0)
+      row_reduce<T, EPV, 0><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, vec, (T*)y, m, n, act, act_arg);
+    else if (mode == 1)
+      row_reduce<T, EPV, 1><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, vec, (T*)y, m, n, act, act_arg);
+    else
+      row_reduce<T, EPV, 2><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, vec, (T*)y, m, n, act, act_arg);
+  });
+  return check_launch(name);
+}
+
+int hmx_row_sum(int dtype, const void* x, void* y, int64_t m, int64_t n, int activation,
+                float activation_arg, void* stream) {
+  return row_reduce_launch("row_sum", 0, dtype, x, nullptr, y, m, n, activation,
+                           activation_arg, stream);
+}
+
+int hmx_row_dot(int dtype, const void* x, const float* v, void* y, int64_t m, int64_t n,
+                int activation, float activation_arg, void* stream) {
+  return row_reduce_launch("row_dot", 1, dtype, x, v, y, m, n, activation, activation_arg,
+                           stream);
+}
+
+int hmx_matvec(int dtype, const void* a, const void* x, void* y, int64_t m, int64_t k,
+               void* stream) {
+  return row_reduce_launch("matvec", 2, dtype, a, x, y, m, k, HMX_EPI_IDENTITY, 0.f, stream);
+}
+
+int hmx_column_sum(int dtype, const void* x, float* y, int64_t m, int64_t n, void* stream) {
+  HMX_REQUIRE(valid_dtype(dtype), "column_sum: unknown dtype %d", dtype);
+  HMX_REQUIRE(m >= 0 && n >= 0, "column_sum: invalid shape");
+  HMX_REQUIRE(x && y, "column_sum: null operand");
+  if (n == 0) return HMX_OK;
+  auto s = (hipStream_t)stream;
+  const dim3 grid((unsigned)ceil_div(n, 256));
+  if (dtype == HMX_DTYPE_BF16)
+    column_sum_kernel<uint16_t><<<grid, 256, 0, s>>>((const uint16_t*)x, y, m, n);
+  else
+    column_sum_kernel<float><<<grid, 256, 0, s>>>((const float*)x, y, m, n);
+  return check_launch("column_sum");
+}
+
+int hmx_elementwise(int op, int dtype, const void* x, void* y, int64_t numel, float arg,
+                    void* stream) {
+  HMX_REQUIRE(valid_dtype(dtype), "elementwise: unknown dtype %d", dtype);
+  HMX_REQUIRE(op >= HMX_ELT_RELU && op <= HMX_ELT_SCALE, "elementwise: unknown op %d", op);
+  HMX_REQUIRE(numel >= 0, "elementwise: negative size");
+  HMX_REQUIRE(x && y, "elementwise: null operand");
+  if (numel == 0) return HMX_OK;
+  auto s = (hipStream_t)stream;
+  const bool vec = aligned16(x) && aligned16(y);
+  with_type(dtype, vec, [&](auto tp, auto epv_c) {
+    using T = std::remove_pointer_t<decltype(tp)>;
+    constexpr int EPV = decltype(epv_c)::value;
+    const int64_t blocks = std::min<int64_t>(ceil_div(numel, 256 * EPV), 8192);
+    elementwise_kernel<T, EPV><<<dim3((unsigned)blocks), 256, 0, s>>>((const T*)x, (T*)y,
+                                                                       numel, op, arg);
+  });
+  return check_launch("elementwise");
+}
+
+}  // extern "C"

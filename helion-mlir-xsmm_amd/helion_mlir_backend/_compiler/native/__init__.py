@@ -1,0 +1,211 @@
+"""The native call path of the ``gpu`` target: ``libhmx.so``, a C-ABI library of
+hand-written gfx950 HIP kernels, bound with ctypes.
+
+Stands in for the reference's native call path
+(``helion_mlir_backend/_compiler/native/__init__.py:107-236`` and ``call.cpp``):
+there, a C++ CPython extension checks arguments and calls a JIT-compiled CPU
+entry without the GIL. Here every hot-path kernel family has one typed C entry
+point (``include/hmx.h``); this module loads the library, declares the
+signatures, and turns a non-zero status into a Python exception. ctypes
+releases the GIL around each call, as ``call.cpp:194-196`` does.
+
+There is no fallback: if the library is missing or the device is not a
+gfx950, calls raise. ``HMX_LIBRARY`` may name another build of the library.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+import threading
+
+import torch
+
+from ..support.errors import UnsupportedTargetError
+
+LIBRARY_ENV = "HMX_LIBRARY"
+NATIVE_CALL_ENV = "HELION_MLIR_NATIVE_CALL"
+_DEFAULT = Path(__file__).resolve().parents[3] / "csrc" / "libhmx.so"
+
+# Status codes, dtypes and enumerations of include/hmx.h.
+OK, ERR_INVALID, ERR_HIP, ERR_UNSUPPORTED = 0, 1, 2, 3
+DTYPE_F32, DTYPE_BF16 = 0, 1
+EPI_IDENTITY, EPI_RELU, EPI_SILU, EPI_SIGMOID = 0, 1, 2, 3
+EPI_GELU, EPI_GELU_TANH, EPI_TANH, EPI_LEAKY_RELU = 4, 5, 6, 7
+B_ROW, B_TRANS, B_VNNI_PANELS, B_BLOCKED_VNNI, B_PANELS, B_BLOCKED = range(6)
+EXTRA_NONE, EXTRA_ADD, EXTRA_MUL = 0, 1, 2
+ELT_RELU, ELT_LEAKY_RELU, ELT_SCALE = 0, 1, 2
+(
+    PACK_PAD,
+    PACK_A_BLOCKED,
+    PACK_A_BLOCKED_T,
+    PACK_B_BLOCKED,
+    PACK_B_BLOCKED_T,
+    PACK_B_BLOCKED_VNNI,
+    PACK_B_BLOCKED_VNNI_T,
+    PACK_B_VNNI_PANELS_T,
+    PACK_B_PANELS,
+    PACK_A_PANELS,
+) = range(10)
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+_IP = ctypes.POINTER(ctypes.c_int)
+_LP = ctypes.POINTER(ctypes.c_int64)
+
+# name -> argument types (restype is int unless listed in _RESTYPES).
+SIGNATURES: dict[str, list[object]] = {
+    "hmx_last_error": [],
+    "hmx_abi_version": [],
+    "hmx_device_check": [_IP],
+    "hmx_gemm": [
+        _I, _I,  # ab_dtype, c_dtype
+        _P, _L, _I,  # a, lda, trans_a
+        _P, _L, _I, _L, _L,  # b, ldb, b_layout, b_panel, b_kpad
+        _P, _L,  # c, ldc
+        _L, _L, _L,  # m, n, k
+        _L, _L, _L, _L,  # batch, stride_a, stride_b, stride_c
+        _P, _P, _P, _I,  # bias, scale, shift, vec_dtype
+        _I, _F,  # epilogue, epilogue_arg
+        _I, _P, _L,  # splits, workspace, workspace_bytes
+        _I, _I, _I,  # tile_m, tile_n, tile_k
+        _P,  # stream
+    ],
+    "hmx_gemm_plan": [
+        _I, _L, _L, _L, _L, _I, _I, _I, _L, _I, _I, _I,
+        _IP, _IP, _IP, _IP, _LP,
+    ],
+    "hmx_softmax_rows": [_I, _P, _P, _L, _L, _P],
+    "hmx_rmsnorm_rows": [_I, _P, _P, _I, _P, _L, _L, _F, _P],
+    "hmx_group_norm_rows": [_I, _P, _P, _P, _P, _I, _P, _L, _L, _L, _F, _I, _I, _F, _P],
+    "hmx_row_sum": [_I, _P, _P, _L, _L, _I, _F, _P],
+    "hmx_column_sum": [_I, _P, _P, _L, _L, _P],
+    "hmx_row_dot": [_I, _P, _P, _P, _L, _L, _I, _F, _P],
+    "hmx_matvec": [_I, _P, _P, _P, _L, _L, _P],
+    "hmx_elementwise": [_I, _I, _P, _P, _L, _F, _P],
+    "hmx_pack": [_I, _I, _P, _L, _L, _L, _P, _L, _L, _L, _P],
+}
+_RESTYPES = {"hmx_last_error": ctypes.c_char_p}
+
+_lock = threading.Lock()
+_lib: list[ctypes.CDLL] = []
+_checked_devices: set[int] = set()
+_calls = [0]
+
+
+def library_path() -> Path:
+    """Where the library is loaded from: ``HMX_LIBRARY`` or the in-tree build."""
+    value = os.environ.get(LIBRARY_ENV, "").strip()
+    return Path(value) if value else _DEFAULT
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises ``RuntimeError`` if it is not built."""
+    if _lib:
+        return _lib[0]
+    with _lock:
+        if _lib:
+            return _lib[0]
+        path = library_path()
+        if not path.is_file():
+            raise RuntimeError(
+                f"libhmx is not built ({path} is missing): build it with "
+                "`make -C helion-mlir-xsmm_amd/csrc` or __graft_entry__.build()"
+            )
+        handle = ctypes.CDLL(str(path))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
+        if handle.hmx_abi_version() != 1:
+            raise RuntimeError(f"{path}: ABI version {handle.hmx_abi_version()}, expected 1")
+        _lib.append(handle)
+        return handle
+
+
+def available() -> bool:
+    """Whether the library is built (it may still refuse a non-gfx950 device)."""
+    return library_path().is_file()
+
+
+def last_error() -> str:
+    return lib().hmx_last_error().decode(errors="replace")
+
+
+def check(status: int, what: str) -> None:
+    """Raise for a non-zero status: ``ValueError`` for arguments the kernels
+    refused, ``UnsupportedTargetError`` for a non-gfx950 device, else
+    ``RuntimeError``."""
+    if status == OK:
+        return
+    message = f"{what}: {last_error()}"
+    if status == ERR_INVALID:
+        raise ValueError(message)
+    if status == ERR_UNSUPPORTED:
+        raise UnsupportedTargetError(what, reason=message)
+    raise RuntimeError(message)
+
+
+def call(name: str, *args: object) -> None:
+    """``name(*args)`` of the library, its status checked."""
+    fn = getattr(lib(), name)
+    _calls[0] += 1
+    check(fn(*args), name)
+
+
+def native_calls() -> int:
+    """Kernel-library calls made by this process."""
+    return _calls[0]
+
+
+def ensure_device(device: torch.device) -> None:
+    """Check once per device that it is a gfx950 the library was built for."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if index in _checked_devices:
+        return
+    with torch.cuda.device(index):
+        units = ctypes.c_int(0)
+        check(lib().hmx_device_check(ctypes.byref(units)), "hmx_device_check")
+    _checked_devices.add(index)
+
+
+def stream_of(device: torch.device) -> int:
+    """The current torch HIP stream of ``device``, as a ``hipStream_t`` value."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return DTYPE_F32
+    if dtype == torch.bfloat16:
+        return DTYPE_BF16
+    raise ValueError(f"the gpu target computes in float32 or bfloat16, got {dtype}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+# Native calls are always on for the gpu target; the switch is kept for the
+# reference's API (set_native_call), which turns the CPU target's native
+# paths on and off.
+_enabled = os.environ.get(NATIVE_CALL_ENV, "").strip().lower() not in ("0", "false", "no", "off")
+
+
+def enabled() -> bool:
+    return _enabled
+
+
+def set_native_call(enabled: bool) -> None:
+    """Kept for the reference's API (``helion_mlir_backend.set_native_call``).
+    The gpu target has a single, native path: turning it off makes its entry
+    points raise rather than run anything else."""
+    global _enabled
+    _enabled = bool(enabled)
+
+
+def refresh_allocator() -> None:
+    """No-op: device outputs come from torch's caching allocator."""

@@ -1,0 +1,169 @@
+"""The C ABI of libhmx without a GPU: the library loads, exports every entry
+point ``include/hmx.h`` declares with the signatures the Python binding uses,
+refuses bad arguments before touching a device, and plans launches on the host."""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+import re
+import subprocess
+
+import pytest
+
+from helion_mlir_backend._compiler import native
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "hmx.h"
+
+
+# The refusal tests pass fake device pointers: they must never reach a launch,
+# so they run only where no GPU is visible (the CPU suite).
+no_device = pytest.mark.skipif(
+    __import__("torch").cuda.is_available(), reason="fake pointers: CPU-only refusal test"
+)
+
+
+@pytest.fixture(scope="module")
+def lib() -> ctypes.CDLL:
+    if not native.available():
+        subprocess.run(["make", "-C", str(ROOT / "helion-mlir-xsmm_amd" / "csrc"), "-j8"], check=True,
+                       capture_output=True)
+    return native.lib()
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return re.findall(r"^(?:int|const char\*|int64_t|void)\s+\*?(hmx_\w+)\(", text, re.M)
+
+
+def test_header_declares_the_entry_points() -> None:
+    names = declared_functions()
+    for name in ("hmx_gemm", "hmx_gemm_plan", "hmx_softmax_rows", "hmx_rmsnorm_rows",
+                 "hmx_group_norm_rows", "hmx_row_sum", "hmx_column_sum", "hmx_row_dot",
+                 "hmx_matvec", "hmx_elementwise", "hmx_pack", "hmx_last_error",
+                 "hmx_abi_version", "hmx_device_check"):
+        assert name in names
+
+
+def test_library_exports_every_declared_symbol(lib: ctypes.CDLL) -> None:
+    missing = [name for name in declared_functions() if not hasattr(lib, name)]
+    assert not missing
+    out = subprocess.run(["nm", "-D", "--defined-only", str(native.library_path())],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r" T (hmx_\w+)$", out, re.M))
+    assert set(declared_functions()) <= exported
+
+
+def test_binding_covers_the_header() -> None:
+    assert set(declared_functions()) == set(native.SIGNATURES)
+
+
+def test_abi_version(lib: ctypes.CDLL) -> None:
+    assert lib.hmx_abi_version() == 1
+
+
+@pytest.mark.parametrize(
+    ("name", "args", "message"),
+    [
+        ("hmx_softmax_rows", (7, 16, 16, 4, 4, None), "unknown dtype"),
+        ("hmx_softmax_rows", (0, 16, 16, 4, 0, None), "invalid shape"),
+        ("hmx_softmax_rows", (0, None, 16, 4, 4, None), "null operand"),
+        ("hmx_rmsnorm_rows", (1, 16, None, 0, 16, -1, 4, 1e-6, None), "invalid shape"),
+        ("hmx_group_norm_rows", (0, 16, 16, 16, None, 0, 16, 2, 3, 4, 1e-5, 1, 0, 0.0, None),
+         "extra op without an extra operand"),
+        ("hmx_group_norm_rows", (0, 16, 16, 16, 16, 0, 16, 2, 3, 4, 1e-5, 0, 99, 0.0, None),
+         "unknown activation"),
+        ("hmx_row_sum", (0, 16, 16, 2, 2, 42, 0.0, None), "unknown activation"),
+        ("hmx_elementwise", (9, 0, 16, 16, 4, 0.0, None), "unknown op"),
+        ("hmx_pack", (42, 0, 16, 4, 4, 4, 16, 32, 32, 0, None), "unknown kind"),
+        ("hmx_pack", (1, 0, 16, 4, 4, 4, 16, 40, 32, 0, None), "multiples of 32"),
+        ("hmx_pack", (7, 1, 16, 4, 4, 4, 16, 32, 30, 32, None), "VNNI panels"),
+    ],
+)
+@no_device
+def test_invalid_arguments_are_refused(lib: ctypes.CDLL, name: str, args: tuple, message: str) -> None:
+    fn = getattr(lib, name)
+    assert fn(*args) == native.ERR_INVALID
+    assert message in native.last_error()
+
+
+def _gemm(lib: ctypes.CDLL, **kw: object) -> int:
+    args = dict(ab=1, c=1, a=16, lda=64, trans_a=0, b=16, ldb=64, layout=0, panel=0, kpad=0,
+                cp=16, ldc=64, m=64, n=64, k=64, batch=1, sa=0, sb=0, sc=0, bias=None,
+                scale=None, shift=None, vd=0, epi=0, arg=0.0, splits=1, ws=None, wsb=0,
+                tm=0, tn=0, tk=0, stream=None)
+    args.update(kw)
+    return lib.hmx_gemm(*args.values())
+
+
+@pytest.mark.parametrize(
+    ("kw", "message"),
+    [
+        ({"ab": 5}, "unknown dtype"),
+        ({"layout": 9}, "unknown B layout"),
+        ({"ab": 0, "layout": native.B_VNNI_PANELS, "panel": 64, "kpad": 64}, "VNNI layouts"),
+        ({"epi": 77}, "unknown epilogue"),
+        ({"lda": 8}, "lda"),
+        ({"ldb": 8}, "ldb"),
+        ({"ldc": 8}, "ldc"),
+        ({"batch": 0}, "invalid shape"),
+        ({"a": None}, "null operand"),
+        ({"splits": 4, "k": 4096, "lda": 4096}, "split-K needs"),
+        ({"layout": native.B_BLOCKED, "kpad": 80}, "multiple of 32"),
+        ({"layout": native.B_VNNI_PANELS, "panel": 64, "kpad": 32}, "does not cover"),
+        ({"trans_a": 1, "layout": native.B_BLOCKED, "kpad": 64}, "row-major A"),
+    ],
+)
+@no_device
+def test_gemm_refuses_bad_arguments(lib: ctypes.CDLL, kw: dict, message: str) -> None:
+    assert _gemm(lib, **kw) == native.ERR_INVALID
+    assert message in native.last_error()
+
+
+def _plan(lib: ctypes.CDLL, ab: int, m: int, n: int, k: int, batch: int = 1, splits: int = 0,
+          max_ws: int = -1, tiles: tuple[int, int, int] = (0, 0, 0)) -> tuple[int, int, int, int, int]:
+    outs = [ctypes.c_int() for _ in range(4)]
+    ws = ctypes.c_int64()
+    assert lib.hmx_gemm_plan(ab, m, n, k, batch, 0, 0, splits, max_ws, *tiles,
+                             *[ctypes.byref(o) for o in outs], ctypes.byref(ws)) == 0
+    return (*[o.value for o in outs], ws.value)
+
+
+def test_plans_of_the_baseline_configs(lib: ctypes.CDLL) -> None:
+    bf16, f32 = native.DTYPE_BF16, native.DTYPE_F32
+    # 4096^3 bf16: 256 tiles of 256 x 256 fill the 256 CUs, no split.
+    assert _plan(lib, bf16, 4096, 4096, 4096) == (1, 256, 256, 64, 0)
+    # Fused linear, 8192 x 11008 x 4096: 1376 tiles, no split.
+    assert _plan(lib, bf16, 8192, 11008, 4096) == (1, 256, 256, 64, 0)
+    # Split-K bmm [16, 256, 65536] @ [16, 65536, 256]: 64 tiles x 16 splits.
+    s, tm, tn, tk, ws = _plan(lib, f32, 256, 256, 65536, batch=16)
+    assert (s, tm, tn) == (16, 128, 128) and ws == 16 * 16 * 256 * 256 * 4
+    # The f32 512^3 plumbing case: 16 tiles, partials would cost more than they save.
+    assert _plan(lib, f32, 512, 512, 512)[0] == 1
+
+
+def test_plan_honours_requests_and_limits(lib: ctypes.CDLL) -> None:
+    bf16 = native.DTYPE_BF16
+    assert _plan(lib, bf16, 4096, 4096, 4096, tiles=(128, 128, 64))[1:4] == (128, 128, 64)
+    # A request below every tile gets the smallest.
+    assert _plan(lib, bf16, 4096, 4096, 4096, tiles=(64, 64, 64))[1:3] == (128, 128)
+    # Explicit splits, rounded to whole K tiles and no empty chunk.
+    s, *_, ws = _plan(lib, bf16, 256, 256, 1000, splits=3)
+    assert s == 3 and ws == 3 * 256 * 256 * 4
+    assert _plan(lib, bf16, 256, 256, 100, splits=8)[0] == 2  # 2 K tiles: 2 chunks
+    # The workspace limit stops the split.
+    assert _plan(lib, native.DTYPE_F32, 256, 256, 65536, batch=16, max_ws=0)[0] == 1
+
+
+@no_device
+def test_error_message_is_per_thread(lib: ctypes.CDLL) -> None:
+    import threading
+
+    assert lib.hmx_softmax_rows(7, 16, 16, 4, 4, None) == native.ERR_INVALID
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(native.last_error()))
+    t.start()
+    t.join()
+    assert seen == [""]
+    assert "unknown dtype" in native.last_error()

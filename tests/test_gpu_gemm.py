@@ -1,0 +1,294 @@
+"""Parity of the gfx950 GEMMs with the CPU oracle: bf16 and f32 ``matmul``
+(every transpose, ragged shapes, fused bias/scale/shift/activations), ``bmm``
+with deterministic split-K, ``linear`` / ``linear_affine``, the prepacked-B
+GEMMs over every packed layout, and the pack kernels (bit-exact).
+
+Tolerances (BASELINE): bf16-in / f32-accumulate rtol 1e-2 plus an atol scaled
+by sqrt(K) (``bf16_gemm_atol``); f32 rtol 1e-4, and the reference's own
+max-normalised error < 1e-5 for bmm (tests/test_cpu_utils_split_k_bmm.py:15-16).
+Full BASELINE sizes are checked on sampled rows / slices against the oracle.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import helion_mlir_utils as U
+import hmx_workloads as W
+from oracle import restate as R
+from tests.helpers import assert_close, bf16_gemm_atol, max_rel_error, tensor, to_np
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(7)
+ACTS = {"identity": U.identity_epilogue, "relu": torch.relu, "silu": F.silu, "sigmoid": torch.sigmoid,
+        "gelu": F.gelu, "gelu_tanh": U.Activation("gelu_tanh"), "tanh": torch.tanh,
+        "leaky_relu": U.Activation("leaky_relu", 0.2)}
+
+
+def _operands(m, n, k, trans_a, trans_b, dtype, device, scale=1.0):
+    a = tensor(RNG.normal(0, scale, (k, m) if trans_a else (m, k)).astype(np.float32), dtype, device)
+    b = tensor(RNG.normal(0, scale, (n, k) if trans_b else (k, n)).astype(np.float32), dtype, device)
+    return a, b
+
+
+def _check(got, ref, k, a, b, dtype):
+    if dtype == "f32":
+        assert_close(got, ref, 1e-4, 1e-5 * np.sqrt(k) * max(1.0, float(np.abs(ref).max()) * 1e-2))
+    else:
+        assert_close(got, ref, 1e-2, bf16_gemm_atol(k, a, b))
+
+
+@pytest.mark.parametrize("mnk", [(100, 100, 130), (33, 35, 66), (70, 40, 201), (20, 40, 50), (65, 372, 47),
+                                 (256, 256, 256), (512, 256, 128), (1, 1, 1), (300, 64, 128), (37, 45, 19)])
+@pytest.mark.parametrize(("trans_a", "trans_b"), [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_matmul_matches_oracle(gpu_device, mnk, trans_a, trans_b, dtype) -> None:
+    m, n, k = mnk
+    a, b = _operands(m, n, k, trans_a, trans_b, dtype, gpu_device)
+    got = to_np(U.matmul(a, b, trans_a=trans_a, trans_b=trans_b))
+    ref = R.matmul(to_np(a), to_np(b), trans_a, trans_b, out=dtype)
+    _check(got, ref, k, to_np(a), to_np(b), dtype)
+
+
+@pytest.mark.parametrize("act", list(ACTS))
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_matmul_fused_epilogues(gpu_device, act: str, dtype: str) -> None:
+    m, n, k = 200, 300, 256
+    a, b = _operands(m, n, k, False, True, dtype, gpu_device, 0.2)
+    bias, scale, shift = (tensor(RNG.normal(0, 1, n).astype(np.float32), dtype, gpu_device) for _ in range(3))
+    got = to_np(U.matmul(a, b, trans_b=True, bias=bias, scale=scale, shift=shift, epilogue=ACTS[act]))
+    arg = 0.2 if act == "leaky_relu" else 0.01
+    ref = R.matmul(to_np(a), to_np(b), False, True, to_np(bias), to_np(scale), to_np(shift), act, arg, out=dtype)
+    _check(got, ref, k, to_np(a), to_np(b), dtype)
+
+
+def test_matmul_scalar_affine_and_out_dtype(gpu_device) -> None:
+    m, n, k = 64, 96, 128
+    a, b = _operands(m, n, k, False, False, "bf16", gpu_device)
+    scale = torch.tensor([0.5], device=gpu_device, dtype=torch.bfloat16)
+    shift = torch.tensor([2.0], device=gpu_device, dtype=torch.bfloat16)
+    got = U.matmul(a, b, scale=scale, shift=shift, out_dtype=torch.float32)
+    assert got.dtype == torch.float32
+    ref = R.matmul(to_np(a), to_np(b), scale=np.float32(0.5), shift=np.float32(2.0))
+    assert_close(to_np(got), ref, 1e-5, 1e-4)
+
+
+def test_matmul_transposed_views_are_read_in_place(gpu_device) -> None:
+    a, b = _operands(96, 80, 64, False, False, "bf16", gpu_device)
+    at = a.t().contiguous().t()  # a view with strides (1, 96)
+    bt = b.t().contiguous().t()
+    got = to_np(U.matmul(at, bt))
+    ref = R.matmul(to_np(a), to_np(b), out="bf16")
+    _check(got, ref, 64, to_np(a), to_np(b), "bf16")
+
+
+@pytest.mark.parametrize("block_sizes", [(256, 256, 64), (128, 128, 64), (64, 64, 64)])
+def test_matmul_block_sizes_pick_the_tile(gpu_device, block_sizes) -> None:
+    a, b = _operands(300, 260, 200, False, False, "bf16", gpu_device)
+    got = to_np(U.matmul(a, b, block_sizes=block_sizes))
+    _check(got, R.matmul(to_np(a), to_np(b), out="bf16"), 200, to_np(a), to_np(b), "bf16")
+
+
+def test_matmul_config1_f32_512(gpu_device) -> None:
+    cfg = W.config1()
+    got = to_np(U.matmul(cfg["a"].to(gpu_device), cfg["b"].to(gpu_device), block_sizes=[64, 64, 64]))
+    ref = R.matmul(cfg["a"].numpy(), cfg["b"].numpy())
+    assert max_rel_error(got, ref) < 1e-5
+    f64 = cfg["a"].double().numpy() @ cfg["b"].double().numpy()
+    assert max_rel_error(got, f64) < 1e-5
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_matmul_config3_bf16_4096(gpu_device, out_dtype) -> None:
+    cfg = W.config3()
+    a, b = cfg["a"].to(gpu_device), cfg["b"].to(gpu_device)
+    c = U.matmul(a, b, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    rows = torch.from_numpy(np.sort(RNG.choice(4096, 96, replace=False)))
+    got = to_np(c[rows.to(gpu_device)])
+    an, bn = to_np(cfg["a"][rows]), to_np(cfg["b"])
+    ref = R.matmul(an, bn, out="bf16" if out_dtype == torch.bfloat16 else "f32")
+    _check(got, ref, 4096, an, bn, "bf16")
+
+
+def test_linear_config4_silu(gpu_device) -> None:
+    cfg = W.config4()
+    x, w, b = (cfg[k].to(gpu_device) for k in ("x", "w", "b"))
+    layer = torch.nn.Linear(4096, 11008, device=gpu_device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        layer.weight.copy_(w)
+        layer.bias.copy_(b)
+        y, cache = U.linear(x, layer, F.silu)
+        y2, cache2 = U.linear(x, layer, F.silu, cache=cache)
+    assert cache2.call is cache.call and torch.equal(y, y2)
+    torch.cuda.synchronize()
+    rows = torch.from_numpy(np.sort(RNG.choice(8192, 64, replace=False)))
+    got = to_np(y[rows.to(gpu_device)])
+    xn, wn, bn = to_np(cfg["x"][rows]), to_np(cfg["w"]), to_np(cfg["b"])
+    ref = R.matmul(xn, wn, False, True, bn, act="silu", out="bf16")
+    _check(got, ref, 4096, xn, wn, "bf16")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_linear_follows_weight_updates(gpu_device, dtype) -> None:
+    tdtype = torch.float32 if dtype == "f32" else torch.bfloat16
+    layer = torch.nn.Linear(128, 64).to(device=gpu_device, dtype=tdtype)
+    x = tensor(RNG.normal(0, 1, (32, 128)).astype(np.float32), dtype, gpu_device)
+    with torch.no_grad():
+        y, cache = U.linear(x, layer, torch.relu)
+        layer.weight.mul_(-1.0)
+        y3, cache3 = U.linear(x, layer, torch.relu, cache=cache)
+    assert cache3.packed_weight is not cache.packed_weight
+    ref = R.matmul(to_np(x), to_np(layer.weight), False, True, to_np(layer.bias), act="relu", out=dtype)
+    _check(to_np(y3), ref, 128, to_np(x), to_np(layer.weight), dtype)
+
+
+def test_linear_affine_and_panel(gpu_device) -> None:
+    layer = torch.nn.Linear(96, 70).to(device=gpu_device, dtype=torch.bfloat16)
+    x = tensor(RNG.normal(0, 1, (40, 96)).astype(np.float32), "bf16", gpu_device)
+    post_scale = tensor(RNG.uniform(0, 1, 70).astype(np.float32), "bf16", gpu_device)
+    post_bias = tensor(RNG.normal(0, 1, 1).astype(np.float32), "bf16", gpu_device)
+    with torch.no_grad():
+        y, _ = U.linear_affine(x, layer, post_scale, post_bias, torch.relu)
+        yp, cache = U.linear(x, layer, torch.relu, panel=64)
+    assert cache.packed_weight.dim() == 4
+    xs, ws, bs = to_np(x), to_np(layer.weight), to_np(layer.bias)
+    ref = R.matmul(xs, ws, False, True, bs, to_np(post_scale), to_np(post_bias), "relu", out="bf16")
+    _check(to_np(y), ref, 96, xs, ws, "bf16")
+    _check(to_np(yp), R.matmul(xs, ws, False, True, bs, act="relu", out="bf16"), 96, xs, ws, "bf16")
+
+
+# ---------------------------------------------------------------------------
+# bmm / split-K
+
+
+@pytest.mark.parametrize("shape", [(2, 160, 96, 224), (2, 65, 129, 129), (3, 100, 70, 130), (4, 64, 64, 8192),
+                                   (1, 33, 17, 40000)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_bmm_matches_oracle(gpu_device, shape, dtype) -> None:
+    batch, m, n, k = shape
+    a = tensor(RNG.uniform(-1, 1, (batch, m, k)).astype(np.float32), dtype, gpu_device)
+    b = tensor(RNG.uniform(-1, 1, (batch, k, n)).astype(np.float32), dtype, gpu_device)
+    got = to_np(U.bmm(a, b))
+    ref = R.bmm(to_np(a), to_np(b), out=dtype)
+    if dtype == "f32":
+        assert max_rel_error(got, ref) < 1e-5
+    else:
+        assert max_rel_error(got, ref) < 2e-2
+        assert_close(got, ref, 1e-2, bf16_gemm_atol(k, to_np(a), to_np(b)))
+
+
+@pytest.mark.parametrize("splits", [1, 2, 5, 16])
+def test_bmm_split_k_is_deterministic(gpu_device, splits) -> None:
+    a = tensor(RNG.uniform(-1, 1, (3, 64, 4096)).astype(np.float32), "f32", gpu_device)
+    b = tensor(RNG.uniform(-1, 1, (3, 4096, 96)).astype(np.float32), "f32", gpu_device)
+    first = U.bmm(a, b, splits=splits)
+    for _ in range(3):
+        assert torch.equal(U.bmm(a, b, splits=splits), first)
+    assert max_rel_error(to_np(first), R.bmm(to_np(a), to_np(b))) < 1e-5
+
+
+def test_bmm_rejects_mismatched_operands(gpu_device) -> None:
+    a = torch.randn(3, 64, 64, device=gpu_device)
+    with pytest.raises(RuntimeError, match="batch2"):
+        U.bmm(a, torch.randn(1, 64, 64, device=gpu_device))
+    with pytest.raises(RuntimeError, match="batch2"):
+        U.bmm(a, torch.randn(3, 32, 64, device=gpu_device))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_bmm_config5_full_size(gpu_device, dtype) -> None:
+    cfg = W.config5(torch.float32 if dtype == "f32" else torch.bfloat16)
+    a, b = cfg["a"].to(gpu_device), cfg["b"].to(gpu_device)
+    plan = U.gemm_plan(a.dtype, 256, 256, 65536, batch=16)
+    assert plan["splits"] >= 16
+    c = U.bmm(a, b, out_dtype=torch.float32)
+    c2 = U.bmm(a, b, out_dtype=torch.float32)
+    assert torch.equal(c, c2)
+    torch.cuda.synchronize()
+    for s in (0, 11):
+        got = to_np(c[s])
+        ref = R.bmm(to_np(cfg["a"][s]), to_np(cfg["b"][s]))
+        assert max_rel_error(got, ref) < (1e-5 if dtype == "f32" else 1e-5)
+
+
+# ---------------------------------------------------------------------------
+# Packing and prepacked GEMMs
+
+
+@pytest.mark.parametrize(("rows", "cols"), [(128, 96), (70, 45), (1, 1), (33, 64)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_pack_kernels_match_oracle(gpu_device, rows, cols, dtype) -> None:
+    x = tensor(RNG.normal(0, 1, (rows, cols)).astype(np.float32), dtype, gpu_device)
+    xs = to_np(x)
+    xt = x.t().contiguous()
+    np.testing.assert_array_equal(to_np(U.pack_a_blocked(x)), R.pack_a_blocked(xs))
+    np.testing.assert_array_equal(to_np(U.pack_a_blocked_t(xt)), R.pack_a_blocked(xs))
+    np.testing.assert_array_equal(to_np(U.pack_b_blocked(x)), R.pack_b_blocked(xs))
+    np.testing.assert_array_equal(to_np(U.pack_b_blocked_t(xt)), R.pack_b_blocked(xs))
+    np.testing.assert_array_equal(to_np(U.pack_b_blocked_vnni(x)), R.pack_b_blocked_vnni(xs))
+    np.testing.assert_array_equal(to_np(U.pack_b_blocked_vnni_t(xt)), R.pack_b_blocked_vnni(xs))
+    np.testing.assert_array_equal(to_np(U.pad_2d(x, rows + 3, cols + 5)), R.pad_2d(xs, rows + 3, cols + 5))
+    if cols % 2 == 0:  # x as a transposed weight [N, K], K even
+        np.testing.assert_array_equal(to_np(U.pack_b_vnni_t(x)), R.pack_b_vnni_t(xs))
+        np.testing.assert_array_equal(to_np(U.pack_b_vnni_t(x, 32)), R.pack_b_vnni_t(xs, 32))
+    if cols % 16 == 0:
+        np.testing.assert_array_equal(to_np(U.pack_b_panels(x, 16)), R.pack_b_panels(xs, 16))
+        np.testing.assert_array_equal(to_np(U.pack_a_panels(x, 16)), R.pack_a_panels(xs, 16))
+
+
+@pytest.mark.parametrize("mkn", [(64, 256, 128), (40, 66, 100), (64, 4096, 64), (300, 128, 64), (33, 64, 70)])
+@pytest.mark.parametrize("panel", [64, 128])
+def test_matmul_prepacked_vnni(gpu_device, mkn, panel) -> None:
+    m, k, n = mkn
+    a = tensor(RNG.normal(0, 1, (m, k)).astype(np.float32), "bf16", gpu_device)
+    w = tensor(RNG.normal(0, 1, (n, k)).astype(np.float32), "bf16", gpu_device)
+    bias = tensor(RNG.normal(0, 1, n).astype(np.float32), "bf16", gpu_device)
+    got = to_np(U.matmul_prepacked_b(a, U.pack_b_vnni_t(w, panel), n, bias, torch.relu))
+    ref = R.matmul(to_np(a), to_np(w), False, True, to_np(bias), act="relu", out="bf16")
+    _check(got, ref, k, to_np(a), to_np(w), "bf16")
+
+
+@pytest.mark.parametrize("mkn", [(64, 256, 96), (33, 256, 64), (130, 96, 70), (17, 64, 32), (40, 100, 64)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_matmul_prepacked_blocked(gpu_device, mkn, dtype) -> None:
+    m, k, n = mkn
+    a = tensor(RNG.normal(0, 1, (m, k)).astype(np.float32), dtype, gpu_device)
+    w = tensor(RNG.normal(0, 1, (n, k)).astype(np.float32), dtype, gpu_device)
+    bias = tensor(RNG.normal(0, 1, n).astype(np.float32), dtype, gpu_device)
+    ref = R.matmul(to_np(a), to_np(w), False, True, to_np(bias), act="relu", out=dtype)
+    got = to_np(U.matmul_prepacked_b(a, U.pack_b_blocked_t(w), n, bias, torch.relu))
+    _check(got, ref, k, to_np(a), to_np(w), dtype)
+    call = U.prepacked_b_call(a, U.pack_b_blocked_t(w), n, bias, torch.relu)
+    _check(to_np(call(a)), ref, k, to_np(a), to_np(w), dtype)
+    if dtype == "bf16":
+        got = to_np(U.matmul_prepacked_b(a, U.pack_b_blocked_vnni_t(w), n, bias, torch.relu))
+        _check(got, ref, k, to_np(a), to_np(w), dtype)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_matmul_bench_panels(gpu_device, dtype) -> None:
+    m, k, n = 96, 192, 256
+    a = tensor(RNG.uniform(-1, 1, (m, k)).astype(np.float32), dtype, gpu_device)
+    b = tensor(RNG.uniform(-1, 1, (k, n)).astype(np.float32), dtype, gpu_device)
+    if dtype == "f32":
+        with pytest.raises(ValueError):
+            U.matmul_prepacked_b(a, U.pack_b_panels(b, 64), n)
+        return
+    got = to_np(U.matmul_prepacked_b(a, U.pack_b_panels(b, 64), n))
+    _check(got, R.matmul(to_np(a), to_np(b), out=dtype), k, to_np(a), to_np(b), dtype)
+
+
+def test_matmul_config3_prepacked_layouts(gpu_device) -> None:
+    cfg = W.config3(scale=4)  # 1024^3, the config-3 distribution
+    a, b = cfg["a"].to(gpu_device), cfg["b"].to(gpu_device)
+    plain = U.matmul(a, b)
+    bt = b.t().contiguous()
+    for packed in (U.pack_b_blocked_vnni(b), U.pack_b_vnni_t(bt, 256), U.pack_b_panels(b, 256), U.pack_b_blocked(b)):
+        got = U.matmul_prepacked_b(a, packed, 1024)
+        # The same products summed in the same K order: bit-equal to the plain kernel.
+        assert torch.equal(got, plain)
