@@ -307,6 +307,30 @@ class MatmulF32(Workload):
                 "sample": f"oracle.restate.matmul 512^3 f32, {reps} reps, {_cpu_model()}"}
 
 
+class Copy(Workload):
+    """A plain device copy of known size (torch's copy kernel): the calibration
+    point for the rocprofv3 FETCH_SIZE / WRITE_SIZE counters, not a hot-path op."""
+
+    def __init__(self, device) -> None:
+        import torch
+
+        self.x = torch.empty((32768, 8192), dtype=torch.bfloat16, device=device).fill_(1.0)
+        self.y = torch.empty_like(self.x)
+        self.name = "copy"
+        self.description = "device copy of 512 MiB (counter calibration)"
+        self.unit, self.bound, self.peak = "GB/s", "hbm", PEAK_HBM_GBS
+        self.work = 2.0 * self.x.numel() * 2
+        self.dtype = "bf16"
+        self.kernel = "copy"
+        self.config = {"workload": self.description, "bytes_read": self.x.numel() * 2, "bytes_written": self.x.numel() * 2}
+
+    def step(self):
+        return self.y.copy_(self.x)
+
+    def cpu_baseline(self) -> dict:
+        return {"value": None, "unit": "GB/s", "cores": 0, "kind": "port", "sample": "none (calibration workload)"}
+
+
 def make(name: str, device) -> Workload:
     return {
         "gemm": lambda: Gemm(device),
@@ -320,6 +344,7 @@ def make(name: str, device) -> Workload:
         "bmm": lambda: Bmm(device, "f32"),
         "bmm_bf16": lambda: Bmm(device, "bf16"),
         "matmul_f32": lambda: MatmulF32(device),
+        "copy": lambda: Copy(device),
     }[name]()
 
 

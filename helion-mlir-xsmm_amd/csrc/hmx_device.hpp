@@ -17,17 +17,19 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
   return __uint_as_float(h << 16);
 }
 
-// Round-to-nearest-even f32 -> bf16, NaN kept quiet (the rounding torch's
-// `.to(torch.bfloat16)` performs).
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two f32 -> packed bf16 (lo in bits 0-15) with one v_cvt_pk_bf16_f32:
+// round to nearest even, NaN kept NaN -- the rounding of torch's
+// `.to(torch.bfloat16)`.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const bf16x2_t v = __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t);
+  return __builtin_bit_cast(uint32_t, v);
 }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  return pack_bf16x2(f, 0.f) & 0xffffu;
 }
 
 // Element access by storage type: float or bf16 (uint16_t bits).
@@ -90,9 +92,16 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+constexpr float kLog2e = 1.4426950408889634f;
+
 // exp through the hardware base-2 exponential.
 __device__ __forceinline__ float fast_exp(float x) {
-  return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+  return __builtin_amdgcn_exp2f(x * kLog2e);
+}
+
+// exp(x - m) given ml = m * log2(e): one FMA and one v_exp_f32.
+__device__ __forceinline__ float exp_shifted(float x, float ml) {
+  return __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2e, -ml));
 }
 
 // The activations a fused epilogue may apply to an f32 value, codes as in

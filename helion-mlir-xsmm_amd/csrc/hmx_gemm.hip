@@ -50,7 +50,21 @@ struct Operand {
   int64_t panel;   // panel width (panel layouts)
   int64_t kpad;    // padded K (packed layouts)
   bool vec;        // 16-byte loads allowed (alignment of base and lines)
+  int32_t bytes;   // extent of one batch slice in bytes (buffer loads; < 2^31)
 };
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// A buffer resource over one operand slice: loads past `bytes` return zeros
+// instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, int32_t voff, int32_t soff) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
 
 template <int L>
 __device__ __forceinline__ int64_t offset_of(const Operand& o, int64_t r, int64_t k) {
@@ -104,6 +118,44 @@ struct Bf16Loader {
     }
     return make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
                       h[6] | (h[7] << 16));
+  }
+
+  // Whole tiles (no guard): buffer loads, whose offsets split into one
+  // per-thread VGPR and a uniform SGPR part for row-major layouts.
+  __device__ __forceinline__ void load_whole(__amdgpu_buffer_rsrc_t rsrc, const Operand& o,
+                                             int64_t r0, int64_t k0, int tid) {
+    constexpr int KV = BK / 8;  // 16-byte vectors per K tile row
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int item = i * NT + tid;
+      if (ITEMS < NT && item >= ITEMS) break;
+      if constexpr (L == L_KCONTIG) {
+        const int32_t voff = (int32_t)(((item / KV) - i * (NT / KV)) * o.ld + (item % KV) * 8) * 2;
+        const int32_t soff = (int32_t)(((r0 + i * (NT / KV)) * o.ld + k0) * 2);
+        r[i][0] = buffer_load16(rsrc, voff, soff);
+      } else if constexpr (L == L_RCONTIG) {
+        const int kb = item % KV;
+        const int rb = item / KV;
+        const int32_t voff = (int32_t)((kb * 8) * o.ld + (rb - i * (NT / KV)) * 8) * 2;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          const int32_t soff = (int32_t)(((k0 + kk) * o.ld + r0 + i * (NT / KV) * 8) * 2);
+          r[i][kk] = buffer_load16(rsrc, voff, soff);
+        }
+      } else if constexpr (KIND == 1) {
+        const int64_t k = k0 + (item % KV) * 8;
+        const int64_t row = r0 + (item / KV) * 8;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+          r[i][kk] = buffer_load16(rsrc, (int32_t)(offset_of<L>(o, row, k + kk) * 2), 0);
+      } else {
+        const int64_t k = k0 + (item % KV) * 8;
+        const int64_t row = r0 + (item / KV) * 4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          r[i][q] = buffer_load16(rsrc, (int32_t)(offset_of<L>(o, row, k + 2 * q) * 2), 0);
+      }
+    }
   }
 
   __device__ __forceinline__ void load(const Operand& o, int64_t r0, int64_t k0, int64_t k_end,
@@ -246,8 +298,80 @@ __device__ __forceinline__ void column_vectors(const GemmArgs& g, int64_t col, b
 template <int WN>
 constexpr int epi_pitch() { return WN + 8; }
 
+// Activation classes compiled into the register epilogue.
+enum : int { ACT_ID = 0, ACT_RELU = 1, ACT_SILU = 2 };
+
+template <int ACT>
+__device__ __forceinline__ float activate(float v) {
+  if constexpr (ACT == ACT_RELU) return apply_activation(HMX_EPI_RELU, v, 0.f);
+  if constexpr (ACT == ACT_SILU) return apply_activation(HMX_EPI_SILU, v, 0.f);
+  return v;
+}
+
+// Exchange with the neighbouring lane (lane ^ 1) through DPP, no LDS.
+__device__ __forceinline__ float swap_pair(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1 /* quad_perm [1,0,3,2] */, 0xF, 0xF, false));
+}
+
+// Register epilogue: each lane finishes its own accumulators (column
+// lane % 32 of each fragment: bias, scale, shift, activation) and stores them
+// directly. bf16 pairs: rows r and r + 1 of adjacent columns are exchanged
+// between lanes 2c and 2c + 1, so every lane writes one 4-byte word (two
+// columns of one row); f32 lanes write their own 4-byte values.
+template <int FM, int FN, int WM, int WN, bool GUARD, int ACT, bool BF16>
+__device__ __forceinline__ void epilogue_direct(const GemmArgs& g, int split, int batch, int64_t m0,
+                                                int64_t n0, int wm, int wn, int lane, bool pair_ok,
+                                                const f32x16_t (&acc)[FM][FN]) {
+  const int64_t off = split * g.stride_split + batch * g.stride_c;
+  const bool odd = lane & 1;
+  (void)pair_ok;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int64_t col = n0 + wn * WN + j * 32 + (lane & 31);
+    const bool col_in = !GUARD || col < g.n;
+    float bias, scale, shift;
+    column_vectors(g, col, col_in, bias, scale, shift);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int64_t row0 = m0 + wm * WM + i * 32 + 4 * (lane >> 5);
+      if constexpr (BF16) {
+        uint16_t* c = (uint16_t*)g.c + off;
+        if constexpr (!GUARD) {
+          // Whole tile: 4-byte stores of column pairs.
+          const int64_t pcol = col & ~(int64_t)1;
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const int e0 = 2 * q, e1 = 2 * q + 1;
+            const float v0 = activate<ACT>((acc[i][j][e0] + bias) * scale + shift);
+            const float v1 = activate<ACT>((acc[i][j][e1] + bias) * scale + shift);
+            const float recv = swap_pair(odd ? v0 : v1);
+            const int64_t row = row0 + 8 * (e0 >> 2) + (e0 & 3) + (odd ? 1 : 0);
+            *(uint32_t*)(c + row * g.ldc + pcol) = odd ? pack_bf16x2(recv, v1) : pack_bf16x2(v0, recv);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int64_t row = row0 + 8 * (e >> 2) + (e & 3);
+            const float v = activate<ACT>((acc[i][j][e] + bias) * scale + shift);
+            if (col_in && row < g.m) c[row * g.ldc + col] = (uint16_t)f32_to_bf16_bits(v);
+          }
+        }
+      } else {
+        float* c = (float*)g.c + off;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int64_t row = row0 + 8 * (e >> 2) + (e & 3);
+          const float v = activate<ACT>((acc[i][j][e] + bias) * scale + shift);
+          if (!GUARD || (col_in && row < g.m)) c[row * g.ldc + col] = v;
+        }
+      }
+    }
+  }
+}
+
 template <int FM, int FN, int WM, int WN, bool GUARD>
-__device__ __forceinline__ void epilogue(const GemmArgs& g, float* lds, int split, int batch,
+__device__ __forceinline__ void epilogue_staged(const GemmArgs& g, float* lds, int split, int batch,
                                          int64_t m0, int64_t n0, int wm, int wn, int wave,
                                          int lane, const f32x16_t (&acc)[FM][FN]) {
   constexpr int P = epi_pitch<WN>();
@@ -300,6 +424,80 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, float* lds, int spli
   }
 }
 
+#ifndef HMX_GEMM_SCHED
+#define HMX_GEMM_SCHED 1
+#endif
+
+// Instruction-class masks of __builtin_amdgcn_sched_group_barrier.
+enum : int { SG_VALU = 0x002, SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100, SG_DS_WRITE = 0x200 };
+
+// The order one K step's instructions issue in: the first fragment reads,
+// then every MFMA paired with one other instruction -- the next K slice's
+// fragment reads, the next-next tile's buffer loads, and the register
+// transposes and LDS writes of the next tile -- so that the matrix core
+// never waits on an LDS or memory instruction issued just before it.
+template <int FM, int FN, int BK, int LOADS, int WRITES, int PERMS>
+__device__ __forceinline__ void schedule_k_step() {
+#if HMX_GEMM_SCHED
+  constexpr int KS = BK / 16, MF = FM * FN, RD = FM + FN;
+  constexpr int TOTAL = KS * MF;
+  __builtin_amdgcn_sched_group_barrier(SG_DS_READ, RD, 0);
+  int loads = LOADS, writes = WRITES, perms = PERMS;
+#pragma unroll
+  for (int i = 0; i < TOTAL; ++i) {
+    const int ks = i / MF, m = i % MF;
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+    if (ks + 1 < KS && m < RD) {
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+    } else if (HMX_GEMM_SCHED > 1 && loads > 0 && i < TOTAL / 2) {
+      __builtin_amdgcn_sched_group_barrier(SG_VMEM_READ, 1, 0);
+      --loads;
+    } else if (i >= TOTAL / 2) {
+      if (perms > 0) {
+        __builtin_amdgcn_sched_group_barrier(SG_VALU, 2, 0);
+        perms -= 2;
+      }
+      if (writes > 0) {
+        __builtin_amdgcn_sched_group_barrier(SG_DS_WRITE, 1, 0);
+        --writes;
+      }
+    }
+  }
+#endif
+}
+
+// Epilogue dispatch: identity, ReLU and SiLU store from registers; other
+// activations go through the LDS-staged path.
+template <int FM, int FN, int WM, int WN, bool GUARD>
+__device__ __forceinline__ void epilogue(const GemmArgs& g, float* lds, int split, int batch,
+                                         int64_t m0, int64_t n0, int wm, int wn, int wave,
+                                         int lane, const f32x16_t (&acc)[FM][FN]) {
+  const bool bf16 = g.c_dtype == HMX_DTYPE_BF16;
+  const int64_t off = split * g.stride_split + batch * g.stride_c;
+  const bool pair_ok = (g.ldc % 2 == 0) && (off % 2 == 0) && ((((uintptr_t)g.c) & 3) == 0);
+#define HMX_DIRECT(ACT)                                                                          \
+  do {                                                                                           \
+    if (bf16)                                                                                    \
+      epilogue_direct<FM, FN, WM, WN, GUARD, ACT, true>(g, split, batch, m0, n0, wm, wn, lane,   \
+                                                         pair_ok, acc);                          \
+    else                                                                                         \
+      epilogue_direct<FM, FN, WM, WN, GUARD, ACT, false>(g, split, batch, m0, n0, wm, wn, lane,  \
+                                                          pair_ok, acc);                         \
+  } while (0)
+  if (!GUARD && !pair_ok && bf16) {
+    epilogue_staged<FM, FN, WM, WN, GUARD>(g, lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
+    return;
+  }
+  switch (g.act) {
+    case HMX_EPI_IDENTITY: HMX_DIRECT(ACT_ID); break;
+    case HMX_EPI_RELU: HMX_DIRECT(ACT_RELU); break;
+    case HMX_EPI_SILU: HMX_DIRECT(ACT_SILU); break;
+    default:
+      epilogue_staged<FM, FN, WM, WN, GUARD>(g, lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
+  }
+#undef HMX_DIRECT
+}
+
 template <int BM_, int BN_, int BK_>
 struct Bf16Cfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_;
@@ -333,8 +531,10 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm_bf16_kernel(GemmArgs g) {
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  Bf16Loader<BM, BK, NT, LA, GUARD> la;
-  Bf16Loader<BN, BK, NT, LB, GUARD> lb;
+  // Two register staging sets: tile t + 2's global loads are issued while
+  // tile t is multiplied, so each load has two K steps to arrive.
+  Bf16Loader<BM, BK, NT, LA, GUARD> la0, la1;
+  Bf16Loader<BN, BK, NT, LB, GUARD> lb0, lb1;
 
   f32x16_t acc[FM][FN];
 #pragma unroll
@@ -345,25 +545,33 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm_bf16_kernel(GemmArgs g) {
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   const int ktiles = (int)((k_end - k_begin + BK - 1) / BK);
+  // K offset of tile t, clamped to the last tile: the loads past the end
+  // re-read it, in bounds, so the loop needs no conditional loads.
+  auto k_of = [&](int t) { return k_begin + (int64_t)min(t, ktiles - 1) * BK; };
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.p, a.bytes);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(b.p, b.bytes);
+  auto fetch = [&](auto& ld_a, auto& ld_b, int t) {
+    if constexpr (GUARD) {
+      ld_a.load(a, m0, k_of(t), k_end, tid);
+      ld_b.load(b, n0, k_of(t), k_end, tid);
+    } else {
+      ld_a.load_whole(ra, a, m0, k_of(t), tid);
+      ld_b.load_whole(rb, b, n0, k_of(t), tid);
+    }
+  };
   if (ktiles > 0) {
-    la.load(a, m0, k_begin, k_end, tid);
-    lb.load(b, n0, k_begin, k_end, tid);
-    la.store(lds, tid);
-    lb.store(lds + BM * PITCH, tid);
+    fetch(la0, lb0, 0);
+    fetch(la1, lb1, 1);
+    la0.store(lds, tid);
+    lb0.store(lds + BM * PITCH, tid);
   }
   __syncthreads();
 
   // Fragment read offsets: row lane % 32 of the fragment, K half lane / 32.
   const int frag_row = lane & 31, frag_k = (lane >> 5) * 8;
-  for (int kt = 0; kt < ktiles; ++kt) {
-    const int cur = kt & 1;
-    // Prefetch the next K tile (the last iteration re-reads its own, in
-    // bounds): unconditional, so the staging registers stay registers.
-    const int64_t kn = k_begin + (int64_t)min(kt + 1, ktiles - 1) * BK;
-    la.load(a, m0, kn, k_end, tid);
-    lb.load(b, n0, kn, k_end, tid);
-    const uint16_t* As = lds + cur * STAGE + (wm * Cfg::WM + frag_row) * PITCH + frag_k;
-    const uint16_t* Bs = lds + cur * STAGE + BM * PITCH + (wn * Cfg::WN + frag_row) * PITCH + frag_k;
+  auto multiply = [&](const uint16_t* stage) {
+    const uint16_t* As = stage + (wm * Cfg::WM + frag_row) * PITCH + frag_k;
+    const uint16_t* Bs = stage + BM * PITCH + (wn * Cfg::WN + frag_row) * PITCH + frag_k;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8_t af[FM], bfr[FN];
@@ -377,8 +585,46 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm_bf16_kernel(GemmArgs g) {
         for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
-    la.store(lds + (cur ^ 1) * STAGE, tid);
-    lb.store(lds + (cur ^ 1) * STAGE + BM * PITCH, tid);
+  };
+  uint16_t* const stage0 = lds;
+  uint16_t* const stage1 = lds + STAGE;
+  using LoadA = Bf16Loader<BM, BK, NT, LA, GUARD>;
+  using LoadB = Bf16Loader<BN, BK, NT, LB, GUARD>;
+  constexpr int kLoads = LoadA::PER_THREAD * LoadA::REGS + LoadB::PER_THREAD * LoadB::REGS;
+  constexpr int kWrites = LoadA::PER_THREAD * (LoadA::KIND == 0 ? 1 : LoadA::KIND == 1 ? 8 : 4) +
+                          LoadB::PER_THREAD * (LoadB::KIND == 0 ? 1 : LoadB::KIND == 1 ? 8 : 4);
+  constexpr int kPerms = (LoadA::KIND == 1 ? LoadA::PER_THREAD * 32 : 0) +
+                         (LoadB::KIND == 1 ? LoadB::PER_THREAD * 32 : 0);
+  int kt = 0;
+  for (; kt + 2 <= ktiles; kt += 2) {
+    // Even step: tile kt from stage 0; tile kt + 1 (set 1) goes to stage 1.
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(la0, lb0, kt + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    multiply(stage0);
+#if !HMX_GEMM_SCHED
+    __builtin_amdgcn_sched_barrier(0);
+#endif
+    la1.store(stage1, tid);
+    lb1.store(stage1 + BM * PITCH, tid);
+    schedule_k_step<FM, FN, BK, kLoads, kWrites, kPerms>();
+    __syncthreads();
+    // Odd step: tile kt + 1 from stage 1; tile kt + 2 (set 0) goes to stage 0.
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(la1, lb1, kt + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    multiply(stage1);
+#if !HMX_GEMM_SCHED
+    __builtin_amdgcn_sched_barrier(0);
+#endif
+    la0.store(stage0, tid);
+    lb0.store(stage0 + BM * PITCH, tid);
+    schedule_k_step<FM, FN, BK, kLoads, kWrites, kPerms>();
+    __syncthreads();
+  }
+  // An odd tile count leaves the last tile in stage 0.
+  if (kt < ktiles) {
+    multiply(stage0);
     __syncthreads();
   }
 
@@ -592,7 +838,15 @@ struct Plan {
   int splits;
   int64_t k_chunk;
   int64_t workspace_bytes;
+  // Row-major bf16 B is first transposed to [N, K] in the workspace (at
+  // offset 0, bt_bytes long) when enough output rows reuse it: the K-contiguous
+  // kernel path then reads it without register transposes.
+  bool transpose_b;
+  int64_t bt_bytes;
 };
+
+// Output rows from which a row-major bf16 B is transposed once up front.
+constexpr int64_t kTransposeMinRows = 512;
 
 int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int b_layout,
               int splits, int64_t max_ws, int tile_m, int tile_n, int tile_k, Plan& plan) {
@@ -645,7 +899,13 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
     plan.k_chunk = k;
   }
   plan.splits = splits;
-  plan.workspace_bytes = splits > 1 ? (int64_t)splits * batch * m * n * 4 : 0;
+  const int64_t partial_bytes = splits > 1 ? (int64_t)splits * batch * m * n * 4 : 0;
+  plan.bt_bytes = ceil_div(n * k * 2, 256) * 256;
+  plan.transpose_b = bf16 && b_layout == HMX_B_ROW && batch == 1 && m >= kTransposeMinRows &&
+                     n * k * 2 < INT32_MAX &&
+                     (max_ws < 0 || plan.bt_bytes + partial_bytes <= max_ws);
+  if (!plan.transpose_b) plan.bt_bytes = 0;
+  plan.workspace_bytes = plan.bt_bytes + partial_bytes;
   return HMX_OK;
 }
 
@@ -783,6 +1043,17 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
                 "gemm: split-K needs %lld workspace bytes, got %lld",
                 (long long)plan.workspace_bytes, (long long)workspace_bytes);
   }
+  void* partials = workspace ? (char*)workspace + plan.bt_bytes : nullptr;
+  int lb_run = lb;
+  if (plan.transpose_b) {
+    // B [K, N] -> B^T [N, K] in the workspace; the GEMM then reads it K-contiguous.
+    launch_transpose16(b, workspace, k, n, ldb, (hipStream_t)stream);
+    const int st = check_launch("gemm B transpose");
+    if (st != HMX_OK) return st;
+    b = workspace;
+    ldb = k;
+    lb_run = L_KCONTIG;
+  }
   const int64_t tiles_m = ceil_div(m, plan.tile.bm), tiles_n = ceil_div(n, plan.tile.bn);
   HMX_REQUIRE(tiles_m * tiles_n < ((int64_t)1 << 31) && batch < 65536 && plan.splits < 65536,
               "gemm: grid too large");
@@ -791,14 +1062,23 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
   const int64_t vec_elems = 16 / esz;
   GemmArgs g{};
   const int la = trans_a ? L_RCONTIG : L_KCONTIG;
-  g.a = Operand{a, lda, m, 0, 0, aligned16(a) && lda % vec_elems == 0 &&
-                                     (batch == 1 || stride_a % vec_elems == 0)};
+  g.a = Operand{a, lda, m, 0, 0,
+                aligned16(a) && lda % vec_elems == 0 && (batch == 1 || stride_a % vec_elems == 0), 0};
   const int64_t b_rows = packed ? (lb == L_BLOCKED_VNNI || lb == L_BLOCKED ? ceil_div(n, 32) * 32
                                                                            : ceil_div(n, b_panel) * b_panel)
                                 : n;
   g.b = Operand{b, ldb, b_rows, b_panel, b_kpad,
                 aligned16(b) && (packed || ldb % vec_elems == 0) &&
-                    (batch == 1 || stride_b % vec_elems == 0)};
+                    (batch == 1 || stride_b % vec_elems == 0),
+                0};
+  // Bytes spanned by one batch slice of each operand: the buffer-load
+  // range of the whole-tile path, which needs it below 2^31.
+  const int64_t a_bytes = (trans_a ? (k - 1) * lda + m : (m - 1) * lda + k) * esz;
+  const int64_t b_bytes =
+      packed ? b_rows * b_kpad * esz : (lb_run == L_RCONTIG ? (k - 1) * ldb + n : (n - 1) * ldb + k) * esz;
+  const bool bytes_ok = a_bytes < INT32_MAX && b_bytes < INT32_MAX;
+  g.a.bytes = bytes_ok ? (int32_t)a_bytes : 0;
+  g.b.bytes = bytes_ok ? (int32_t)b_bytes : 0;
   // Packed layouts read zeros (their padding) past N up to the padded extent;
   // columns past N are never stored.
   g.stride_a = stride_a;
@@ -816,7 +1096,7 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
   g.act = epilogue;
   g.act_arg = epilogue_arg;
   if (plan.splits > 1) {
-    g.c = workspace;
+    g.c = partials;
     g.c_dtype = HMX_DTYPE_F32;
     g.ldc = n;
     g.stride_c = m * n;
@@ -833,15 +1113,15 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
 
   const bool whole = m % plan.tile.bm == 0 && n % plan.tile.bn == 0 &&
                      plan.k_chunk % plan.tile.bk == 0 && k % plan.tile.bk == 0;
-  const bool guard = !(whole && g.a.vec && g.b.vec);
+  const bool guard = !(whole && g.a.vec && g.b.vec && bytes_ok);
   const dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)plan.splits, (unsigned)batch);
   auto s = (hipStream_t)stream;
   if (ab_dtype == HMX_DTYPE_BF16) {
     const TileChoice t = plan.tile;
     if (t.bm == 256)
-      dispatch_bf16<Bf16Cfg<256, 256, 64>>(g, la, lb, guard, grid, s);
+      dispatch_bf16<Bf16Cfg<256, 256, 64>>(g, la, lb_run, guard, grid, s);
     else
-      dispatch_bf16<Bf16Cfg<128, 128, 64>>(g, la, lb, guard, grid, s);
+      dispatch_bf16<Bf16Cfg<128, 128, 64>>(g, la, lb_run, guard, grid, s);
   } else {
     dispatch_f32<F32Cfg<128, 128, 32>>(g, la, lb, guard, grid, s);
   }
@@ -859,7 +1139,7 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
   r.act = epilogue;
   const int64_t total = batch * m * n;
   const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(total, 256), 16384);
-  splitk_reduce_kernel<<<blocks, 256, 0, s>>>((const float*)workspace, plan.splits, batch, r);
+  splitk_reduce_kernel<<<blocks, 256, 0, s>>>((const float*)partials, plan.splits, batch, r);
   return check_launch("gemm split-K reduce");
 }
 

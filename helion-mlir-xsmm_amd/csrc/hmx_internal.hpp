@@ -19,6 +19,11 @@ void clear_error();
 // The HIP error of the last launch on this thread, as an hmx status.
 int check_launch(const char* what);
 
+// Enqueues dst[c, r] = src[r, c] for 16-bit elements, src [rows, cols] with
+// row stride ld, dst [cols, rows] contiguous (hmx_pack.hip).
+void launch_transpose16(const void* src, void* dst, int64_t rows, int64_t cols, int64_t ld,
+                        hipStream_t stream);
+
 inline bool valid_dtype(int dtype) {
   return dtype == HMX_DTYPE_F32 || dtype == HMX_DTYPE_BF16;
 }

@@ -94,12 +94,68 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
   }
 }
 
+// Transpose of 16-bit elements, [rows, cols] (row stride ld) -> [cols, rows]
+// contiguous. Each lane moves an 8 x 8 block: eight 16-byte row loads, a
+// register transpose (v_perm_b32), eight 16-byte stores; a wave covers a
+// 64 x 64 tile with 128-byte segments on both sides. Edge blocks go element
+// by element.
+__device__ __forceinline__ uint32_t lo_pair(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t hi_pair(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x07060302u);
+}
+__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+__global__ __launch_bounds__(256) void transpose16_kernel(const uint16_t* __restrict__ src,
+                                                          uint16_t* __restrict__ dst, int64_t rows,
+                                                          int64_t cols, int64_t ld, bool vec) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r0 = (int64_t)blockIdx.y * 64 + (lane & 7) * 8;
+  const int64_t c0 = ((int64_t)blockIdx.x * 4 + wave) * 64 + (lane >> 3) * 8;
+  if (r0 >= rows || c0 >= cols) return;
+  uint4 in[8];
+  const bool whole = vec && r0 + 8 <= rows && c0 + 8 <= cols;
+  if (whole) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) in[k] = *(const uint4*)(src + (r0 + k) * ld + c0);
+    // Output row j (source column c0 + j) holds source rows r0..r0+7.
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint4 o;
+      const int d = j >> 1;
+      if (j & 1) {
+        o = make_uint4(hi_pair(word(in[0], d), word(in[1], d)), hi_pair(word(in[2], d), word(in[3], d)),
+                       hi_pair(word(in[4], d), word(in[5], d)), hi_pair(word(in[6], d), word(in[7], d)));
+      } else {
+        o = make_uint4(lo_pair(word(in[0], d), word(in[1], d)), lo_pair(word(in[2], d), word(in[3], d)),
+                       lo_pair(word(in[4], d), word(in[5], d)), lo_pair(word(in[6], d), word(in[7], d)));
+      }
+      *(uint4*)(dst + (c0 + j) * rows + r0) = o;
+    }
+  } else {
+    for (int j = 0; j < 8 && c0 + j < cols; ++j)
+      for (int k = 0; k < 8 && r0 + k < rows; ++k) dst[(c0 + j) * rows + r0 + k] = src[(r0 + k) * ld + c0 + j];
+  }
+}
+
 bool is_transposed(int kind) {
   return kind == HMX_PACK_A_BLOCKED_T || kind == HMX_PACK_B_BLOCKED_T ||
-         kind == HMX_PACK_B_BLOCKED_VNNI_T || kind == HMX_PACK_B_VNNI_PANELS_T;
+         kind == HMX_PACK_B_BLOCKED_VNNI_T || kind == HMX_PACK_B_VNNI_PANELS_T ||
+         kind == HMX_PACK_TRANSPOSE;
 }
 
 }  // namespace
+
+void launch_transpose16(const void* src, void* dst, int64_t rows, int64_t cols, int64_t ld,
+                        hipStream_t stream) {
+  const bool vec = aligned16(src) && aligned16(dst) && ld % 8 == 0 && rows % 8 == 0;
+  const dim3 grid((unsigned)ceil_div(cols, 256), (unsigned)ceil_div(rows, 64));
+  transpose16_kernel<<<grid, 256, 0, stream>>>((const uint16_t*)src, (uint16_t*)dst, rows, cols, ld, vec);
+}
+
 }  // namespace hmx
 
 using namespace hmx;
@@ -108,7 +164,7 @@ extern "C" int hmx_pack(int kind, int dtype, const void* src, int64_t rows, int6
                         int64_t ld, void* dst, int64_t rows_pad, int64_t cols_pad,
                         int64_t panel, void* stream) {
   HMX_REQUIRE(valid_dtype(dtype), "pack: unknown dtype %d", dtype);
-  HMX_REQUIRE(kind >= HMX_PACK_PAD && kind <= HMX_PACK_A_PANELS, "pack: unknown kind %d", kind);
+  HMX_REQUIRE(kind >= HMX_PACK_PAD && kind <= HMX_PACK_TRANSPOSE, "pack: unknown kind %d", kind);
   HMX_REQUIRE(rows >= 0 && cols >= 0 && rows_pad >= 0 && cols_pad >= 0, "pack: invalid shape");
   HMX_REQUIRE(src && dst, "pack: null operand");
   HMX_REQUIRE(ld >= cols, "pack: ld %lld smaller than %lld columns", (long long)ld, (long long)cols);
@@ -140,6 +196,11 @@ extern "C" int hmx_pack(int kind, int dtype, const void* src, int64_t rows, int6
              rows_pad * cols_pad, kind, t};
   if (a.total == 0) return HMX_OK;
   auto s = (hipStream_t)stream;
+  if (kind == HMX_PACK_TRANSPOSE && dtype == HMX_DTYPE_BF16 && rows_pad == lrows &&
+      cols_pad == lcols && rows > 0 && cols > 0) {
+    launch_transpose16(src, dst, rows, cols, ld, s);
+    return check_launch("pack transpose");
+  }
   const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(a.total, 256), 65536);
   if (dtype == HMX_DTYPE_BF16)
     pack_kernel<uint16_t><<<blocks, 256, 0, s>>>(a);

@@ -117,6 +117,26 @@ __device__ __forceinline__ void load_f32_run(const float* __restrict__ p, int64_
   for (int e = 0; e < EPV; ++e) u[e] = (col + e < n) ? p[col + e] : 0.f;
 }
 
+// EPV consecutive values of a per-column vector of storage type W (f32 or
+// bf16 bits) as f32, with 16-byte loads when `vec` (16-byte aligned base) and
+// the run is whole; zero past n.
+template <typename W, int EPV>
+__device__ __forceinline__ void load_vec_run(const W* __restrict__ p, int64_t n, int64_t col,
+                                             bool vec, float (&u)[EPV]) {
+  constexpr int BYTES = EPV * (int)sizeof(W);
+  constexpr int PER16 = 16 / (int)sizeof(W);
+  if constexpr (BYTES % 16 == 0) {
+    if (vec && col + EPV <= n) {
+      const uint4* q = reinterpret_cast<const uint4*>(p + col);
+#pragma unroll
+      for (int i = 0; i < BYTES / 16; ++i) Elem<W>::unpack(q[i], &u[i * PER16]);
+      return;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) u[e] = (col + e < n) ? Elem<W>::load(p + col + e) : 0.f;
+}
+
 __device__ __forceinline__ int64_t unit_index() {
   return (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
 }
@@ -138,10 +158,11 @@ __global__ __launch_bounds__(kBlock) void softmax_cached(const T* x,
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) mx = fmaxf(mx, v[i]);
   mx = wave_max(mx);
+  const float ml = mx * kLog2e;
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) {
-    v[i] = fast_exp(v[i] - mx);
+    v[i] = exp_shifted(v[i], ml);
     if (col_of<EPV>(i / EPV, lane, i % EPV) < n) sum += v[i];
   }
   sum = wave_sum(sum);
@@ -169,29 +190,31 @@ __global__ __launch_bounds__(kBlock) void softmax_stream(const T* x,
     for (int e = 0; e < EPV; ++e) mx = fmaxf(mx, v[e]);
   }
   mx = wave_max(mx);
+  const float ml = mx * kLog2e;
   float sum = 0.f;
   for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
     load_chunk<T, EPV>(xr, n, col, v, -INFINITY);
 #pragma unroll
     for (int e = 0; e < EPV; ++e)
-      if (col + e < n) sum += fast_exp(v[e] - mx);
+      if (col + e < n) sum += exp_shifted(v[e], ml);
   }
   const float inv = 1.f / wave_sum(sum);
   for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
     load_chunk<T, EPV>(xr, n, col, v, 0.f);
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) v[e] = fast_exp(v[e] - mx) * inv;
+    for (int e = 0; e < EPV; ++e) v[e] = exp_shifted(v[e], ml) * inv;
     store_chunk<T, EPV>(yr, n, col, v);
   }
 }
 
 // ---------------------------------------------------------------------------
-// RMSNorm: x * rsqrt(mean(x^2) + eps) * w in f32, rounded once.
-template <typename T, int EPV, int VPL>
-__global__ __launch_bounds__(kBlock) void rmsnorm_cached(const T* x,
-                                                         const void* __restrict__ w,
-                                                         int w_dtype, T* y,
-                                                         int64_t m, int64_t n, float eps) {
+// RMSNorm: x * rsqrt(mean(x^2) + eps) * w in f32, rounded once. The weight
+// (storage type W; null for none) is read with the same per-lane column map as
+// x, so its loads are vectors too.
+template <typename T, typename W, int EPV, int VPL>
+__global__ __launch_bounds__(kBlock) void rmsnorm_cached(const T* x, const W* __restrict__ w,
+                                                         bool w_vec, T* y, int64_t m,
+                                                         int64_t n, float eps) {
   const int64_t row = unit_index();
   if (row >= m) return;
   const int lane = threadIdx.x & (kWave - 1);
@@ -199,26 +222,28 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_cached(const T* x,
   load_row<T, EPV, VPL>(x + row * n, n, lane, v, 0.f);
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < VPL * EPV; ++i) ss += v[i] * v[i];
+  for (int i = 0; i < VPL * EPV; ++i) ss = __builtin_fmaf(v[i], v[i], ss);
   ss = wave_sum(ss);
   const float r = rsqrtf(ss / (float)n + eps);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
+    float wv[EPV];
+    if (w != nullptr) {
+      load_vec_run<W, EPV>(w, n, col_of<EPV>(j, lane, 0), w_vec, wv);
+    } else {
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) {
-      const int64_t col = col_of<EPV>(j, lane, e);
-      const float wv = (w != nullptr && col < n) ? load_any(w, w_dtype, col) : 1.f;
-      v[j * EPV + e] = v[j * EPV + e] * r * wv;
+      for (int e = 0; e < EPV; ++e) wv[e] = 1.f;
     }
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) v[j * EPV + e] = v[j * EPV + e] * r * wv[e];
   }
   store_row<T, EPV, VPL>(y + row * n, n, lane, v);
 }
 
-template <typename T, int EPV>
-__global__ __launch_bounds__(kBlock) void rmsnorm_stream(const T* x,
-                                                         const void* __restrict__ w,
-                                                         int w_dtype, T* y,
-                                                         int64_t m, int64_t n, float eps) {
+template <typename T, typename W, int EPV>
+__global__ __launch_bounds__(kBlock) void rmsnorm_stream(const T* x, const W* __restrict__ w,
+                                                         bool w_vec, T* y, int64_t m,
+                                                         int64_t n, float eps) {
   const int64_t row = unit_index();
   if (row >= m) return;
   const int lane = threadIdx.x & (kWave - 1);
@@ -230,16 +255,20 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_stream(const T* x,
   for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
     load_chunk<T, EPV>(xr, n, col, v, 0.f);
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) ss += v[e] * v[e];
+    for (int e = 0; e < EPV; ++e) ss = __builtin_fmaf(v[e], v[e], ss);
   }
   const float r = rsqrtf(wave_sum(ss) / (float)n + eps);
   for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
     load_chunk<T, EPV>(xr, n, col, v, 0.f);
+    float wv[EPV];
+    if (w != nullptr) {
+      load_vec_run<W, EPV>(w, n, col, w_vec, wv);
+    } else {
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) {
-      const float wv = (w != nullptr && col + e < n) ? load_any(w, w_dtype, col + e) : 1.f;
-      v[e] = v[e] * r * wv;
+      for (int e = 0; e < EPV; ++e) wv[e] = 1.f;
     }
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) v[e] = v[e] * r * wv[e];
     store_chunk<T, EPV>(yr, n, col, v);
   }
 }
@@ -503,19 +532,27 @@ int hmx_rmsnorm_rows(int dtype, const void* x, const void* w, int w_dtype, void*
   HMX_REQUIRE(m <= ((int64_t)1 << 31) * kRowsPerBlock, "rms_norm: too many rows");
   if (m == 0) return HMX_OK;
   auto s = (hipStream_t)stream;
+  const bool w_vec = aligned16(w);
   with_type(dtype, rows_vectorizable(x, y, n, dtype), [&](auto tp, auto epv_c) {
     using T = std::remove_pointer_t<decltype(tp)>;
     constexpr int EPV = decltype(epv_c)::value;
-    const int vpl = pick_vpl(n, EPV);
-    if (vpl == 0) {
-      rmsnorm_stream<T, EPV>
-          <<<unit_grid(m), kBlock, 0, s>>>((const T*)x, w, w_dtype, (T*)y, m, n, eps);
-    } else {
-      with_vpl<EPV>(vpl, [&](auto vpl_c) {
-        rmsnorm_cached<T, EPV, decltype(vpl_c)::value>
-            <<<unit_grid(m), kBlock, 0, s>>>((const T*)x, w, w_dtype, (T*)y, m, n, eps);
-      });
-    }
+    auto launch = [&](auto wp) {
+      using W = std::remove_pointer_t<decltype(wp)>;
+      const int vpl = pick_vpl(n, EPV);
+      if (vpl == 0) {
+        rmsnorm_stream<T, W, EPV><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, (const W*)w, w_vec,
+                                                                   (T*)y, m, n, eps);
+      } else {
+        with_vpl<EPV>(vpl, [&](auto vpl_c) {
+          rmsnorm_cached<T, W, EPV, decltype(vpl_c)::value><<<unit_grid(m), kBlock, 0, s>>>(
+              (const T*)x, (const W*)w, w_vec, (T*)y, m, n, eps);
+        });
+      }
+    };
+    if (w != nullptr && w_dtype == HMX_DTYPE_BF16)
+      launch((uint16_t*)nullptr);
+    else
+      launch((float*)nullptr);
   });
   return check_launch("rms_norm");
 }

@@ -90,6 +90,7 @@ extern "C" {
 #define HMX_PACK_B_VNNI_PANELS_T 7  /* [N, K] -> [N/P, K/2, P, 2]          (matmul.py:972-983) */
 #define HMX_PACK_B_PANELS 8         /* [K, N] -> [N/P, K, P]   (benchmarks/helion_block_pack.py:40-51) */
 #define HMX_PACK_A_PANELS 9         /* [M, K] -> [K/P, M, P]   (benchmarks/helion_block_pack.py:54-62) */
+#define HMX_PACK_TRANSPOSE 10       /* [R, C] -> [C_pad, R_pad] of the transpose (zero padded) */
 
 /* The calling thread's last error message ("" if none). */
 const char* hmx_last_error(void);
@@ -195,7 +196,8 @@ int hmx_elementwise(int op, int dtype, const void* x, void* y, int64_t numel,
 
 /* Layout conversion of a contiguous 2-D source [rows, cols] (row stride ld)
  * into the packed layout `kind`, zero-padded to rows_pad x cols_pad of the
- * logical matrix (for *_T kinds the source is the transpose). `panel` is the
+ * logical matrix (for *_T kinds and TRANSPOSE the logical matrix is the
+ * source's transpose). `panel` is the
  * panel width of the PANELS kinds. The pack kernels of
  * helion_mlir_utils/matmul.py:78-153, 972-983 and
  * benchmarks/helion_block_pack.py:40-62. */

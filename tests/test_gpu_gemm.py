@@ -43,7 +43,9 @@ def _check(got, ref, k, a, b, dtype):
 
 
 @pytest.mark.parametrize("mnk", [(100, 100, 130), (33, 35, 66), (70, 40, 201), (20, 40, 50), (65, 372, 47),
-                                 (256, 256, 256), (512, 256, 128), (1, 1, 1), (300, 64, 128), (37, 45, 19)])
+                                 (256, 256, 256), (512, 256, 128), (1, 1, 1), (300, 64, 128), (37, 45, 19),
+                                 # M >= 512 with row-major B: B transposed up front (ragged and whole)
+                                 (600, 333, 129), (1024, 512, 256)])
 @pytest.mark.parametrize(("trans_a", "trans_b"), [(False, False), (True, False), (False, True), (True, True)])
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 def test_matmul_matches_oracle(gpu_device, mnk, trans_a, trans_b, dtype) -> None:
