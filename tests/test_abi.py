@@ -132,13 +132,14 @@ def _plan(lib: ctypes.CDLL, ab: int, m: int, n: int, k: int, batch: int = 1, spl
 
 def test_plans_of_the_baseline_configs(lib: ctypes.CDLL) -> None:
     bf16, f32 = native.DTYPE_BF16, native.DTYPE_F32
-    # 4096^3 bf16: 256 tiles of 256 x 256 fill the 256 CUs, no split; the
-    # row-major B is transposed once into the workspace (4096 * 4096 * 2 bytes).
-    assert _plan(lib, bf16, 4096, 4096, 4096) == (1, 256, 256, 64, 4096 * 4096 * 2)
-    # Without workspace the same plan reads B row-major in the kernel.
-    assert _plan(lib, bf16, 4096, 4096, 4096, max_ws=0) == (1, 256, 256, 64, 0)
+    # 4096^3 bf16: 256 tiles of 256 x 256 fill the 256 CUs, no split; whole
+    # tiles read the row-major B in place, so no workspace.
+    assert _plan(lib, bf16, 4096, 4096, 4096) == (1, 256, 256, 64, 0)
+    # Ragged shapes with enough rows transpose B once into the workspace.
+    assert _plan(lib, bf16, 4000, 4096, 4096) == (1, 256, 256, 64, 4096 * 4096 * 2)
+    assert _plan(lib, bf16, 4000, 4096, 4096, max_ws=0) == (1, 256, 256, 64, 0)
     # Few output rows do not amortize the transpose.
-    assert _plan(lib, bf16, 256, 4096, 4096)[4] == 0
+    assert _plan(lib, bf16, 256, 4000, 4096)[4] == 0
     # Fused linear, 8192 x 11008 x 4096 (B row-major here): 1376 tiles, no split.
     assert _plan(lib, bf16, 8192, 11008, 4096)[:4] == (1, 256, 256, 64)
     # Split-K bmm [16, 256, 65536] @ [16, 65536, 256]: 64 tiles x 16 splits.

@@ -95,6 +95,34 @@ def test_matmul_block_sizes_pick_the_tile(gpu_device, block_sizes) -> None:
     _check(got, R.matmul(to_np(a), to_np(b), out="bf16"), 200, to_np(a), to_np(b), "bf16")
 
 
+# Whole 256 x 256 tiles of row-major A run the direct-to-LDS kernel, which
+# reads B either K-contiguous or row-major (through transposing LDS reads);
+# its register epilogue covers identity / ReLU / SiLU into bf16 or f32.
+@pytest.mark.parametrize("act", ["identity", "relu", "silu"])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_matmul_whole_tiles_direct_to_lds(gpu_device, act, out_dtype, trans_b) -> None:
+    m, n, k = 512, 768, 320
+    a, b = _operands(m, n, k, False, trans_b, "bf16", gpu_device, 0.3)
+    bias, scale, shift = (tensor(RNG.normal(0, 1, n).astype(np.float32), "bf16", gpu_device) for _ in range(3))
+    got = U.matmul(a, b, trans_b=trans_b, bias=bias, scale=scale, shift=shift, epilogue=ACTS[act],
+                   block_sizes=(256, 256, 64), out_dtype=out_dtype)
+    out = "bf16" if out_dtype == torch.bfloat16 else "f32"
+    ref = R.matmul(to_np(a), to_np(b), False, trans_b, to_np(bias), to_np(scale), to_np(shift), act, out=out)
+    _check(to_np(got), ref, k, to_np(a), to_np(b), "bf16")
+
+
+def test_bmm_whole_tiles_split_k_direct_to_lds(gpu_device) -> None:
+    a = tensor(RNG.uniform(-1, 1, (1, 4096, 1024)).astype(np.float32), "bf16", gpu_device)
+    b = tensor(RNG.uniform(-1, 1, (1, 1024, 4096)).astype(np.float32), "bf16", gpu_device)
+    c = U.bmm(a, b, splits=2)
+    assert torch.equal(U.bmm(a, b, splits=2), c)
+    torch.cuda.synchronize()
+    rows = np.sort(RNG.choice(4096, 64, replace=False))
+    an, bn = to_np(a)[0][rows], to_np(b)[0]
+    _check(to_np(c)[0][rows], R.matmul(an, bn, out="bf16"), 1024, an, bn, "bf16")
+
+
 def test_matmul_config1_f32_512(gpu_device) -> None:
     cfg = W.config1()
     got = to_np(U.matmul(cfg["a"].to(gpu_device), cfg["b"].to(gpu_device), block_sizes=[64, 64, 64]))
@@ -169,7 +197,7 @@ def test_linear_affine_and_panel(gpu_device) -> None:
 
 
 @pytest.mark.parametrize("shape", [(2, 160, 96, 224), (2, 65, 129, 129), (3, 100, 70, 130), (4, 64, 64, 8192),
-                                   (1, 33, 17, 40000)])
+                                   (1, 33, 17, 40000), (4, 2048, 2048, 128)])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_bmm_matches_oracle(gpu_device, shape, dtype) -> None:
     batch, m, n, k = shape
