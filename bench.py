@@ -118,7 +118,7 @@ class Gemm(Workload):
         self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_BF16_TFLOPS
         self.work = 2.0 * m * n * k
         self.dtype = "bf16"
-        self.kernel = "gemm_bf16_kernel"
+        self.kernel = "gemm_bf16_kernel" if prepacked else "gemm_bf16_dma_kernel"
         self.config = {"workload": self.description, "m": m, "n": n, "k": k, "a": "bf16 row-major",
                        "b": "bf16 row-major" if not prepacked else "bf16 [N/32,K/32,16,32,2]",
                        "c": out_dtype_name, "seed": 2, "values": "U[-1,1]"}
@@ -161,7 +161,7 @@ class Linear(Workload):
         self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_BF16_TFLOPS
         self.work = 2.0 * 8192 * 11008 * 4096
         self.dtype = "bf16"
-        self.kernel = "gemm_bf16_kernel"
+        self.kernel = "gemm_bf16_dma_kernel"
         self.config = {"workload": self.description, "m": 8192, "n": 11008, "k": 4096, "seed": 3}
 
     def step(self):
