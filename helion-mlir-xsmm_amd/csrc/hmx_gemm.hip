@@ -314,6 +314,20 @@ __device__ __forceinline__ float swap_pair(float v) {
       __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1 /* quad_perm [1,0,3,2] */, 0xF, 0xF, false));
 }
 
+#ifndef HMX_EPI_STREAM
+#define HMX_EPI_STREAM 1
+#endif
+
+// A 4-byte store of C. C is written once and not read back by the kernel:
+// the non-temporal hint keeps the writes from allocating cache lines.
+__device__ __forceinline__ void store_c32(void* p, uint32_t v) {
+#if HMX_EPI_STREAM
+  __builtin_nontemporal_store(v, (uint32_t*)p);
+#else
+  *(uint32_t*)p = v;
+#endif
+}
+
 // Register epilogue: each lane finishes its own accumulators (column
 // lane % 32 of each fragment: bias, scale, shift, activation) and stores them
 // directly. bf16 pairs: rows r and r + 1 of adjacent columns are exchanged
@@ -347,7 +361,7 @@ __device__ __forceinline__ void epilogue_direct(const GemmArgs& g, int split, in
             const float v1 = activate<ACT>((acc[i][j][e1] + bias) * scale + shift);
             const float recv = swap_pair(odd ? v0 : v1);
             const int64_t row = row0 + 8 * (e0 >> 2) + (e0 & 3) + (odd ? 1 : 0);
-            *(uint32_t*)(c + row * g.ldc + pcol) = odd ? pack_bf16x2(recv, v1) : pack_bf16x2(v0, recv);
+            store_c32(c + row * g.ldc + pcol, odd ? pack_bf16x2(recv, v1) : pack_bf16x2(v0, recv));
           }
         } else {
 #pragma unroll
@@ -363,7 +377,7 @@ __device__ __forceinline__ void epilogue_direct(const GemmArgs& g, int split, in
         for (int e = 0; e < 16; ++e) {
           const int64_t row = row0 + 8 * (e >> 2) + (e & 3);
           const float v = activate<ACT>((acc[i][j][e] + bias) * scale + shift);
-          if (!GUARD || (col_in && row < g.m)) c[row * g.ldc + col] = v;
+          if (!GUARD || (col_in && row < g.m)) store_c32(c + row * g.ldc + col, __float_as_uint(v));
         }
       }
     }

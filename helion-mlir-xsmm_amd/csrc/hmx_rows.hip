@@ -25,14 +25,15 @@ constexpr int kMaxPerLane = 64;
 // Row access. A lane's j-th vector of a row covers columns
 // [(j * 64 + lane) * EPV, ... + EPV): for each j the wave reads one contiguous
 // 64 * EPV run, so every load instruction is fully coalesced.
-template <typename T, int EPV, int VPL>
+// WHOLE: n == 64 * VPL * EPV, every vector is in the row (no guards).
+template <typename T, int EPV, int VPL, bool WHOLE = false>
 __device__ __forceinline__ void load_row(const T* __restrict__ p, int64_t n, int lane,
                                          float (&v)[VPL * EPV], float fill) {
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int64_t col = ((int64_t)j * kWave + lane) * EPV;
     if constexpr (EPV > 1) {
-      if (col + EPV <= n) {
+      if (WHOLE || col + EPV <= n) {
         const uint4 raw = *reinterpret_cast<const uint4*>(p + col);
         Elem<T>::unpack(raw, &v[j * EPV]);
       } else {
@@ -46,15 +47,15 @@ __device__ __forceinline__ void load_row(const T* __restrict__ p, int64_t n, int
   }
 }
 
-template <typename T, int EPV, int VPL>
+template <typename T, int EPV, int VPL, bool WHOLE = false>
 __device__ __forceinline__ void store_row(T* __restrict__ p, int64_t n, int lane,
                                           const float (&v)[VPL * EPV]) {
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int64_t col = ((int64_t)j * kWave + lane) * EPV;
     if constexpr (EPV > 1) {
-      if (col + EPV <= n) {
-        *reinterpret_cast<uint4*>(p + col) = Elem<T>::pack(&v[j * EPV]);
+      if (WHOLE || col + EPV <= n) {
+        store16_stream(p + col, Elem<T>::pack(&v[j * EPV]));
       } else {
 #pragma unroll
         for (int e = 0; e < EPV; ++e)
@@ -92,7 +93,7 @@ __device__ __forceinline__ void store_chunk(T* __restrict__ p, int64_t n, int64_
                                             const float (&v)[EPV]) {
   if constexpr (EPV > 1) {
     if (col + EPV <= n) {
-      *reinterpret_cast<uint4*>(p + col) = Elem<T>::pack(v);
+      store16_stream(p + col, Elem<T>::pack(v));
       return;
     }
   }
@@ -145,7 +146,7 @@ __device__ __forceinline__ int64_t unit_index() {
 // Softmax: max, sum of exp(x - max), then exp(x - max) * (1 / sum), as
 // helion_mlir_utils/normalization.py:47-72 computes it (f32 inside, one
 // rounding), with the row held in registers between the passes.
-template <typename T, int EPV, int VPL>
+template <typename T, int EPV, int VPL, bool WHOLE>
 __global__ __launch_bounds__(kBlock) void softmax_cached(const T* x,
                                                          T* y, int64_t m,
                                                          int64_t n) {
@@ -153,7 +154,7 @@ __global__ __launch_bounds__(kBlock) void softmax_cached(const T* x,
   if (row >= m) return;
   const int lane = threadIdx.x & (kWave - 1);
   float v[VPL * EPV];
-  load_row<T, EPV, VPL>(x + row * n, n, lane, v, -INFINITY);
+  load_row<T, EPV, VPL, WHOLE>(x + row * n, n, lane, v, -INFINITY);
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) mx = fmaxf(mx, v[i]);
@@ -163,13 +164,13 @@ __global__ __launch_bounds__(kBlock) void softmax_cached(const T* x,
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) {
     v[i] = exp_shifted(v[i], ml);
-    if (col_of<EPV>(i / EPV, lane, i % EPV) < n) sum += v[i];
+    if (WHOLE || col_of<EPV>(i / EPV, lane, i % EPV) < n) sum += v[i];
   }
   sum = wave_sum(sum);
   const float inv = 1.f / sum;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) v[i] *= inv;
-  store_row<T, EPV, VPL>(y + row * n, n, lane, v);
+  store_row<T, EPV, VPL, WHOLE>(y + row * n, n, lane, v);
 }
 
 template <typename T, int EPV>
@@ -211,15 +212,48 @@ __global__ __launch_bounds__(kBlock) void softmax_stream(const T* x,
 // RMSNorm: x * rsqrt(mean(x^2) + eps) * w in f32, rounded once. The weight
 // (storage type W; null for none) is read with the same per-lane column map as
 // x, so its loads are vectors too.
-template <typename T, typename W, int EPV, int VPL>
+template <typename T, typename W, int EPV, int VPL, bool WHOLE>
 __global__ __launch_bounds__(kBlock) void rmsnorm_cached(const T* x, const W* __restrict__ w,
                                                          bool w_vec, T* y, int64_t m,
                                                          int64_t n, float eps) {
   const int64_t row = unit_index();
   if (row >= m) return;
   const int lane = threadIdx.x & (kWave - 1);
+  if constexpr (WHOLE && EPV > 1) {
+    // Whole rows stay packed in registers (half the VGPRs of f32 for bf16)
+    // and are unpacked once per pass.
+    const uint4* xr = reinterpret_cast<const uint4*>(x + row * n) + lane;
+    uint4 raw[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) raw[j] = xr[j * kWave];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      float t[EPV];
+      Elem<T>::unpack(raw[j], t);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) ss = __builtin_fmaf(t[e], t[e], ss);
+    }
+    const float r = rsqrtf(wave_sum(ss) / (float)n + eps);
+    uint4* yr = reinterpret_cast<uint4*>(y + row * n) + lane;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      float t[EPV], wv[EPV];
+      Elem<T>::unpack(raw[j], t);
+      if (w != nullptr) {
+        load_vec_run<W, EPV>(w, n, col_of<EPV>(j, lane, 0), w_vec, wv);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) wv[e] = 1.f;
+      }
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) t[e] = t[e] * r * wv[e];
+      store16_stream(yr + j * kWave, Elem<T>::pack(t));
+    }
+    return;
+  }
   float v[VPL * EPV];
-  load_row<T, EPV, VPL>(x + row * n, n, lane, v, 0.f);
+  load_row<T, EPV, VPL, WHOLE>(x + row * n, n, lane, v, 0.f);
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) ss = __builtin_fmaf(v[i], v[i], ss);
@@ -237,7 +271,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_cached(const T* x, const W* __
 #pragma unroll
     for (int e = 0; e < EPV; ++e) v[j * EPV + e] = v[j * EPV + e] * r * wv[e];
   }
-  store_row<T, EPV, VPL>(y + row * n, n, lane, v);
+  store_row<T, EPV, VPL, WHOLE>(y + row * n, n, lane, v);
 }
 
 template <typename T, typename W, int EPV>
@@ -514,8 +548,14 @@ int hmx_softmax_rows(int dtype, const void* x, void* y, int64_t m, int64_t n,
       softmax_stream<T, EPV><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, (T*)y, m, n);
     } else {
       with_vpl<EPV>(vpl, [&](auto vpl_c) {
-        softmax_cached<T, EPV, decltype(vpl_c)::value>
-            <<<unit_grid(m), kBlock, 0, s>>>((const T*)x, (T*)y, m, n);
+        constexpr int VPL = decltype(vpl_c)::value;
+        if constexpr (EPV > 1) {
+          if (n == (int64_t)kWave * VPL * EPV) {
+            softmax_cached<T, EPV, VPL, true><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, (T*)y, m, n);
+            return;
+          }
+        }
+        softmax_cached<T, EPV, VPL, false><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, (T*)y, m, n);
       });
     }
   });
@@ -544,7 +584,15 @@ int hmx_rmsnorm_rows(int dtype, const void* x, const void* w, int w_dtype, void*
                                                                    (T*)y, m, n, eps);
       } else {
         with_vpl<EPV>(vpl, [&](auto vpl_c) {
-          rmsnorm_cached<T, W, EPV, decltype(vpl_c)::value><<<unit_grid(m), kBlock, 0, s>>>(
+          constexpr int VPL = decltype(vpl_c)::value;
+          if constexpr (EPV > 1) {
+            if (n == (int64_t)kWave * VPL * EPV) {
+              rmsnorm_cached<T, W, EPV, VPL, true><<<unit_grid(m), kBlock, 0, s>>>(
+                  (const T*)x, (const W*)w, w_vec, (T*)y, m, n, eps);
+              return;
+            }
+          }
+          rmsnorm_cached<T, W, EPV, VPL, false><<<unit_grid(m), kBlock, 0, s>>>(
               (const T*)x, (const W*)w, w_vec, (T*)y, m, n, eps);
         });
       }
