@@ -1076,6 +1076,26 @@ struct Plan {
 // Output rows from which a row-major bf16 B is transposed once up front.
 constexpr int64_t kTransposeMinRows = 512;
 
+// Split K while the grid holds fewer workgroups than fit the CUs at once
+// (one 256 x 256 workgroup per CU, four of the smaller tiles), each chunk
+// keeps at least 8 K tiles, and the partials (written and read again as f32)
+// stay within a quarter of the operand traffic and the workspace limit.
+int auto_splits(TileChoice tile, int64_t tiles, int64_t m, int64_t n, int64_t k, int64_t batch,
+                int64_t esz, int64_t max_ws) {
+  const int64_t kt = ceil_div(k, tile.bk);
+  const int64_t operand_bytes = batch * (m + n) * k * esz;
+  const int64_t resident = (tile.bm == 256 ? 1 : 4) * kCus;
+  int splits = 1;
+  for (;;) {
+    const int s2 = splits * 2;
+    if (tiles * splits >= resident || kt / s2 < 8) break;
+    const int64_t need = (int64_t)s2 * batch * m * n * 4;
+    if ((max_ws >= 0 && need > max_ws) || 2 * need > operand_bytes / 4) break;
+    splits = s2;
+  }
+  return splits;
+}
+
 int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int trans_a,
               int b_layout, int splits, int64_t max_ws, int tile_m, int tile_n, int tile_k,
               Plan& plan) {
@@ -1100,25 +1120,21 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
       const int64_t tiles = ceil_div(m, table[i].bm) * ceil_div(n, table[i].bn) * batch;
       if (tiles >= kCus) { pick = i; break; }
     }
+    // Long-K bf16 products of whole 256 x 256 tiles that split-K can spread
+    // over every CU take the big tile: it reads each operand once (half the
+    // operand traffic of 128 x 128 tiles), and that traffic bounds them.
+    const int64_t big_tiles = (m / 256) * (n / 256) * batch;
+    if (bf16 && !packed && !trans_a && m % 256 == 0 && n % 256 == 0 && k % 64 == 0 &&
+        big_tiles > 0 && big_tiles < kCus &&
+        big_tiles * (splits > 0 ? splits : auto_splits(table[0], big_tiles, m, n, k, batch, 2, max_ws)) >=
+            kCus)
+      pick = 0;
   }
   if (packed && bf16) pick = 0;
   plan.tile = table[pick];
   const int64_t tiles = ceil_div(m, plan.tile.bm) * ceil_div(n, plan.tile.bn) * batch;
   const int64_t kt = ceil_div(k, plan.tile.bk);
-  if (splits == 0) {
-    // Split K while the grid holds fewer than 4 workgroups per CU, each chunk
-    // keeps at least 8 K tiles, and the partials (written and read again as
-    // f32) stay within a quarter of the operand traffic.
-    splits = 1;
-    const int64_t operand_bytes = batch * (m + n) * k * (bf16 ? 2 : 4);
-    for (;;) {
-      const int s2 = splits * 2;
-      if (tiles * splits >= 4 * kCus || kt / s2 < 8) break;
-      const int64_t need = (int64_t)s2 * batch * m * n * 4;
-      if ((max_ws >= 0 && need > max_ws) || 2 * need > operand_bytes / 4) break;
-      splits = s2;
-    }
-  }
+  if (splits == 0) splits = auto_splits(plan.tile, tiles, m, n, k, batch, bf16 ? 2 : 4, max_ws);
   if (splits < 1) splits = 1;
   if (splits > 1) {
     // Whole K tiles per chunk; no empty chunks.
