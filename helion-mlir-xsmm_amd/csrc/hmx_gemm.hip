@@ -865,8 +865,11 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(GemmArgs g) {
 template <int BM_, int BN_, int BK_>
 struct F32Cfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_;
-  static constexpr int NT = 256;
-  static constexpr int WM = BM / 2, WN = BN / 2;
+  // 256 x 256 tiles run 8 waves (2 per SIMD, 2 x 4 over the tile) so that one
+  // wave's LDS traffic and barrier hide behind the other's MFMAs.
+  static constexpr int NT = BM == 256 ? 512 : 256;
+  static constexpr int WAVES_N = NT / 128;
+  static constexpr int WM = BM / 2, WN = BN / WAVES_N;
   static constexpr int FM = WM / 32, FN = WN / 32;
 };
 
@@ -958,7 +961,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm_f32_kernel(GemmArgs g) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / Cfg::WAVES_N, wn = wave % Cfg::WAVES_N;
 
   LA la;
   LB lb;
@@ -1007,33 +1010,71 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm_f32_kernel(GemmArgs g) {
     __syncthreads();
   }
 
-  static_assert(4 * 32 * epi_pitch<Cfg::WN>() <= 2 * STAGE, "epilogue does not fit LDS");
-  epilogue<FM, FN, Cfg::WM, Cfg::WN, GUARD>(g, lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
+  if constexpr (BM == 256) {
+    // Launched only for split-K partials: identity into f32, no vectors.
+    epilogue_direct<FM, FN, Cfg::WM, Cfg::WN, GUARD, ACT_ID, false>(g, split, batch, m0, n0, wm, wn, lane,
+                                                                     true, acc);
+  } else {
+    static_assert(4 * 32 * epi_pitch<Cfg::WN>() <= 2 * STAGE, "epilogue does not fit LDS");
+    epilogue<FM, FN, Cfg::WM, Cfg::WN, GUARD>(g, lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
+  }
 }
 
 // ---------------------------------------------------------------------------
 // Split-K reduction: out[b, i, j] = epilogue(sum_s ws[s, b, i, j]) with s in
-// increasing order, so the result never depends on scheduling.
+// increasing order, so the result never depends on scheduling. V consecutive
+// columns per thread: 16-byte partial loads and 8/16-byte C stores when rows
+// and C keep that alignment (V = 4), else one element (V = 1).
+template <int V>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws,
                                                             int splits, int64_t batch,
                                                             GemmArgs g) {
   const int64_t mn = g.m * g.n;
-  const int64_t total = batch * mn;
+  const int64_t total = batch * mn / V;
   const int64_t split_stride = batch * mn;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
-    float s = 0.f;
-    for (int sp = 0; sp < splits; ++sp) s += ws[sp * split_stride + idx];
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t idx = t * V;
+    float acc[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc[e] = 0.f;
+    for (int sp = 0; sp < splits; ++sp) {
+      const float* p = ws + sp * split_stride + idx;
+      if constexpr (V == 4) {
+        const float4 q = *reinterpret_cast<const float4*>(p);
+        acc[0] += q.x;
+        acc[1] += q.y;
+        acc[2] += q.z;
+        acc[3] += q.w;
+      } else {
+        acc[0] += p[0];
+      }
+    }
     const int64_t b = idx / mn, rem = idx % mn;
     const int64_t row = rem / g.n, col = rem % g.n;
-    float bias, scale, shift;
-    column_vectors(g, col, true, bias, scale, shift);
-    const float v = apply_activation(g.act, (s + bias) * scale + shift, g.act_arg);
+    float v[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      float bias, scale, shift;
+      column_vectors(g, col + e, true, bias, scale, shift);
+      v[e] = apply_activation(g.act, (acc[e] + bias) * scale + shift, g.act_arg);
+    }
     const int64_t off = b * g.stride_c + row * g.ldc + col;
-    if (g.c_dtype == HMX_DTYPE_BF16)
-      ((uint16_t*)g.c)[off] = (uint16_t)f32_to_bf16_bits(v);
-    else
-      ((float*)g.c)[off] = v;
+    if (g.c_dtype == HMX_DTYPE_BF16) {
+      uint16_t* c = (uint16_t*)g.c + off;
+      if constexpr (V == 4)
+        __builtin_nontemporal_store(
+            (uint64_t)pack_bf16x2(v[0], v[1]) | ((uint64_t)pack_bf16x2(v[2], v[3]) << 32), (uint64_t*)c);
+      else
+        *c = (uint16_t)f32_to_bf16_bits(v[0]);
+    } else {
+      float* c = (float*)g.c + off;
+      if constexpr (V == 4)
+        store16_stream(c, make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                     __float_as_uint(v[3])));
+      else
+        *c = v[0];
+    }
   }
 }
 
@@ -1047,6 +1088,9 @@ struct TileChoice {
 // Instantiated workgroup tiles, largest first.
 constexpr TileChoice kBf16Tiles[] = {{256, 256, 64}, {128, 128, 64}};
 constexpr TileChoice kF32Tiles[] = {{128, 128, 32}};
+// The f32 tile long-K split-K products of whole 256 x 256 tiles take (see
+// make_plan): one workgroup per CU reading each operand once.
+constexpr TileChoice kF32Big = {256, 256, 16};
 constexpr int kCus = 256;  // MI355X compute units
 
 int layout_code(int b_layout) {
@@ -1124,14 +1168,16 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
     // over every CU take the big tile: it reads each operand once (half the
     // operand traffic of 128 x 128 tiles), and that traffic bounds them.
     const int64_t big_tiles = (m / 256) * (n / 256) * batch;
-    if (bf16 && !packed && !trans_a && m % 256 == 0 && n % 256 == 0 && k % 64 == 0 &&
-        big_tiles > 0 && big_tiles < kCus &&
-        big_tiles * (splits > 0 ? splits : auto_splits(table[0], big_tiles, m, n, k, batch, 2, max_ws)) >=
+    const TileChoice big = bf16 ? table[0] : kF32Big;
+    if (!packed && !trans_a && m % 256 == 0 && n % 256 == 0 && k % big.bk == 0 && big_tiles > 0 &&
+        big_tiles < kCus &&
+        big_tiles * (splits > 0 ? splits
+                                : auto_splits(big, big_tiles, m, n, k, batch, bf16 ? 2 : 4, max_ws)) >=
             kCus)
-      pick = 0;
+      pick = bf16 ? 0 : -2;
   }
   if (packed && bf16) pick = 0;
-  plan.tile = table[pick];
+  plan.tile = pick == -2 ? kF32Big : table[pick];
   const int64_t tiles = ceil_div(m, plan.tile.bm) * ceil_div(n, plan.tile.bn) * batch;
   const int64_t kt = ceil_div(k, plan.tile.bk);
   if (splits == 0) splits = auto_splits(plan.tile, tiles, m, n, k, batch, bf16 ? 2 : 4, max_ws);
@@ -1250,7 +1296,12 @@ void launch_f32(const GemmArgs& g, bool guard, dim3 grid, hipStream_t s) {
 
 template <class Cfg>
 void dispatch_f32(const GemmArgs& g, int la, int lb, bool guard, dim3 grid, hipStream_t s) {
-  if (la == L_KCONTIG) {
+  if constexpr (Cfg::BM == 256) {
+    if (lb == L_RCONTIG)
+      launch_f32<Cfg, L_KCONTIG, L_RCONTIG>(g, guard, grid, s);
+    else
+      launch_f32<Cfg, L_KCONTIG, L_KCONTIG>(g, guard, grid, s);
+  } else if (la == L_KCONTIG) {
     switch (lb) {
       case L_KCONTIG: launch_f32<Cfg, L_KCONTIG, L_KCONTIG>(g, guard, grid, s); break;
       case L_RCONTIG: launch_f32<Cfg, L_KCONTIG, L_RCONTIG>(g, guard, grid, s); break;
@@ -1420,6 +1471,12 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
       dispatch_bf16<Bf16Cfg<256, 256, 64>>(g, la, lb_run, guard, grid, s);
     else
       dispatch_bf16<Bf16Cfg<128, 128, 64>>(g, la, lb_run, guard, grid, s);
+  } else if (plan.tile.bm == 256) {
+    // Planned only for row-major A, B [N, K] or [K, N] and two or more
+    // splits, so the kernel writes f32 partials with the identity epilogue.
+    if (plan.splits < 2 || la != L_KCONTIG)
+      return set_error(HMX_ERR_INVALID, "gemm: internal f32 plan without split-K");
+    dispatch_f32<F32Cfg<256, 256, 16>>(g, la, lb, guard, grid, s);
   } else {
     dispatch_f32<F32Cfg<128, 128, 32>>(g, la, lb, guard, grid, s);
   }
@@ -1436,8 +1493,16 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
   r.shift = shift;
   r.act = epilogue;
   const int64_t total = batch * m * n;
-  const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(total, 256), 16384);
-  splitk_reduce_kernel<<<blocks, 256, 0, s>>>((const float*)partials, plan.splits, batch, r);
+  const int64_t c_align = c_dtype == HMX_DTYPE_BF16 ? 8 : 16;
+  const bool vec4 = n % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && ((uintptr_t)c % c_align) == 0 &&
+                    ((uintptr_t)partials % 16) == 0;
+  if (vec4) {
+    const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(total / 4, 256), 16384);
+    splitk_reduce_kernel<4><<<blocks, 256, 0, s>>>((const float*)partials, plan.splits, batch, r);
+  } else {
+    const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(total, 256), 16384);
+    splitk_reduce_kernel<1><<<blocks, 256, 0, s>>>((const float*)partials, plan.splits, batch, r);
+  }
   return check_launch("gemm split-K reduce");
 }
 

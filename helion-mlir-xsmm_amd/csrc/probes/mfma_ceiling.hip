@@ -56,8 +56,40 @@ __global__ __launch_bounds__(256, 1) void mfma_block(float* out, int iters) {
   out[t] = s;
 }
 
+// The same block on the f32 MFMA (v_mfma_f32_32x32x2_f32, one value per lane
+// per operand), the instruction of the f32 GEMM.
+template <int MODE>
+__global__ __launch_bounds__(256, 1) void mfma_block_f32(float* out, int iters) {
+  float a[4], b[4];
+  const uint32_t t = blockIdx.x * 256 + threadIdx.x;
+  for (int i = 0; i < 4; ++i) {
+    a[i] = (float)operand(mix(t * 8 + i), MODE);
+    b[i] = (float)operand(mix(0x9e3779b9u ^ (t * 8 + i)), MODE);
+    if (MODE == 1) {  // full 24-bit mantissas, not bf16 values
+      a[i] += (mix(t * 8 + i + 4) >> 8) * (1.0f / 4294967296.0f);
+      b[i] -= (mix(0x85ebca6bu ^ (t * 8 + i)) >> 8) * (1.0f / 4294967296.0f);
+    }
+  }
+  f32x16_t acc[4][4];
+  for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 4; ++j)
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+  }
+  float s = 0.f;
+  for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 4; ++j)
+      for (int e = 0; e < 16; ++e) s += acc[i][j][e];
+  out[t] = s;
+}
+
 template <typename K>
-static int run(const char* name, K kernel, int iters) {
+static int run(const char* name, K kernel, int iters, double flops_per_mfma = 32768.0) {
   float* out = nullptr;
   if (hipMalloc(&out, 256 * 256 * sizeof(float)) != hipSuccess) return 1;
   hipEvent_t s, e;
@@ -72,7 +104,7 @@ static int run(const char* name, K kernel, int iters) {
     hipEventSynchronize(e);
     float ms = 0.f;
     hipEventElapsedTime(&ms, s, e);
-    const double flops = 1024.0 * iters * 16 * 32768.0;
+    const double flops = 1024.0 * iters * 16 * flops_per_mfma;
     printf("%-28s %9.3f ms %8.1f TFLOP/s\n", name, ms, flops / ms / 1e9);
   }
   fflush(stdout);
@@ -85,5 +117,7 @@ int main() {
   rc |= run("constant operands", mfma_block<0>, 50000);
   rc |= run("random U[-1,1] operands", mfma_block<1>, 50000);
   rc |= run("random, 1.5 ms runs", mfma_block<1>, 5000);
+  rc |= run("f32 constant operands", mfma_block_f32<0>, 10000, 4096.0);
+  rc |= run("f32 random operands", mfma_block_f32<1>, 10000, 4096.0);
   return rc;
 }
