@@ -1,0 +1,339 @@
+// Host side of the GEMM: the tile table and planner (hmx_gemm_plan), argument
+// checks, the up-front B transpose, kernel selection and the split-K
+// reduction launch (hmx_gemm). The kernels live in hmx_gemm_bf16_*.hip,
+// hmx_gemm_dma.hip and hmx_gemm_f32.hip.
+#include <algorithm>
+#include <cstdlib>
+
+#include "hmx_gemm_common.hpp"
+
+namespace hmx {
+namespace {
+
+struct TileChoice {
+  int bm, bn, bk;
+};
+
+// Instantiated workgroup tiles, largest first.
+constexpr TileChoice kBf16Tiles[] = {{256, 256, 64}, {128, 128, 64}};
+constexpr TileChoice kF32Tiles[] = {{128, 128, 32}};
+// The f32 tile long-K split-K products of whole 256 x 256 tiles take (see
+// make_plan): one workgroup per CU reading each operand once.
+constexpr TileChoice kF32Big = {256, 256, 16};
+constexpr int kCus = 256;  // MI355X compute units
+
+int layout_code(int b_layout) {
+  switch (b_layout) {
+    case HMX_B_ROW: return L_RCONTIG;
+    case HMX_B_TRANS: return L_KCONTIG;
+    case HMX_B_VNNI_PANELS: return L_VNNI_PANELS;
+    case HMX_B_BLOCKED_VNNI: return L_BLOCKED_VNNI;
+    case HMX_B_PANELS: return L_PANELS;
+    case HMX_B_BLOCKED: return L_BLOCKED;
+  }
+  return -1;
+}
+
+struct Plan {
+  TileChoice tile;
+  int splits;
+  int64_t k_chunk;
+  int64_t workspace_bytes;
+  // Row-major bf16 B is first transposed to [N, K] in the workspace (at
+  // offset 0, bt_bytes long) when enough output rows reuse it: the K-contiguous
+  // kernel path then reads it without register transposes.
+  bool transpose_b;
+  int64_t bt_bytes;
+};
+
+// Output rows from which a row-major bf16 B is transposed once up front.
+constexpr int64_t kTransposeMinRows = 512;
+
+// Split K while the grid holds fewer workgroups than fit the CUs at once
+// (one 256 x 256 workgroup per CU, four of the smaller tiles), each chunk
+// keeps at least 8 K tiles, and the partials (written and read again as f32)
+// stay within a quarter of the operand traffic and the workspace limit.
+int auto_splits(TileChoice tile, int64_t tiles, int64_t m, int64_t n, int64_t k, int64_t batch,
+                int64_t esz, int64_t max_ws) {
+  const int64_t kt = ceil_div(k, tile.bk);
+  const int64_t operand_bytes = batch * (m + n) * k * esz;
+  const int64_t resident = (tile.bm == 256 ? 1 : 4) * kCus;
+  int splits = 1;
+  for (;;) {
+    const int s2 = splits * 2;
+    if (tiles * splits >= resident || kt / s2 < 8) break;
+    const int64_t need = (int64_t)s2 * batch * m * n * 4;
+    if ((max_ws >= 0 && need > max_ws) || 2 * need > operand_bytes / 4) break;
+    splits = s2;
+  }
+  return splits;
+}
+
+int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int trans_a,
+              int b_layout, int splits, int64_t max_ws, int tile_m, int tile_n, int tile_k,
+              Plan& plan) {
+  const bool bf16 = ab_dtype == HMX_DTYPE_BF16;
+  const TileChoice* table = bf16 ? kBf16Tiles : kF32Tiles;
+  const int count = bf16 ? (int)(sizeof(kBf16Tiles) / sizeof(TileChoice))
+                         : (int)(sizeof(kF32Tiles) / sizeof(TileChoice));
+  // Packed B layouts are instantiated for the first tile only.
+  const bool packed = b_layout != HMX_B_ROW && b_layout != HMX_B_TRANS;
+  int pick = -1;
+  if (tile_m > 0 || tile_n > 0 || tile_k > 0) {
+    for (int i = 0; i < count && pick < 0; ++i) {
+      if ((tile_m <= 0 || table[i].bm <= tile_m) && (tile_n <= 0 || table[i].bn <= tile_n) &&
+          (tile_k <= 0 || table[i].bk <= tile_k))
+        pick = i;
+    }
+    if (pick < 0) pick = count - 1;
+  } else {
+    // The largest tile that still gives every CU a workgroup; else the smallest.
+    pick = count - 1;
+    for (int i = 0; i < count; ++i) {
+      const int64_t tiles = ceil_div(m, table[i].bm) * ceil_div(n, table[i].bn) * batch;
+      if (tiles >= kCus) { pick = i; break; }
+    }
+    // Long-K bf16 products of whole 256 x 256 tiles that split-K can spread
+    // over every CU take the big tile: it reads each operand once (half the
+    // operand traffic of 128 x 128 tiles), and that traffic bounds them.
+    const int64_t big_tiles = (m / 256) * (n / 256) * batch;
+    const TileChoice big = bf16 ? table[0] : kF32Big;
+    if (!packed && !trans_a && m % 256 == 0 && n % 256 == 0 && k % big.bk == 0 && big_tiles > 0 &&
+        big_tiles < kCus &&
+        big_tiles * (splits > 0 ? splits
+                                : auto_splits(big, big_tiles, m, n, k, batch, bf16 ? 2 : 4, max_ws)) >=
+            kCus)
+      pick = bf16 ? 0 : -2;
+  }
+  if (packed && bf16) pick = 0;
+  plan.tile = pick == -2 ? kF32Big : table[pick];
+  const int64_t tiles = ceil_div(m, plan.tile.bm) * ceil_div(n, plan.tile.bn) * batch;
+  const int64_t kt = ceil_div(k, plan.tile.bk);
+  if (splits == 0) splits = auto_splits(plan.tile, tiles, m, n, k, batch, bf16 ? 2 : 4, max_ws);
+  if (splits < 1) splits = 1;
+  if (splits > 1) {
+    // Whole K tiles per chunk; no empty chunks.
+    plan.k_chunk = ceil_div(kt, splits) * plan.tile.bk;
+    splits = (int)ceil_div(k, plan.k_chunk);
+  } else {
+    plan.k_chunk = k;
+  }
+  plan.splits = splits;
+  const int64_t partial_bytes = splits > 1 ? (int64_t)splits * batch * m * n * 4 : 0;
+  plan.bt_bytes = ceil_div(n * k * 2, 256) * 256;
+  // Whole 256 x 256 tiles of row-major A read row-major B in place
+  // (direct-to-LDS kernel); other bf16 shapes with enough rows read it
+  // transposed up front.
+  const bool dma_reads_b = plan.tile.bm == 256 && !trans_a && m % 256 == 0 && n % 256 == 0 &&
+                           k % plan.tile.bk == 0 && plan.k_chunk % plan.tile.bk == 0;
+  plan.transpose_b = bf16 && b_layout == HMX_B_ROW && !dma_reads_b && batch == 1 &&
+                     m >= kTransposeMinRows &&
+                     n * k * 2 < INT32_MAX &&
+                     (max_ws < 0 || plan.bt_bytes + partial_bytes <= max_ws);
+  if (!plan.transpose_b) plan.bt_bytes = 0;
+  plan.workspace_bytes = plan.bt_bytes + partial_bytes;
+  return HMX_OK;
+}
+
+// The direct-to-LDS bf16 kernel serves every case it can unless the
+// environment sets HMX_GEMM_DMA=0 (which selects the register-staged kernel,
+// for comparison).
+bool dma_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("HMX_GEMM_DMA");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
+// The direct-to-LDS kernel finishes C with the register epilogue only:
+// identity, ReLU or SiLU, and 4-byte aligned column pairs for bf16 C.
+bool dma_direct_ok(const GemmArgs& g) {
+  const bool act_ok = g.act == HMX_EPI_IDENTITY || g.act == HMX_EPI_RELU || g.act == HMX_EPI_SILU;
+  const bool pair_ok = g.c_dtype != HMX_DTYPE_BF16 ||
+                       (g.ldc % 2 == 0 && g.stride_c % 2 == 0 && g.stride_split % 2 == 0 &&
+                        (((uintptr_t)g.c) & 3) == 0);
+  return act_ok && pair_ok && g.k_chunk % 32 == 0 && g.k > 0;
+}
+
+}  // namespace
+}  // namespace hmx
+
+using namespace hmx;
+
+extern "C" {
+
+int hmx_gemm_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int trans_a,
+                  int b_layout, int splits, int64_t max_workspace_bytes, int tile_m,
+                  int tile_n, int tile_k, int* out_splits, int* out_tile_m, int* out_tile_n,
+                  int* out_tile_k, int64_t* out_workspace_bytes) {
+  HMX_REQUIRE(valid_dtype(ab_dtype), "gemm_plan: unknown dtype %d", ab_dtype);
+  HMX_REQUIRE(layout_code(b_layout) >= 0, "gemm_plan: unknown B layout %d", b_layout);
+  HMX_REQUIRE(m >= 0 && n >= 0 && k >= 0 && batch >= 1, "gemm_plan: invalid shape");
+  HMX_REQUIRE(splits >= 0, "gemm_plan: negative splits");
+  Plan plan;
+  int st = make_plan(ab_dtype, m, n, k, batch, trans_a, b_layout, splits, max_workspace_bytes, tile_m,
+                     tile_n, tile_k, plan);
+  if (st != HMX_OK) return st;
+  if (out_splits) *out_splits = plan.splits;
+  if (out_tile_m) *out_tile_m = plan.tile.bm;
+  if (out_tile_n) *out_tile_n = plan.tile.bn;
+  if (out_tile_k) *out_tile_k = plan.tile.bk;
+  if (out_workspace_bytes) *out_workspace_bytes = plan.workspace_bytes;
+  return HMX_OK;
+}
+
+int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
+             const void* b, int64_t ldb, int b_layout, int64_t b_panel, int64_t b_kpad,
+             void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int64_t batch,
+             int64_t stride_a, int64_t stride_b, int64_t stride_c, const void* bias,
+             const void* scale, const void* shift, int vec_dtype, int epilogue,
+             float epilogue_arg, int splits, void* workspace, int64_t workspace_bytes,
+             int tile_m, int tile_n, int tile_k, void* stream) {
+  HMX_REQUIRE(valid_dtype(ab_dtype) && valid_dtype(c_dtype), "gemm: unknown dtype");
+  HMX_REQUIRE((bias == nullptr && scale == nullptr && shift == nullptr) || valid_dtype(vec_dtype),
+              "gemm: unknown vector dtype %d", vec_dtype);
+  HMX_REQUIRE(valid_activation(epilogue), "gemm: unknown epilogue %d", epilogue);
+  const int lb = layout_code(b_layout);
+  HMX_REQUIRE(lb >= 0, "gemm: unknown B layout %d", b_layout);
+  HMX_REQUIRE(ab_dtype == HMX_DTYPE_BF16 || lb == L_KCONTIG || lb == L_RCONTIG ||
+                  lb == L_BLOCKED || lb == L_PANELS,
+              "gemm: VNNI layouts pair bf16 values; f32 B takes row-major, blocked or panel layouts");
+  HMX_REQUIRE(!trans_a || lb == L_KCONTIG || lb == L_RCONTIG,
+              "gemm: packed B layouts take a row-major A");
+  HMX_REQUIRE(m >= 0 && n >= 0 && k >= 0 && batch >= 1, "gemm: invalid shape [%lld, %lld, %lld] x %lld",
+              (long long)m, (long long)n, (long long)k, (long long)batch);
+  HMX_REQUIRE(a && b && c, "gemm: null operand");
+  HMX_REQUIRE(splits >= 0, "gemm: negative splits");
+  const bool packed = lb != L_KCONTIG && lb != L_RCONTIG;
+  if (!packed) {
+    HMX_REQUIRE(lda >= (trans_a ? m : k) && lda >= 1, "gemm: lda %lld too small", (long long)lda);
+    HMX_REQUIRE(ldb >= (lb == L_KCONTIG ? k : n) && ldb >= 1, "gemm: ldb %lld too small", (long long)ldb);
+  } else {
+    HMX_REQUIRE(b_kpad >= k && b_kpad % (lb == L_VNNI_PANELS ? 2 : 1) == 0,
+                "gemm: packed K extent %lld does not cover K %lld", (long long)b_kpad, (long long)k);
+    if (lb == L_BLOCKED_VNNI || lb == L_BLOCKED)
+      HMX_REQUIRE(b_kpad % 32 == 0, "gemm: blocked K extent %lld is not a multiple of 32", (long long)b_kpad);
+    if (lb == L_VNNI_PANELS || lb == L_PANELS)
+      HMX_REQUIRE(b_panel >= 8 && b_panel % (lb == L_VNNI_PANELS ? 4 : 8) == 0,
+                  "gemm: panel width %lld unsupported", (long long)b_panel);
+  }
+  HMX_REQUIRE(ldc >= n && ldc >= 1, "gemm: ldc %lld too small", (long long)ldc);
+  if (m == 0 || n == 0) return HMX_OK;
+
+  Plan plan;
+  make_plan(ab_dtype, m, n, k, batch, trans_a, b_layout, splits, workspace ? workspace_bytes : 0,
+            tile_m, tile_n, tile_k, plan);
+  if (plan.splits > 1) {
+    HMX_REQUIRE(workspace != nullptr && workspace_bytes >= plan.workspace_bytes,
+                "gemm: split-K needs %lld workspace bytes, got %lld",
+                (long long)plan.workspace_bytes, (long long)workspace_bytes);
+  }
+  void* partials = workspace ? (char*)workspace + plan.bt_bytes : nullptr;
+  int lb_run = lb;
+  if (plan.transpose_b) {
+    // B [K, N] -> B^T [N, K] in the workspace; the GEMM then reads it K-contiguous.
+    launch_transpose16(b, workspace, k, n, ldb, (hipStream_t)stream);
+    const int st = check_launch("gemm B transpose");
+    if (st != HMX_OK) return st;
+    b = workspace;
+    ldb = k;
+    lb_run = L_KCONTIG;
+  }
+  const int64_t tiles_m = ceil_div(m, plan.tile.bm), tiles_n = ceil_div(n, plan.tile.bn);
+  HMX_REQUIRE(tiles_m * tiles_n < ((int64_t)1 << 31) && batch < 65536 && plan.splits < 65536,
+              "gemm: grid too large");
+
+  const int64_t esz = dtype_bytes(ab_dtype);
+  const int64_t vec_elems = 16 / esz;
+  GemmArgs g{};
+  const int la = trans_a ? L_RCONTIG : L_KCONTIG;
+  g.a = Operand{a, lda, m, 0, 0,
+                aligned16(a) && lda % vec_elems == 0 && (batch == 1 || stride_a % vec_elems == 0), 0};
+  const int64_t b_rows = packed ? (lb == L_BLOCKED_VNNI || lb == L_BLOCKED ? ceil_div(n, 32) * 32
+                                                                           : ceil_div(n, b_panel) * b_panel)
+                                : n;
+  g.b = Operand{b, ldb, b_rows, b_panel, b_kpad,
+                aligned16(b) && (packed || ldb % vec_elems == 0) &&
+                    (batch == 1 || stride_b % vec_elems == 0),
+                0};
+  // Bytes spanned by one batch slice of each operand: the buffer-load
+  // range of the whole-tile path, which needs it below 2^31.
+  const int64_t a_bytes = (trans_a ? (k - 1) * lda + m : (m - 1) * lda + k) * esz;
+  const int64_t b_bytes =
+      packed ? b_rows * b_kpad * esz : (lb_run == L_RCONTIG ? (k - 1) * ldb + n : (n - 1) * ldb + k) * esz;
+  const bool bytes_ok = a_bytes < INT32_MAX && b_bytes < INT32_MAX;
+  g.a.bytes = bytes_ok ? (int32_t)a_bytes : 0;
+  g.b.bytes = bytes_ok ? (int32_t)b_bytes : 0;
+  // Packed layouts read zeros (their padding) past N up to the padded extent;
+  // columns past N are never stored.
+  g.stride_a = stride_a;
+  g.stride_b = stride_b;
+  g.m = m;
+  g.n = n;
+  g.k = k;
+  g.k_chunk = plan.k_chunk;
+  g.tiles_m = (int)tiles_m;
+  g.tiles_n = (int)tiles_n;
+  g.bias = bias;
+  g.scale = scale;
+  g.shift = shift;
+  g.vec_dtype = vec_dtype;
+  g.act = epilogue;
+  g.act_arg = epilogue_arg;
+  if (plan.splits > 1) {
+    g.c = partials;
+    g.c_dtype = HMX_DTYPE_F32;
+    g.ldc = n;
+    g.stride_c = m * n;
+    g.stride_split = batch * m * n;
+    g.bias = g.scale = g.shift = nullptr;
+    g.act = HMX_EPI_IDENTITY;
+  } else {
+    g.c = c;
+    g.c_dtype = c_dtype;
+    g.ldc = ldc;
+    g.stride_c = stride_c;
+    g.stride_split = 0;
+  }
+
+  const bool whole = m % plan.tile.bm == 0 && n % plan.tile.bn == 0 &&
+                     plan.k_chunk % plan.tile.bk == 0 && k % plan.tile.bk == 0;
+  const bool guard = !(whole && g.a.vec && g.b.vec && bytes_ok);
+  const dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)plan.splits, (unsigned)batch);
+  auto s = (hipStream_t)stream;
+  if (ab_dtype == HMX_DTYPE_BF16) {
+    const TileChoice t = plan.tile;
+    if (t.bm == 256 && !guard && la == L_KCONTIG && (lb_run == L_KCONTIG || lb_run == L_RCONTIG) &&
+        dma_direct_ok(g) && dma_enabled())
+      launch_gemm_bf16_dma(g, lb_run, grid, s);
+    else
+      launch_gemm_bf16(g, t.bm, la, lb_run, guard, grid, s);
+  } else {
+    // The 256 x 256 f32 tile is planned only for row-major A, B [N, K] or
+    // [K, N] and two or more splits: its kernel writes f32 partials with the
+    // identity epilogue.
+    if (plan.tile.bm == 256 && (plan.splits < 2 || la != L_KCONTIG))
+      return set_error(HMX_ERR_INVALID, "gemm: internal f32 plan without split-K");
+    launch_gemm_f32(g, plan.tile.bm, la, lb, guard, grid, s);
+  }
+  int st = check_launch("gemm");
+  if (st != HMX_OK || plan.splits <= 1) return st;
+
+  GemmArgs r = g;
+  r.c = c;
+  r.c_dtype = c_dtype;
+  r.ldc = ldc;
+  r.stride_c = stride_c;
+  r.bias = bias;
+  r.scale = scale;
+  r.shift = shift;
+  r.act = epilogue;
+  const int64_t c_align = c_dtype == HMX_DTYPE_BF16 ? 8 : 16;
+  const bool vec4 = n % 4 == 0 && ldc % 4 == 0 && stride_c % 4 == 0 && ((uintptr_t)c % c_align) == 0 &&
+                    ((uintptr_t)partials % 16) == 0;
+  launch_splitk_reduce((const float*)partials, plan.splits, batch, r, vec4, s);
+  return check_launch("gemm split-K reduce");
+}
+
+}  // extern "C"

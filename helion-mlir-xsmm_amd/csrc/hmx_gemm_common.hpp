@@ -1,0 +1,320 @@
+// Shared pieces of the GEMM translation units (hmx_gemm_bf16_*.hip,
+// hmx_gemm_dma.hip, hmx_gemm_f32.hip and the host side hmx_gemm.cpp): operand
+// layouts, the kernel argument block, the workgroup -> tile mapping, the fused
+// epilogues, and the launchers each kernel unit exports.
+#pragma once
+
+#include <type_traits>
+
+#include "hmx_device.hpp"
+
+namespace hmx {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// Operand layouts (A: rows are M, B: rows are N; both indexed (row, k)).
+enum : int {
+  L_KCONTIG = 0,      // row * ld + k
+  L_RCONTIG = 1,      // k * ld + row
+  L_VNNI_PANELS = 2,  // [R/P, Kp/2, P, 2]
+  L_BLOCKED_VNNI = 3, // [R/32, Kp/32, 16, 32, 2]
+  L_PANELS = 4,       // [R/P, Kp, P]
+  L_BLOCKED = 5,      // [R/32, Kp/32, 32, 32]
+};
+
+// How a layout's 16-byte vectors run: along K, along rows, or 4 rows x 2 K.
+template <int L>
+constexpr int vec_kind() {
+  return L == L_KCONTIG ? 0 : (L == L_VNNI_PANELS || L == L_BLOCKED_VNNI) ? 2 : 1;
+}
+
+struct Operand {
+  const void* p;   // this batch slice
+  int64_t ld;      // line stride (row-major layouts)
+  int64_t rows;    // logical extent along rows (M or N)
+  int64_t panel;   // panel width (panel layouts)
+  int64_t kpad;    // padded K (packed layouts)
+  bool vec;        // 16-byte loads allowed (alignment of base and lines)
+  int32_t bytes;   // extent of one batch slice in bytes (buffer loads; < 2^31)
+};
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// A buffer resource over one operand slice: loads past `bytes` return zeros
+// instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, int32_t voff, int32_t soff) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+template <int L>
+__device__ __forceinline__ int64_t offset_of(const Operand& o, int64_t r, int64_t k) {
+  if constexpr (L == L_KCONTIG) return r * o.ld + k;
+  if constexpr (L == L_RCONTIG) return k * o.ld + r;
+  if constexpr (L == L_VNNI_PANELS)
+    return (((r / o.panel) * (o.kpad >> 1) + (k >> 1)) * o.panel + (r % o.panel)) * 2 + (k & 1);
+  if constexpr (L == L_BLOCKED_VNNI)
+    return ((((r >> 5) * (o.kpad >> 5) + (k >> 5)) * 16 + ((k & 31) >> 1)) * 32 + (r & 31)) * 2 +
+           (k & 1);
+  if constexpr (L == L_PANELS) return ((r / o.panel) * o.kpad + k) * o.panel + (r % o.panel);
+  if constexpr (L == L_BLOCKED)
+    return (((r >> 5) * (o.kpad >> 5) + (k >> 5)) * 32 + (k & 31)) * 32 + (r & 31);
+  return 0;
+}
+
+__device__ __forceinline__ uint32_t lo_pair(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x05040100u);  // {x.lo16, y.lo16}
+}
+__device__ __forceinline__ uint32_t hi_pair(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x07060302u);  // {x.hi16, y.hi16}
+}
+__device__ __forceinline__ uint32_t dw(const uint4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// ---------------------------------------------------------------------------
+struct GemmArgs {
+  Operand a, b;
+  int64_t stride_a, stride_b;  // batch strides (elements)
+  void* c;
+  int64_t ldc, stride_c, stride_split;
+  int c_dtype;
+  int64_t m, n, k, k_chunk;
+  const void* bias;
+  const void* scale;
+  const void* shift;
+  int vec_dtype;
+  int act;
+  float act_arg;
+  int tiles_m, tiles_n;
+};
+
+// blockIdx.x -> (tile_m, tile_n). Consecutive workgroups are dealt to the 8
+// XCDs in turn; renumbering them so that each XCD gets one contiguous range,
+// then walking that range in groups of kGroupM tile rows, makes the tiles
+// that share A rows and B columns run on the same XCD and its L2.
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+  constexpr int kXcds = 8, kGroupM = 4;
+  const int nb = tiles_m * tiles_n;
+  int bid = blockIdx.x;
+  if (nb % kXcds == 0) bid = (bid % kXcds) * (nb / kXcds) + bid / kXcds;
+  const int per_group = kGroupM * tiles_n;
+  const int group = bid / per_group;
+  const int first_m = group * kGroupM;
+  const int gm = min(kGroupM, tiles_m - first_m);
+  const int in_group = bid % per_group;
+  tm = first_m + in_group % gm;
+  tn = in_group / gm;
+}
+
+__device__ __forceinline__ void column_vectors(const GemmArgs& g, int64_t col, bool in,
+                                               float& bias, float& scale, float& shift) {
+  bias = (g.bias && in) ? load_any(g.bias, g.vec_dtype, col) : 0.f;
+  scale = (g.scale && in) ? load_any(g.scale, g.vec_dtype, col) : 1.f;
+  shift = (g.shift && in) ? load_any(g.shift, g.vec_dtype, col) : 0.f;
+}
+
+
+// Epilogue, staged through LDS (free once the K loop is done). Each wave owns
+// a region of 32 x (WN + 8) f32; for each of its FM fragment rows it writes
+// the accumulators there (element e of lane l of a 32 x 32 fragment is row
+// 8*(e/4) + 4*(l/32) + e%4, column l % 32), then reads them back four
+// columns per lane to apply bias, scale, shift and the activation and store
+// C with 8- or 16-byte coalesced writes.
+template <int WN>
+constexpr int epi_pitch() { return WN + 8; }
+
+// Activation classes compiled into the register epilogue.
+enum : int { ACT_ID = 0, ACT_RELU = 1, ACT_SILU = 2 };
+
+template <int ACT>
+__device__ __forceinline__ float activate(float v) {
+  if constexpr (ACT == ACT_RELU) return apply_activation(HMX_EPI_RELU, v, 0.f);
+  if constexpr (ACT == ACT_SILU) return apply_activation(HMX_EPI_SILU, v, 0.f);
+  return v;
+}
+
+// Exchange with the neighbouring lane (lane ^ 1) through DPP, no LDS.
+__device__ __forceinline__ float swap_pair(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1 /* quad_perm [1,0,3,2] */, 0xF, 0xF, false));
+}
+
+#ifndef HMX_EPI_STREAM
+#define HMX_EPI_STREAM 1
+#endif
+
+// A 4-byte store of C. C is written once and not read back by the kernel:
+// the non-temporal hint keeps the writes from allocating cache lines.
+__device__ __forceinline__ void store_c32(void* p, uint32_t v) {
+#if HMX_EPI_STREAM
+  __builtin_nontemporal_store(v, (uint32_t*)p);
+#else
+  *(uint32_t*)p = v;
+#endif
+}
+
+// Register epilogue: each lane finishes its own accumulators (column
+// lane % 32 of each fragment: bias, scale, shift, activation) and stores them
+// directly. bf16 pairs: rows r and r + 1 of adjacent columns are exchanged
+// between lanes 2c and 2c + 1, so every lane writes one 4-byte word (two
+// columns of one row); f32 lanes write their own 4-byte values.
+template <int FM, int FN, int WM, int WN, bool GUARD, int ACT, bool BF16>
+__device__ __forceinline__ void epilogue_direct(const GemmArgs& g, int split, int batch, int64_t m0,
+                                                int64_t n0, int wm, int wn, int lane, bool pair_ok,
+                                                const f32x16_t (&acc)[FM][FN]) {
+  const int64_t off = split * g.stride_split + batch * g.stride_c;
+  const bool odd = lane & 1;
+  (void)pair_ok;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int64_t col = n0 + wn * WN + j * 32 + (lane & 31);
+    const bool col_in = !GUARD || col < g.n;
+    float bias, scale, shift;
+    column_vectors(g, col, col_in, bias, scale, shift);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int64_t row0 = m0 + wm * WM + i * 32 + 4 * (lane >> 5);
+      if constexpr (BF16) {
+        uint16_t* c = (uint16_t*)g.c + off;
+        if constexpr (!GUARD) {
+          // Whole tile: 4-byte stores of column pairs.
+          const int64_t pcol = col & ~(int64_t)1;
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const int e0 = 2 * q, e1 = 2 * q + 1;
+            const float v0 = activate<ACT>((acc[i][j][e0] + bias) * scale + shift);
+            const float v1 = activate<ACT>((acc[i][j][e1] + bias) * scale + shift);
+            const float recv = swap_pair(odd ? v0 : v1);
+            const int64_t row = row0 + 8 * (e0 >> 2) + (e0 & 3) + (odd ? 1 : 0);
+            store_c32(c + row * g.ldc + pcol, odd ? pack_bf16x2(recv, v1) : pack_bf16x2(v0, recv));
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int64_t row = row0 + 8 * (e >> 2) + (e & 3);
+            const float v = activate<ACT>((acc[i][j][e] + bias) * scale + shift);
+            if (col_in && row < g.m) c[row * g.ldc + col] = (uint16_t)f32_to_bf16_bits(v);
+          }
+        }
+      } else {
+        float* c = (float*)g.c + off;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int64_t row = row0 + 8 * (e >> 2) + (e & 3);
+          const float v = activate<ACT>((acc[i][j][e] + bias) * scale + shift);
+          if (!GUARD || (col_in && row < g.m)) store_c32(c + row * g.ldc + col, __float_as_uint(v));
+        }
+      }
+    }
+  }
+}
+
+template <int FM, int FN, int WM, int WN, bool GUARD>
+__device__ __forceinline__ void epilogue_staged(const GemmArgs& g, float* lds, int split, int batch,
+                                         int64_t m0, int64_t n0, int wm, int wn, int wave,
+                                         int lane, const f32x16_t (&acc)[FM][FN]) {
+  constexpr int P = epi_pitch<WN>();
+  float* ep = lds + wave * 32 * P;
+  const int64_t off = split * g.stride_split + batch * g.stride_c;
+  const bool bf16 = g.c_dtype == HMX_DTYPE_BF16;
+  const bool vec_ok = (g.ldc % 4 == 0) &&
+                      ((((uintptr_t)g.c) & (bf16 ? 7 : 15)) == 0) && (off % 4 == 0);
+  const int64_t col0 = n0 + wn * WN;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        ep[(8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * P + j * 32 + (lane & 31)] = acc[i][j][e];
+    __syncthreads();
+    const int64_t row0 = m0 + wm * WM + i * 32;
+    for (int idx = lane; idx < 32 * (WN / 4); idx += 64) {
+      const int r = idx / (WN / 4), cq = (idx % (WN / 4)) * 4;
+      const int64_t row = row0 + r, col = col0 + cq;
+      if (GUARD && row >= g.m) continue;
+      const float4 q = *(const float4*)(ep + r * P + cq);
+      float v[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const bool in = !GUARD || col + t < g.n;
+        float bias, scale, shift;
+        column_vectors(g, col + t, in, bias, scale, shift);
+        v[t] = apply_activation(g.act, (v[t] + bias) * scale + shift, g.act_arg);
+      }
+      const int64_t o = off + row * g.ldc + col;
+      if ((!GUARD || col + 4 <= g.n) && vec_ok) {
+        if (bf16)
+          *(uint2*)((uint16_t*)g.c + o) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        else
+          *(float4*)((float*)g.c + o) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if (GUARD && col + t >= g.n) break;
+          if (bf16)
+            ((uint16_t*)g.c)[o + t] = (uint16_t)f32_to_bf16_bits(v[t]);
+          else
+            ((float*)g.c)[o + t] = v[t];
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Epilogue dispatch: identity, ReLU and SiLU store from registers; other
+// activations go through the LDS-staged path.
+template <int FM, int FN, int WM, int WN, bool GUARD>
+__device__ __forceinline__ void epilogue(const GemmArgs& g, float* lds, int split, int batch,
+                                         int64_t m0, int64_t n0, int wm, int wn, int wave,
+                                         int lane, const f32x16_t (&acc)[FM][FN]) {
+  const bool bf16 = g.c_dtype == HMX_DTYPE_BF16;
+  const int64_t off = split * g.stride_split + batch * g.stride_c;
+  const bool pair_ok = (g.ldc % 2 == 0) && (off % 2 == 0) && ((((uintptr_t)g.c) & 3) == 0);
+#define HMX_DIRECT(ACT)                                                                          \
+  do {                                                                                           \
+    if (bf16)                                                                                    \
+      epilogue_direct<FM, FN, WM, WN, GUARD, ACT, true>(g, split, batch, m0, n0, wm, wn, lane,   \
+                                                         pair_ok, acc);                          \
+    else                                                                                         \
+      epilogue_direct<FM, FN, WM, WN, GUARD, ACT, false>(g, split, batch, m0, n0, wm, wn, lane,  \
+                                                          pair_ok, acc);                         \
+  } while (0)
+  if (!GUARD && !pair_ok && bf16) {
+    epilogue_staged<FM, FN, WM, WN, GUARD>(g, lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
+    return;
+  }
+  switch (g.act) {
+    case HMX_EPI_IDENTITY: HMX_DIRECT(ACT_ID); break;
+    case HMX_EPI_RELU: HMX_DIRECT(ACT_RELU); break;
+    case HMX_EPI_SILU: HMX_DIRECT(ACT_SILU); break;
+    default:
+      epilogue_staged<FM, FN, WM, WN, GUARD>(g, lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
+  }
+#undef HMX_DIRECT
+}
+
+// Kernel launchers, one translation unit each. `la` / `lb` are L_* layouts
+// of A and B; `guard` selects the kernels that check every edge.
+// hmx_gemm_bf16_*.hip: register-staged bf16 kernel, tiles 256 x 256 or 128 x 128
+// (packed B layouts at 256 x 256 only).
+void launch_gemm_bf16(const GemmArgs& g, int tile_bm, int la, int lb, bool guard, dim3 grid,
+                      hipStream_t s);
+// hmx_gemm_dma.hip: direct-to-LDS bf16 kernel; whole 256 x 256 tiles, A
+// K-contiguous, B K-contiguous or row-major, identity / ReLU / SiLU epilogue.
+void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s);
+// hmx_gemm_f32.hip: f32 kernel, tiles 128 x 128 or (split-K partials only)
+// 256 x 256; and the fixed-order split-K reduction into C.
+void launch_gemm_f32(const GemmArgs& g, int tile_bm, int la, int lb, bool guard, dim3 grid,
+                     hipStream_t s);
+void launch_splitk_reduce(const float* partials, int splits, int64_t batch, const GemmArgs& r,
+                          bool vec4, hipStream_t s);
+
+}  // namespace hmx

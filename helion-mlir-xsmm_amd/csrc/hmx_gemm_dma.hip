@@ -1,0 +1,246 @@
+// Direct-to-LDS bf16 GEMM kernel for gfx950 (v_mfma_f32_32x32x16_bf16):
+// whole 256 x 256 tiles of row-major A and a B that is either K-contiguous
+// ([N, K]) or row-major ([K, N]). Operand tiles go from memory straight into LDS (`buffer_load_dwordx4 ... lds`), with no VGPR
+// staging and no LDS write instructions. Four LDS stages of BK = 32 keep
+// three tiles in flight.
+//
+// LDS tiles are unpadded: one such load fills 1 KiB of LDS contiguously
+// (lane l at byte 16 l), so bank conflicts are avoided by XOR-swizzling
+// 16-byte chunks instead -- the lane that fills slot c of tile row r fetches
+// global chunk c ^ swz(r).
+//  * A, and K-contiguous B: [256 rows][32 k], 64-byte rows (4 chunks),
+//    swz_k(r) = ((r >> 1) & 3) ^ ((r >> 3) & 1). A fragment read (16 bytes:
+//    row lane % 32, chunk 2 ks + lane / 32) then meets distinct banks whether
+//    LDS serves 8 or 16 lanes per cycle.
+//  * row-major B: [32 k][256 n], 512-byte rows (32 chunks),
+//    swz_n(r) = ((r & 3) << 1) ^ ((r & 3) << 2). Fragments come from
+//    ds_read_b64_tr_b16, which transposes within each group of 16 lanes:
+//    lane j receives, as its element e, element j % 4 of the 8 bytes lane
+//    4 e + j / 4 addressed. Lane s of a group addresses row k0 + s / 4 at
+//    columns n0 + 4 (s % 4) .. + 3, so lane j ends with B[k0 .. k0 + 3][n0 + j],
+//    the MFMA's K-ordered operand; two such reads make the 8-value operand.
+//    The 4 rows x 2 (16 lanes) or 4 (32 lanes) chunks touched per pass land
+//    on distinct banks.
+//
+// These loads and their waits are inline assembly: the compiler would
+// otherwise wait for every outstanding LDS load (vmcnt(0)) before any LDS
+// read, which leaves nothing in flight. Loads complete in issue order, so the
+// compiler's own waits for other memory operations stay correct.
+#include "hmx_gemm_common.hpp"
+
+namespace hmx {
+namespace {
+
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ i32x4_t make_srd(const void* p, int32_t bytes) {
+  const uint64_t a = (uint64_t)p;
+  return i32x4_t{(int32_t)(uint32_t)a, (int32_t)((a >> 32) & 0xffff), bytes, 0x00020000};
+}
+
+// One 16-byte-per-lane load from buffer `srd` at voff + soff bytes into LDS
+// bytes [lds, lds + 1024) (lane l at lds + 16 l). An LDS load must not read M0
+// in the cycle after the SALU write of it (one wait state, the s_nop). The
+// kernel has no other use of M0, so clobbering it is safe.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(i32x4_t srd, int32_t voff, int32_t soff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :: "v"(voff), "s"(srd), "s"(soff), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+__device__ __forceinline__ int swz_k(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int swz_n(int r) { return ((r & 3) << 1) ^ ((r & 3) << 2); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+__device__ __forceinline__ bf16x4_t lds_read_tr(const uint8_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_t*)p);
+}
+
+// One instantiation per B orientation, register-epilogue class and C dtype:
+// a single straight-line epilogue keeps the accumulators out of scratch.
+template <int LB, int ACT, bool BF16>
+__global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(GemmArgs g) {
+  constexpr bool BT = LB == L_RCONTIG;             // B row-major [K, N]
+  constexpr int BM = 256, BN = 256, BK = 32, S = 4;
+  constexpr int ROWB = BK * 2;                     // bytes per K-contiguous tile row
+  constexpr int NROWB = BN * 2;                    // bytes per row-major B tile row
+  constexpr int A_BYTES = BM * ROWB;               // 16 KiB
+  constexpr int STAGE = A_BYTES + BN * BK * 2;     // 32 KiB
+  constexpr int FM = 4, FN = 4, WM = 128, WN = 128;
+  constexpr int LOADS = 8;                         // DMA instructions per wave per tile
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE];
+
+  int tm, tn;
+  tile_coords(g.tiles_m, g.tiles_n, tm, tn);
+  const int split = blockIdx.y, batch = blockIdx.z;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t k_begin = (int64_t)split * g.k_chunk;
+  const int64_t k_end = min(g.k, k_begin + g.k_chunk);
+  const int ktiles = (int)((k_end - k_begin) / BK);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const i32x4_t srd_a = make_srd((const uint16_t*)g.a.p + batch * g.stride_a, g.a.bytes);
+  const i32x4_t srd_b = make_srd((const uint16_t*)g.b.p + batch * g.stride_b, g.b.bytes);
+  // Wave w loads 16-row blocks 4w .. 4w + 3 of the A tile: lane l fills slot
+  // l % 4 of block row l / 4. Byte offsets below 2^31: the operands' byte
+  // ranges are.
+  const int drow = lane >> 2;
+  const int32_t voff_a = (int32_t)((drow * g.a.ld + ((lane & 3) ^ swz_k(drow)) * 8) * 2);
+  const int32_t soff_a = (int32_t)((m0 + wave * 64) * g.a.ld * 2);
+  const int32_t blk_a = (int32_t)(16 * g.a.ld * 2);
+  // B: K-contiguous as A; row-major in pairs of rows 8w + 2q, 8w + 2q + 1
+  // (q < 4), lane l filling slot l % 32 of row l / 32 of the pair.
+  int32_t voff_b0, voff_b1, soff_b, blk_b;
+  if constexpr (BT) {
+    const int r = lane >> 5, c = lane & 31;
+    voff_b0 = (int32_t)((r * g.b.ld + (c ^ swz_n(r)) * 8) * 2);      // even q
+    voff_b1 = (int32_t)((r * g.b.ld + (c ^ swz_n(r + 2)) * 8) * 2);  // odd q
+    soff_b = (int32_t)((wave * 8 * g.b.ld + n0) * 2);
+    blk_b = (int32_t)(2 * g.b.ld * 2);
+  } else {
+    voff_b0 = voff_b1 = (int32_t)((drow * g.b.ld + ((lane & 3) ^ swz_k(drow)) * 8) * 2);
+    soff_b = (int32_t)((n0 + wave * 64) * g.b.ld * 2);
+    blk_b = (int32_t)(16 * g.b.ld * 2);
+  }
+  const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + wave * 4 * 1024;
+
+  // DMA q (< 8) of tile t: A blocks for q < 4, then B.
+  auto dma = [&](int t, int q) {
+    const int64_t k0 = k_begin + (int64_t)min(t, ktiles - 1) * BK;
+    const uint32_t st = lds_w + (uint32_t)((t % S) * STAGE);
+    if (q < 4) {
+      lds_dma16(srd_a, voff_a, soff_a + q * blk_a + (int32_t)(k0 * 2), st + q * 1024);
+    } else {
+      const int32_t kb = BT ? (int32_t)(k0 * g.b.ld * 2) : (int32_t)(k0 * 2);
+      lds_dma16(srd_b, (q & 1) ? voff_b1 : voff_b0, soff_b + (q - 4) * blk_b + kb,
+                st + A_BYTES + (q - 4) * 1024);
+    }
+  };
+
+  f32x16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Fragment reads. A (and K-contiguous B): row lane % 32 of the fragment,
+  // chunk 2 ks + lane / 32.
+  const int frow = lane & 31, fk = lane >> 5, fswz = swz_k(frow);
+  const uint8_t* a_frag = lds + (wm * WM + frow) * ROWB;
+  const uint8_t* b_frag = lds + A_BYTES + (wn * WN + frow) * ROWB;
+  // Row-major B: lane s of 16-lane group gi addresses row 8 (gi / 2) + s / 4
+  // (+ 16 ks, + 4 for the second read) and the chunk holding columns
+  // wn * 128 + 32 j + 16 (gi % 2) + 4 (s % 4).
+  int b_tr[FN];
+  {
+    const int gi = lane >> 4, sl = lane & 15;
+    const int v = (2 * (gi & 1) + ((sl & 3) >> 1)) ^ swz_n(sl >> 2);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      b_tr[j] = A_BYTES + (8 * (gi >> 1) + (sl >> 2)) * NROWB + (wn * 16 + ((4 * j) ^ v)) * 16 + 8 * (sl & 1);
+  }
+  auto a_read = [&](int stage, int ks, int i) -> bf16x8_t {
+    return *(const bf16x8_t*)(a_frag + stage * STAGE + i * 32 * ROWB + ((2 * ks + fk) ^ fswz) * 16);
+  };
+  auto b_read = [&](int stage, int ks, int j) -> bf16x8_t {
+    if constexpr (BT) {
+      const uint8_t* p = lds + stage * STAGE + b_tr[j] + 16 * ks * NROWB;
+      return __builtin_shufflevector(lds_read_tr(p), lds_read_tr(p + 4 * NROWB), 0, 1, 2, 3, 4, 5, 6, 7);
+    } else {
+      return *(const bf16x8_t*)(b_frag + stage * STAGE + j * 32 * ROWB + ((2 * ks + fk) ^ fswz) * 16);
+    }
+  };
+
+  // The host launches this kernel only with at least one K tile per split.
+  bf16x8_t a0[FM], b0[FN], a1[FM], b1[FN];
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+#pragma unroll
+    for (int q = 0; q < LOADS; ++q) dma(t, q);
+  wait_vmem<2 * LOADS>();  // tile 0 landed
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < FM; ++i) a0[i] = a_read(0, 0, i);
+#pragma unroll
+  for (int j = 0; j < FN; ++j) b0[j] = b_read(0, 0, j);
+
+  for (int t = 0; t < ktiles; ++t) {
+    // Tiles t + 1 and t + 2 are in flight: wait for t + 1, then the barrier
+    // publishes it and frees stage (t + 3) % S (last read in step t - 1).
+    // The barrier carries no LDS fence: every LDS read of the freed stage
+    // was consumed by an MFMA of step t - 1 before it.
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(LOADS) : "memory");
+    const int cur = t % S, nxt = t + 1 < ktiles ? (t + 1) % S : cur;
+    // 32 MFMA slots per step, each paired with at most one other memory
+    // operation: slots 0-7 read k-step 1's fragments, slots 8-15 issue the
+    // DMA of tile t + 3, slots 16-23 read the next tile's k-step 0 fragments
+    // (a quarter step ahead of the barrier that follows).
+#pragma unroll
+    for (int x = 0; x < 32; ++x) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int f = x & 7;
+      if (x < 8) {
+        if (f < 4) a1[f] = a_read(cur, 1, f);
+        else b1[f - 4] = b_read(cur, 1, f - 4);
+      } else if (x < 16) {
+        dma(t + 3, f);
+      } else if (x < 24) {
+        if (f < 4) a0[f] = a_read(nxt, 0, f);
+        else b0[f - 4] = b_read(nxt, 0, f - 4);
+      }
+      const int idx = x & 15, i = idx >> 2, j = idx & 3;
+      if (x < 16)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[i], b0[j], acc[i][j], 0, 0, 0);
+      else
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[i], b1[j], acc[i][j], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  wait_vmem<0>();  // no load into LDS outlives the loop
+  epilogue_direct<FM, FN, WM, WN, false, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
+}
+
+template <int LB, bool BF16>
+void launch_bf16_dma_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  switch (g.act) {
+    case HMX_EPI_RELU: gemm_bf16_dma_kernel<LB, ACT_RELU, BF16><<<grid, 256, 0, s>>>(g); break;
+    case HMX_EPI_SILU: gemm_bf16_dma_kernel<LB, ACT_SILU, BF16><<<grid, 256, 0, s>>>(g); break;
+    default: gemm_bf16_dma_kernel<LB, ACT_ID, BF16><<<grid, 256, 0, s>>>(g); break;
+  }
+}
+
+template <int LB>
+void launch_bf16_dma_b(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  if (g.c_dtype == HMX_DTYPE_BF16)
+    launch_bf16_dma_c<LB, true>(g, grid, s);
+  else
+    launch_bf16_dma_c<LB, false>(g, grid, s);
+}
+
+}  // namespace
+
+void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {
+  if (lb == L_RCONTIG)
+    launch_bf16_dma_b<L_RCONTIG>(g, grid, s);
+  else
+    launch_bf16_dma_b<L_KCONTIG>(g, grid, s);
+}
+
+
+}  // namespace hmx
