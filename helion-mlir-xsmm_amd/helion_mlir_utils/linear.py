@@ -26,7 +26,7 @@ from helion_mlir_backend import output_pool, prepared_call
 from helion_mlir_backend._compiler import native
 
 from ._gpu import epilogue_code, identity_epilogue, is_gpu
-from .matmul import _launch_gemm, _vectors, matmul, matmul_prepacked_b, pack_b_vnni_t, prepacked_b_call
+from .matmul import GemmLaunch, _vectors, matmul, matmul_prepacked_b, pack_b_vnni_t, prepacked_b_call
 
 if TYPE_CHECKING:
     from torch import Tensor, nn
@@ -124,14 +124,11 @@ def _weight_call(
     bias_, scale_, shift_, vec_dtype = _vectors(bias, scale, shift, n, x)
     dtype, device = x.dtype, x.device
 
-    def launch(a: Tensor) -> Tensor:
-        c = output_pool.empty((m, n), dtype=dtype, device=device)
-        return _launch_gemm(
-            a, k, False, packed, k, native.B_TRANS, 0, 0, c, m, n, k,
-            bias=bias_, scale=scale_, shift=shift_, vec_dtype=vec_dtype, epilogue=code,
-        )
-
-    return prepared_call(launch, [x], general)
+    launch = GemmLaunch(
+        native.dtype_code(dtype), dtype, device, (m, n), k, False, k, native.B_TRANS, 0, 0, m, n, k,
+        bias=bias_, scale=scale_, shift=shift_, vec_dtype=vec_dtype, epilogue=code,
+    )
+    return prepared_call(lambda a: launch.run(a, packed), [x], general)
 
 
 def linear(

@@ -136,10 +136,21 @@ def _vectors(
     return out[0], out[1], out[2], native.dtype_code(dtype)
 
 
+# hmx_gemm_plan results by problem: the plan is a pure function of these
+# arguments, so a repeated shape skips the native call (bounded, cleared when
+# full, like the reference's LRU of bound kernels, matmul.py:487-489).
+_PLANS: dict[tuple, tuple[int, int, int, int, int]] = {}
+_PLANS_MAX = 1024
+
+
 def _plan(ab: int, m: int, n: int, k: int, batch: int, trans_a: bool, layout: int,
           splits: int, tiles: Sequence[int] | None) -> tuple[int, int, int, int, int]:
     """hmx_gemm_plan: (splits, tile_m, tile_n, tile_k, workspace bytes)."""
     tm, tn, tk = (list(tiles) + [0, 0, 0])[:3] if tiles else (0, 0, 0)
+    key = (ab, m, n, k, batch, bool(trans_a), layout, splits, int(tm), int(tn), int(tk))
+    hit = _PLANS.get(key)
+    if hit is not None:
+        return hit
     out = [ctypes.c_int() for _ in range(4)]
     ws = ctypes.c_int64()
     native.check(
@@ -148,7 +159,11 @@ def _plan(ab: int, m: int, n: int, k: int, batch: int, trans_a: bool, layout: in
                                    ctypes.byref(ws)),
         "hmx_gemm_plan",
     )
-    return out[0].value, out[1].value, out[2].value, out[3].value, ws.value
+    plan = (out[0].value, out[1].value, out[2].value, out[3].value, ws.value)
+    if len(_PLANS) >= _PLANS_MAX:
+        _PLANS.clear()
+    _PLANS[key] = plan
+    return plan
 
 
 def gemm_plan(a_dtype: torch.dtype, m: int, n: int, k: int, batch: int = 1,
@@ -161,6 +176,78 @@ def gemm_plan(a_dtype: torch.dtype, m: int, n: int, k: int, batch: int = 1,
     return {"splits": s, "tile_m": tm, "tile_n": tn, "tile_k": tk, "workspace_bytes": ws}
 
 
+class GemmLaunch:
+    """One ``hmx_gemm`` problem with everything but the operand and output
+    data pointers bound: the plan (splits, workspace bytes), shapes, strides,
+    layout, epilogue and per-column vectors. A call allocates C (and the
+    workspace, from torch's caching allocator), reads the current stream and
+    makes the one native call -- the prepared launch that stands in for the
+    reference's ``PreparedRun`` (``native/call.cpp:703-830``). The bound
+    vectors are kept alive by the launch."""
+
+    __slots__ = ("_fn", "_args", "_vectors", "_ws_bytes", "_device", "_shape", "_dtype", "splits")
+
+    def __init__(
+        self, ab: int, c_dtype: torch.dtype, device: torch.device, c_shape: tuple[int, ...],
+        lda: int, trans_a: bool, ldb: int, layout: int, panel: int, kpad: int,
+        m: int, n: int, k: int, batch: int = 1, stride_a: int = 0, stride_b: int = 0,
+        stride_c: int = 0, bias: Tensor | None = None, scale: Tensor | None = None,
+        shift: Tensor | None = None, vec_dtype: int = native.DTYPE_F32,
+        epilogue: tuple[int, float] = (native.EPI_IDENTITY, 0.0), splits: int = 0,
+        tiles: Sequence[int] | None = None,
+    ) -> None:
+        tm, tn, tk = (list(tiles) + [0, 0, 0])[:3] if tiles else (0, 0, 0)
+        s, _, _, _, ws_bytes = _plan(ab, m, n, k, batch, trans_a, layout, splits, tiles)
+        self._fn = native.lib().hmx_gemm
+        self._vectors = (bias, scale, shift)
+        # The arguments of hmx_gemm in order (include/hmx.h); slots 2 (A),
+        # 5 (B), 10 (C), 26 (workspace) and 31 (stream) are filled per call.
+        self._args = [
+            ab, native.dtype_code(c_dtype),
+            None, lda, int(trans_a),
+            None, ldb, layout, panel, kpad,
+            None, n,
+            m, n, k,
+            batch, stride_a, stride_b, stride_c,
+            native.ptr(bias), native.ptr(scale), native.ptr(shift), vec_dtype,
+            epilogue[0], epilogue[1],
+            s, None, ws_bytes,
+            int(tm), int(tn), int(tk),
+            None,
+        ]
+        self._ws_bytes = ws_bytes
+        self._device = device
+        self._shape = c_shape
+        self._dtype = c_dtype
+        self.splits = s
+
+    def run(self, a: Tensor, b: Tensor, c: Tensor | None = None) -> Tensor:
+        """C = the bound GEMM of ``a`` and ``b`` (buffers as planned)."""
+        if c is None:
+            c = output_pool.empty(self._shape, dtype=self._dtype, device=self._device)
+        args = list(self._args)
+        args[2] = a.data_ptr()
+        args[5] = b.data_ptr()
+        args[10] = c.data_ptr()
+        ws = None
+        if self._ws_bytes > 0:
+            ws = torch.empty(self._ws_bytes, dtype=torch.uint8, device=self._device)
+            args[26] = ws.data_ptr()
+        device = self._device
+        if device.index is None or device.index == torch.cuda.current_device():
+            native.ensure_device(device)
+            args[31] = native.stream_of(device)
+            status = self._fn(*args)
+        else:
+            with on_device(device) as stream:
+                args[31] = stream
+                status = self._fn(*args)
+        native.count_call()
+        if status:
+            native.check(status, "hmx_gemm")
+        return c
+
+
 def _launch_gemm(
     a: Tensor, lda: int, trans_a: bool,
     b: Tensor, ldb: int, layout: int, panel: int, kpad: int,
@@ -170,25 +257,12 @@ def _launch_gemm(
     vec_dtype: int = native.DTYPE_F32, epilogue: tuple[int, float] = (native.EPI_IDENTITY, 0.0),
     splits: int = 0, tiles: Sequence[int] | None = None,
 ) -> Tensor:
-    ab = native.dtype_code(a.dtype)
-    tm, tn, tk = (list(tiles) + [0, 0, 0])[:3] if tiles else (0, 0, 0)
-    with on_device(a.device) as stream:
-        s, _, _, _, ws_bytes = _plan(ab, m, n, k, batch, trans_a, layout, splits, tiles)
-        ws = (
-            torch.empty(ws_bytes, dtype=torch.uint8, device=a.device) if ws_bytes > 0 else None
-        )
-        native.call(
-            "hmx_gemm", ab, native.dtype_code(c.dtype),
-            a.data_ptr(), lda, int(trans_a),
-            b.data_ptr(), ldb, layout, panel, kpad,
-            c.data_ptr(), n if c.dim() >= 2 else n,
-            m, n, k, batch, stride_a, stride_b, stride_c,
-            native.ptr(bias), native.ptr(scale), native.ptr(shift), vec_dtype,
-            epilogue[0], epilogue[1],
-            s, native.ptr(ws), ws_bytes,
-            int(tm), int(tn), int(tk), stream,
-        )
-    return c
+    launch = GemmLaunch(
+        native.dtype_code(a.dtype), c.dtype, a.device, tuple(c.shape), lda, trans_a, ldb, layout,
+        panel, kpad, m, n, k, batch, stride_a, stride_b, stride_c, bias, scale, shift, vec_dtype,
+        epilogue, splits, tiles,
+    )
+    return launch.run(a, b, c)
 
 
 def matmul(
@@ -567,13 +641,9 @@ def prepacked_b_call(
     bias_, scale_, shift_, vec_dtype = _vectors(bias, scale, shift, n, a)
     b_buf = b4.contiguous()
     tiles = (tile_m, 0, 0) if tile_m else None
-    return prepared_call(
-        lambda x: _launch_gemm(
-            x, k, False, b_buf, 0, layout, panel, kpad,
-            output_pool.empty((m, n), dtype=a.dtype, device=a.device), m, n, k,
-            bias=bias_, scale=scale_, shift=shift_, vec_dtype=vec_dtype, epilogue=code,
-            tiles=tiles,
-        ),
-        [a],
-        general,
+    launch = GemmLaunch(
+        native.dtype_code(a.dtype), a.dtype, a.device, (m, n), k, False, 0, layout, panel, kpad,
+        m, n, k, bias=bias_, scale=scale_, shift=shift_, vec_dtype=vec_dtype, epilogue=code,
+        tiles=tiles,
     )
+    return prepared_call(lambda x: launch.run(x, b_buf), [a], general)
