@@ -13,9 +13,10 @@ softmax, softmax_f32, rmsnorm, rmsnorm_f32, bmm, bmm_bf16, matmul_f32.
 
 Timing: W untimed steps, then K steps bracketed by ``torch.cuda.synchronize()``
 and HIP events recorded on the stream the kernels run on (torch's current
-stream, which the library launches on). ``roofline.achieved`` is the
-algorithmic work per launch of the dominant kernel over its average launch
-time; ``roofline.traffic`` is the HBM bytes per launch measured with
+stream, which the library launches on); ``value`` spans all K steps. Each
+step also has its own event pair: ``roofline.achieved`` is the algorithmic
+work per launch of the dominant kernel over the mean of those pairs (its
+average launch duration); ``roofline.traffic`` is the HBM bytes per launch measured with
 rocprofv3 counters (``profiles/traffic.json``), or null when not measured.
 ``cpu_baseline`` times the CPU oracle (``oracle/restate.py``, numpy) on the
 host cores on a bounded sample of the same workload.
@@ -349,23 +350,31 @@ def make(name: str, device) -> Workload:
 
 
 def measure(w: Workload, steps: int, warmup: int) -> dict:
-    """Step time (ms) over ``steps`` timed steps with HIP events."""
+    """Step time (ms) over ``steps`` timed steps, and the average duration of
+    one step's launches, both from HIP events on the stream the library
+    launches on (torch's current stream).
+
+    Each timed step is bracketed by its own pair of events, so ``launch_ms``
+    (the mean of the pairs) is the GPU time of the step's kernels without the
+    host's time between steps; ``ms`` spans the first event to the last.
+    """
     import torch
 
     for _ in range(warmup):
         w.step()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for i in range(steps):
+        starts[i].record()
         w.step()
-    end.record()
+        ends[i].record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    ms = starts[0].elapsed_time(ends[-1]) / steps
+    launch_ms = sum(a.elapsed_time(b) for a, b in zip(starts, ends)) / steps
     scale = 1e12 if w.unit == "TFLOP/s" else 1e9
     value = w.work / (ms * 1e-3) / scale
-    return {"ms": ms, "value": value, "frac": value / w.peak}
+    return {"ms": ms, "launch_ms": launch_ms, "value": value, "frac": value / w.peak}
 
 
 def traffic_of(name: str) -> float | None:
@@ -401,9 +410,13 @@ def main() -> int:
     print(f"bench: workload={args.workload} steps={args.steps} warmup={args.warmup}", file=sys.stderr, flush=True)
     w = make(args.workload, device)
     result = measure(w, args.steps, args.warmup)
-    print(f"bench: {w.name} {result['ms']:.4f} ms/step {result['value']:.1f} {w.unit}", file=sys.stderr, flush=True)
+    print(f"bench: {w.name} {result['ms']:.4f} ms/step {result['value']:.1f} {w.unit}, "
+          f"{result['launch_ms']:.4f} ms/launch", file=sys.stderr, flush=True)
 
-    per_launch_ms = result["ms"]  # one dominant launch per step (bmm: includes its reduction launch)
+    # The dominant kernel is the step's only launch, except the split-K bmm,
+    # whose step is the split GEMM plus its fixed-order reduction: both are
+    # inside the measured launch time there.
+    per_launch_ms = result["launch_ms"]
     achieved = w.work / (per_launch_ms * 1e-3) / (1e12 if w.unit == "TFLOP/s" else 1e9)
     roofline = {
         "bound": w.bound,
@@ -436,9 +449,15 @@ def main() -> int:
         for name in ("softmax", "rmsnorm"):
             cw = make(name, device)
             r = measure(cw, args.steps, args.warmup)
+            achieved_c = cw.work / (r["launch_ms"] * 1e-3) / 1e9
             components[name + "_bf16"] = {
                 "value": round(r["value"], 1), "unit": "GB/s", "frac": round(r["frac"], 4),
-                "ms_per_step": round(r["ms"], 5), "traffic": traffic_of(cw.name), "config": cw.config,
+                "ms_per_step": round(r["ms"], 5),
+                "roofline": {"bound": "hbm", "achieved": round(achieved_c, 1), "peak": PEAK_HBM_GBS,
+                             "unit": "GB/s", "frac": round(achieved_c / PEAK_HBM_GBS, 4),
+                             "traffic": traffic_of(cw.name), "kernel": cw.kernel,
+                             "launch_ms": round(r["launch_ms"], 5)},
+                "config": cw.config,
             }
             print(f"bench: {name} {r['ms']:.4f} ms/step {r['value']:.1f} GB/s", file=sys.stderr, flush=True)
             del cw

@@ -1,13 +1,18 @@
 // Memory-bound row kernels for gfx950: softmax, RMSNorm, GroupNorm/LayerNorm,
 // row sums, row dots, gemv, column sums and elementwise ops.
 //
-// One wave64 owns one row (or one (row, group) unit). A row of up to
-// 64 * kMaxPerLane elements is read once from HBM with 16-byte loads
-// (`global_load_dwordx4`) into registers, reduced with xor butterflies across
-// the wave, and written once: one HBM read and one write per element, the
-// floor for these ops. Longer rows stream through the same code in chunks
-// (extra reads from L2/HBM). Four waves share a 256-thread workgroup, so a
-// [32768, 4096] input launches 8192 workgroups (32 per CU).
+// A row (or one (row, group) unit) is read once from HBM with 16-byte loads
+// (`global_load_dwordx4`) into registers, reduced, and written once with
+// non-temporal stores: one HBM read and one write per element, the floor for
+// these ops. Short rows (at most two vectors per lane of one wave) take one
+// wave each, four rows per 256-thread workgroup. Longer rows take a whole
+// workgroup of WPR waves (up to 16) holding two or more vectors per lane and
+// combine the per-wave reductions through LDS: a [32768, 4096] f32 softmax
+// runs 32768 workgroups of 8 waves with 8 values per lane, which measures
+// ~25% more bandwidth on gfx950 than one wave holding the 4096-value row (64
+// values per lane, 5 waves per SIMD). Rows longer than the register cache
+// (16 waves x 64 values per lane) stream through the same math in chunks, one
+// wave per row.
 #include <type_traits>
 #include <utility>
 
@@ -18,20 +23,26 @@ namespace {
 
 constexpr int kRowsPerBlock = 4;
 constexpr int kBlock = kRowsPerBlock * kWave;
-// f32 values a lane keeps of a cached row: 64 VGPRs.
-constexpr int kMaxPerLane = 64;
+// f32 values a lane keeps of a cached row: 16 VGPRs, so that every cached
+// kernel fits a 1024-thread workgroup (128 VGPRs per lane at most) without
+// spilling. Rows of up to 16 waves x 64 lanes x 16 = 16384 values are cached.
+constexpr int kMaxPerLane = 16;
+// Waves of a workgroup that share one row.
+constexpr int kMaxWavesPerRow = 16;
+constexpr int kMaxBlock = kMaxWavesPerRow * kWave;
 
 // ---------------------------------------------------------------------------
-// Row access. A lane's j-th vector of a row covers columns
-// [(j * 64 + lane) * EPV, ... + EPV): for each j the wave reads one contiguous
-// 64 * EPV run, so every load instruction is fully coalesced.
-// WHOLE: n == 64 * VPL * EPV, every vector is in the row (no guards).
+// Row access. `tpr` threads share a row; thread `li` of them holds, as its
+// j-th vector, columns [(j * tpr + li) * EPV, ... + EPV): for each j the
+// threads read one contiguous tpr * EPV run, so every load instruction is
+// fully coalesced.
+// WHOLE: n == tpr * VPL * EPV, every vector is in the row (no guards).
 template <typename T, int EPV, int VPL, bool WHOLE = false>
-__device__ __forceinline__ void load_row(const T* __restrict__ p, int64_t n, int lane,
+__device__ __forceinline__ void load_row(const T* __restrict__ p, int64_t n, int li, int tpr,
                                          float (&v)[VPL * EPV], float fill) {
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    const int64_t col = ((int64_t)j * kWave + lane) * EPV;
+    const int64_t col = ((int64_t)j * tpr + li) * EPV;
     if constexpr (EPV > 1) {
       if (WHOLE || col + EPV <= n) {
         const uint4 raw = *reinterpret_cast<const uint4*>(p + col);
@@ -48,11 +59,11 @@ __device__ __forceinline__ void load_row(const T* __restrict__ p, int64_t n, int
 }
 
 template <typename T, int EPV, int VPL, bool WHOLE = false>
-__device__ __forceinline__ void store_row(T* __restrict__ p, int64_t n, int lane,
+__device__ __forceinline__ void store_row(T* __restrict__ p, int64_t n, int li, int tpr,
                                           const float (&v)[VPL * EPV]) {
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    const int64_t col = ((int64_t)j * kWave + lane) * EPV;
+    const int64_t col = ((int64_t)j * tpr + li) * EPV;
     if constexpr (EPV > 1) {
       if (WHOLE || col + EPV <= n) {
         store16_stream(p + col, Elem<T>::pack(&v[j * EPV]));
@@ -67,10 +78,53 @@ __device__ __forceinline__ void store_row(T* __restrict__ p, int64_t n, int lane
   }
 }
 
-// Column of element e of a lane's j-th vector.
+// Column of element e of a thread's j-th vector.
 template <int EPV>
-__device__ __forceinline__ int64_t col_of(int j, int lane, int e) {
-  return ((int64_t)j * kWave + lane) * EPV + e;
+__device__ __forceinline__ int64_t col_of(int j, int li, int tpr, int e) {
+  return ((int64_t)j * tpr + li) * EPV + e;
+}
+
+// Where a thread of a cached-row kernel sits: `wpr` waves per row and
+// blockDim.x / (64 * wpr) rows per workgroup (wpr == 1: one wave per row;
+// wpr > 1: one row per workgroup).
+struct RowPos {
+  int64_t row;
+  int li;   // index among the row's threads
+  int tpr;  // threads per row
+  int wpr;
+};
+
+__device__ __forceinline__ RowPos row_pos(int wpr) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
+  const int rows = blockDim.x / (wpr * kWave);
+  return RowPos{(int64_t)blockIdx.x * rows + wave / wpr, (wave % wpr) * kWave + lane,
+                wpr * kWave, wpr};
+}
+
+// Sum / max over all threads of a row: xor butterflies in each wave, then
+// (wpr > 1) the waves' partials through LDS, combined in wave order by every
+// thread, so all threads hold the same value. Each call site passes its own
+// `slot` array (kMaxWavesPerRow floats): no slot is written twice.
+__device__ __forceinline__ float row_sum_all(float v, float* slot, int wpr) {
+  v = wave_sum(v);
+  if (wpr > 1) {
+    if ((threadIdx.x & (kWave - 1)) == 0) slot[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = slot[0];
+    for (int q = 1; q < wpr; ++q) v += slot[q];
+  }
+  return v;
+}
+
+__device__ __forceinline__ float row_max_all(float v, float* slot, int wpr) {
+  v = wave_max(v);
+  if (wpr > 1) {
+    if ((threadIdx.x & (kWave - 1)) == 0) slot[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = slot[0];
+    for (int q = 1; q < wpr; ++q) v = fmaxf(v, slot[q]);
+  }
+  return v;
 }
 
 // Streaming access for rows longer than the register cache: chunk c of a row
@@ -145,32 +199,33 @@ __device__ __forceinline__ int64_t unit_index() {
 // ---------------------------------------------------------------------------
 // Softmax: max, sum of exp(x - max), then exp(x - max) * (1 / sum), as
 // helion_mlir_utils/normalization.py:47-72 computes it (f32 inside, one
-// rounding), with the row held in registers between the passes.
+// rounding), with the row held in registers between the passes. The grid
+// holds exactly the rows (wpr > 1: one workgroup per row), so no thread that
+// reaches a barrier has returned early.
 template <typename T, int EPV, int VPL, bool WHOLE>
-__global__ __launch_bounds__(kBlock) void softmax_cached(const T* x,
-                                                         T* y, int64_t m,
-                                                         int64_t n) {
-  const int64_t row = unit_index();
-  if (row >= m) return;
-  const int lane = threadIdx.x & (kWave - 1);
+__global__ __launch_bounds__(kMaxBlock) void softmax_cached(const T* x, T* y, int64_t m,
+                                                            int64_t n, int wpr) {
+  __shared__ float red_max[kMaxWavesPerRow], red_sum[kMaxWavesPerRow];
+  const RowPos p = row_pos(wpr);
+  if (p.row >= m) return;
   float v[VPL * EPV];
-  load_row<T, EPV, VPL, WHOLE>(x + row * n, n, lane, v, -INFINITY);
+  load_row<T, EPV, VPL, WHOLE>(x + p.row * n, n, p.li, p.tpr, v, -INFINITY);
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) mx = fmaxf(mx, v[i]);
-  mx = wave_max(mx);
+  mx = row_max_all(mx, red_max, wpr);
   const float ml = mx * kLog2e;
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) {
     v[i] = exp_shifted(v[i], ml);
-    if (WHOLE || col_of<EPV>(i / EPV, lane, i % EPV) < n) sum += v[i];
+    if (WHOLE || col_of<EPV>(i / EPV, p.li, p.tpr, i % EPV) < n) sum += v[i];
   }
-  sum = wave_sum(sum);
+  sum = row_sum_all(sum, red_sum, wpr);
   const float inv = 1.f / sum;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) v[i] *= inv;
-  store_row<T, EPV, VPL, WHOLE>(y + row * n, n, lane, v);
+  store_row<T, EPV, VPL, WHOLE>(y + p.row * n, n, p.li, p.tpr, v);
 }
 
 template <typename T, int EPV>
@@ -210,60 +265,27 @@ __global__ __launch_bounds__(kBlock) void softmax_stream(const T* x,
 
 // ---------------------------------------------------------------------------
 // RMSNorm: x * rsqrt(mean(x^2) + eps) * w in f32, rounded once. The weight
-// (storage type W; null for none) is read with the same per-lane column map as
-// x, so its loads are vectors too.
+// (storage type W; null for none) is read with the same per-thread column map
+// as x, so its loads are vectors too.
 template <typename T, typename W, int EPV, int VPL, bool WHOLE>
-__global__ __launch_bounds__(kBlock) void rmsnorm_cached(const T* x, const W* __restrict__ w,
-                                                         bool w_vec, T* y, int64_t m,
-                                                         int64_t n, float eps) {
-  const int64_t row = unit_index();
-  if (row >= m) return;
-  const int lane = threadIdx.x & (kWave - 1);
-  if constexpr (WHOLE && EPV > 1) {
-    // Whole rows stay packed in registers (half the VGPRs of f32 for bf16)
-    // and are unpacked once per pass.
-    const uint4* xr = reinterpret_cast<const uint4*>(x + row * n) + lane;
-    uint4 raw[VPL];
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) raw[j] = xr[j * kWave];
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      float t[EPV];
-      Elem<T>::unpack(raw[j], t);
-#pragma unroll
-      for (int e = 0; e < EPV; ++e) ss = __builtin_fmaf(t[e], t[e], ss);
-    }
-    const float r = rsqrtf(wave_sum(ss) / (float)n + eps);
-    uint4* yr = reinterpret_cast<uint4*>(y + row * n) + lane;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      float t[EPV], wv[EPV];
-      Elem<T>::unpack(raw[j], t);
-      if (w != nullptr) {
-        load_vec_run<W, EPV>(w, n, col_of<EPV>(j, lane, 0), w_vec, wv);
-      } else {
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) wv[e] = 1.f;
-      }
-#pragma unroll
-      for (int e = 0; e < EPV; ++e) t[e] = t[e] * r * wv[e];
-      store16_stream(yr + j * kWave, Elem<T>::pack(t));
-    }
-    return;
-  }
+__global__ __launch_bounds__(kMaxBlock) void rmsnorm_cached(const T* x, const W* __restrict__ w,
+                                                            bool w_vec, T* y, int64_t m,
+                                                            int64_t n, float eps, int wpr) {
+  __shared__ float red_sum[kMaxWavesPerRow];
+  const RowPos p = row_pos(wpr);
+  if (p.row >= m) return;
   float v[VPL * EPV];
-  load_row<T, EPV, VPL, WHOLE>(x + row * n, n, lane, v, 0.f);
+  load_row<T, EPV, VPL, WHOLE>(x + p.row * n, n, p.li, p.tpr, v, 0.f);
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) ss = __builtin_fmaf(v[i], v[i], ss);
-  ss = wave_sum(ss);
+  ss = row_sum_all(ss, red_sum, wpr);
   const float r = rsqrtf(ss / (float)n + eps);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     float wv[EPV];
     if (w != nullptr) {
-      load_vec_run<W, EPV>(w, n, col_of<EPV>(j, lane, 0), w_vec, wv);
+      load_vec_run<W, EPV>(w, n, col_of<EPV>(j, p.li, p.tpr, 0), w_vec, wv);
     } else {
 #pragma unroll
       for (int e = 0; e < EPV; ++e) wv[e] = 1.f;
@@ -271,7 +293,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_cached(const T* x, const W* __
 #pragma unroll
     for (int e = 0; e < EPV; ++e) v[j * EPV + e] = v[j * EPV + e] * r * wv[e];
   }
-  store_row<T, EPV, VPL, WHOLE>(y + row * n, n, lane, v);
+  store_row<T, EPV, VPL, WHOLE>(y + p.row * n, n, p.li, p.tpr, v);
 }
 
 template <typename T, typename W, int EPV>
@@ -334,37 +356,37 @@ __device__ __forceinline__ float group_norm_out(const GroupNormArgs& a, float ce
   return apply_activation(a.act, yv, a.act_arg);
 }
 
-template <typename T, int EPV, int VPL>
-__global__ __launch_bounds__(kBlock) void group_norm_cached(const T* x,
-                                                            T* y,
-                                                            GroupNormArgs a) {
-  const int64_t unit = unit_index();
+template <typename T, int EPV, int VPL, bool WHOLE>
+__global__ __launch_bounds__(kMaxBlock) void group_norm_cached(const T* x, T* y, GroupNormArgs a,
+                                                               int wpr) {
+  __shared__ float red_mean[kMaxWavesPerRow], red_var[kMaxWavesPerRow];
+  const RowPos p = row_pos(wpr);
+  const int64_t unit = p.row;
   if (unit >= a.units) return;
-  const int lane = threadIdx.x & (kWave - 1);
   const int64_t g = unit % a.groups;
   const int64_t n = a.gs;
   float v[VPL * EPV];
-  load_row<T, EPV, VPL>(x + unit * n, n, lane, v, 0.f);
+  load_row<T, EPV, VPL, WHOLE>(x + unit * n, n, p.li, p.tpr, v, 0.f);
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) s += v[i];
-  const float mean = wave_sum(s) / (float)n;
+  const float mean = row_sum_all(s, red_mean, wpr) / (float)n;
   float q = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) {
     const float c = v[i] - mean;
-    if (col_of<EPV>(i / EPV, lane, i % EPV) < n) q += c * c;
+    if (WHOLE || col_of<EPV>(i / EPV, p.li, p.tpr, i % EPV) < n) q += c * c;
   }
-  const float r = rsqrtf(wave_sum(q) / (float)n + a.eps);
+  const float r = rsqrtf(row_sum_all(q, red_var, wpr) / (float)n + a.eps);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
 #pragma unroll
     for (int e = 0; e < EPV; ++e) {
-      const int64_t col = col_of<EPV>(j, lane, e);
-      if (col < n) v[j * EPV + e] = group_norm_out(a, v[j * EPV + e] - mean, r, g * n + col);
+      const int64_t col = col_of<EPV>(j, p.li, p.tpr, e);
+      if (WHOLE || col < n) v[j * EPV + e] = group_norm_out(a, v[j * EPV + e] - mean, r, g * n + col);
     }
   }
-  store_row<T, EPV, VPL>(y + unit * n, n, lane, v);
+  store_row<T, EPV, VPL, WHOLE>(y + unit * n, n, p.li, p.tpr, v);
 }
 
 template <typename T, int EPV>
@@ -479,29 +501,68 @@ __global__ __launch_bounds__(256) void elementwise_kernel(const T* x,
 // ---------------------------------------------------------------------------
 // Host dispatch.
 
-// The smallest vectors-per-lane that holds an n-element row in registers, or
-// 0 if the row needs the streaming kernel.
-int pick_vpl(int64_t n, int epv) {
-  for (int vpl = 1; vpl * epv <= kMaxPerLane; vpl *= 2)
-    if ((int64_t)kWave * vpl * epv >= n) return vpl;
-  return 0;
+// Layout of a cached row kernel for rows of n elements in vectors of epv:
+// one wave per row (four rows per workgroup) while a row is at most two
+// vectors per lane; longer rows get a workgroup of wpr waves with two vectors
+// per lane, wpr doubling up to 16, then more vectors per lane up to
+// kMaxPerLane values. vpl == 0: the row needs the streaming kernel.
+struct RowShape {
+  int wpr;
+  int vpl;
+  bool whole;  // n == wpr * 64 * vpl * epv with 16-byte vectors: no guards
+};
+
+RowShape row_shape(int64_t n, int epv) {
+  const int64_t vecs = ceil_div(n, epv);
+  RowShape r{1, 0, false};
+  if (vecs <= 2 * kWave) {
+    r.vpl = vecs <= kWave ? 1 : 2;
+  } else {
+    r.wpr = 2;
+    while (r.wpr < kMaxWavesPerRow && (int64_t)r.wpr * kWave * 2 < vecs) r.wpr *= 2;
+    for (int vpl = 2; vpl * epv <= kMaxPerLane; vpl *= 2)
+      if ((int64_t)r.wpr * kWave * vpl >= vecs) {
+        r.vpl = vpl;
+        break;
+      }
+  }
+  r.whole = r.vpl > 0 && epv > 1 && n == (int64_t)r.wpr * kWave * r.vpl * epv;
+  return r;
 }
+
+// Workgroups and threads per workgroup of a cached kernel over `units` rows.
+int64_t row_grid(int64_t units, const RowShape& r) {
+  return r.wpr == 1 ? ceil_div(units, kRowsPerBlock) : units;
+}
+unsigned row_block(const RowShape& r) { return r.wpr == 1 ? kBlock : r.wpr * kWave; }
 
 template <int V>
 using IntC = std::integral_constant<int, V>;
 
-// Calls f(IntC<VPL>) for the runtime vpl (a power of two, VPL * EPV <= 64).
+// Calls f(IntC<VPL>) for the runtime vpl (a power of two, VPL * EPV <= kMaxPerLane).
 template <int EPV, typename F>
 void with_vpl(int vpl, F&& f) {
   switch (vpl) {
     case 1: f(IntC<1>{}); break;
     case 2: f(IntC<2>{}); break;
-    case 4: f(IntC<4>{}); break;
-    case 8: f(IntC<8>{}); break;
+    case 4: if constexpr (4 * EPV <= kMaxPerLane) f(IntC<4>{}); break;
+    case 8: if constexpr (8 * EPV <= kMaxPerLane) f(IntC<8>{}); break;
     case 16: if constexpr (16 * EPV <= kMaxPerLane) f(IntC<16>{}); break;
-    case 32: if constexpr (32 * EPV <= kMaxPerLane) f(IntC<32>{}); break;
-    case 64: if constexpr (64 * EPV <= kMaxPerLane) f(IntC<64>{}); break;
   }
+}
+
+// Calls f(IntC<VPL>, bool_constant<WHOLE>) for a cached row shape.
+template <int EPV, typename F>
+void with_shape(const RowShape& r, F&& f) {
+  with_vpl<EPV>(r.vpl, [&](auto vpl_c) {
+    if constexpr (EPV > 1) {
+      if (r.whole) {
+        f(vpl_c, std::true_type{});
+        return;
+      }
+    }
+    f(vpl_c, std::false_type{});
+  });
 }
 
 // Calls f(T*, IntC<EPV>) for the dtype and whether 16-byte vectors apply.
@@ -524,6 +585,9 @@ bool rows_vectorizable(const void* p, const void* q, int64_t n, int dtype) {
 
 dim3 unit_grid(int64_t units) { return dim3((unsigned)ceil_div(units, kRowsPerBlock)); }
 
+// The largest workgroup count of a one-dimensional launch.
+constexpr int64_t kMaxGrid = 0x7fffffff;
+
 }  // namespace
 }  // namespace hmx
 
@@ -537,27 +601,21 @@ int hmx_softmax_rows(int dtype, const void* x, void* y, int64_t m, int64_t n,
   HMX_REQUIRE(m >= 0 && n >= 1, "softmax: invalid shape [%lld, %lld]", (long long)m,
               (long long)n);
   HMX_REQUIRE(x && y, "softmax: null operand");
-  HMX_REQUIRE(m <= ((int64_t)1 << 31) * kRowsPerBlock, "softmax: too many rows");
+  HMX_REQUIRE(m <= kMaxGrid, "softmax: too many rows");
   if (m == 0) return HMX_OK;
   auto s = (hipStream_t)stream;
   with_type(dtype, rows_vectorizable(x, y, n, dtype), [&](auto tp, auto epv_c) {
     using T = std::remove_pointer_t<decltype(tp)>;
     constexpr int EPV = decltype(epv_c)::value;
-    const int vpl = pick_vpl(n, EPV);
-    if (vpl == 0) {
+    const RowShape r = row_shape(n, EPV);
+    if (r.vpl == 0) {
       softmax_stream<T, EPV><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, (T*)y, m, n);
-    } else {
-      with_vpl<EPV>(vpl, [&](auto vpl_c) {
-        constexpr int VPL = decltype(vpl_c)::value;
-        if constexpr (EPV > 1) {
-          if (n == (int64_t)kWave * VPL * EPV) {
-            softmax_cached<T, EPV, VPL, true><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, (T*)y, m, n);
-            return;
-          }
-        }
-        softmax_cached<T, EPV, VPL, false><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, (T*)y, m, n);
-      });
+      return;
     }
+    with_shape<EPV>(r, [&](auto vpl_c, auto whole_c) {
+      softmax_cached<T, EPV, decltype(vpl_c)::value, decltype(whole_c)::value>
+          <<<dim3((unsigned)row_grid(m, r)), row_block(r), 0, s>>>((const T*)x, (T*)y, m, n, r.wpr);
+    });
   });
   return check_launch("softmax");
 }
@@ -569,7 +627,7 @@ int hmx_rmsnorm_rows(int dtype, const void* x, const void* w, int w_dtype, void*
   HMX_REQUIRE(m >= 0 && n >= 1, "rms_norm: invalid shape [%lld, %lld]", (long long)m,
               (long long)n);
   HMX_REQUIRE(x && y, "rms_norm: null operand");
-  HMX_REQUIRE(m <= ((int64_t)1 << 31) * kRowsPerBlock, "rms_norm: too many rows");
+  HMX_REQUIRE(m <= kMaxGrid, "rms_norm: too many rows");
   if (m == 0) return HMX_OK;
   auto s = (hipStream_t)stream;
   const bool w_vec = aligned16(w);
@@ -578,24 +636,17 @@ int hmx_rmsnorm_rows(int dtype, const void* x, const void* w, int w_dtype, void*
     constexpr int EPV = decltype(epv_c)::value;
     auto launch = [&](auto wp) {
       using W = std::remove_pointer_t<decltype(wp)>;
-      const int vpl = pick_vpl(n, EPV);
-      if (vpl == 0) {
+      const RowShape r = row_shape(n, EPV);
+      if (r.vpl == 0) {
         rmsnorm_stream<T, W, EPV><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, (const W*)w, w_vec,
                                                                    (T*)y, m, n, eps);
-      } else {
-        with_vpl<EPV>(vpl, [&](auto vpl_c) {
-          constexpr int VPL = decltype(vpl_c)::value;
-          if constexpr (EPV > 1) {
-            if (n == (int64_t)kWave * VPL * EPV) {
-              rmsnorm_cached<T, W, EPV, VPL, true><<<unit_grid(m), kBlock, 0, s>>>(
-                  (const T*)x, (const W*)w, w_vec, (T*)y, m, n, eps);
-              return;
-            }
-          }
-          rmsnorm_cached<T, W, EPV, VPL, false><<<unit_grid(m), kBlock, 0, s>>>(
-              (const T*)x, (const W*)w, w_vec, (T*)y, m, n, eps);
-        });
+        return;
       }
+      with_shape<EPV>(r, [&](auto vpl_c, auto whole_c) {
+        rmsnorm_cached<T, W, EPV, decltype(vpl_c)::value, decltype(whole_c)::value>
+            <<<dim3((unsigned)row_grid(m, r)), row_block(r), 0, s>>>(
+                (const T*)x, (const W*)w, w_vec, (T*)y, m, n, eps, r.wpr);
+      });
     };
     if (w != nullptr && w_dtype == HMX_DTYPE_BF16)
       launch((uint16_t*)nullptr);
@@ -618,7 +669,7 @@ int hmx_group_norm_rows(int dtype, const void* x, const void* w, const void* b,
               "group_norm: extra op without an extra operand");
   HMX_REQUIRE(valid_activation(activation), "group_norm: unknown activation %d", activation);
   const int64_t units = m * groups;
-  HMX_REQUIRE(units <= ((int64_t)1 << 31) * kRowsPerBlock, "group_norm: too many rows");
+  HMX_REQUIRE(units <= kMaxGrid, "group_norm: too many rows");
   if (units == 0) return HMX_OK;
   GroupNormArgs a{w, b, extra, vec_dtype, units, groups, group_size, eps,
                   extra_op, activation, activation_arg};
@@ -626,15 +677,15 @@ int hmx_group_norm_rows(int dtype, const void* x, const void* w, const void* b,
   with_type(dtype, rows_vectorizable(x, y, group_size, dtype), [&](auto tp, auto epv_c) {
     using T = std::remove_pointer_t<decltype(tp)>;
     constexpr int EPV = decltype(epv_c)::value;
-    const int vpl = pick_vpl(group_size, EPV);
-    if (vpl == 0) {
+    const RowShape r = row_shape(group_size, EPV);
+    if (r.vpl == 0) {
       group_norm_stream<T, EPV><<<unit_grid(units), kBlock, 0, s>>>((const T*)x, (T*)y, a);
-    } else {
-      with_vpl<EPV>(vpl, [&](auto vpl_c) {
-        group_norm_cached<T, EPV, decltype(vpl_c)::value>
-            <<<unit_grid(units), kBlock, 0, s>>>((const T*)x, (T*)y, a);
-      });
+      return;
     }
+    with_shape<EPV>(r, [&](auto vpl_c, auto whole_c) {
+      group_norm_cached<T, EPV, decltype(vpl_c)::value, decltype(whole_c)::value>
+          <<<dim3((unsigned)row_grid(units, r)), row_block(r), 0, s>>>((const T*)x, (T*)y, a, r.wpr);
+    });
   });
   return check_launch("group_norm");
 }

@@ -35,7 +35,9 @@ def _tol(dtype: str) -> tuple[float, float]:
 @pytest.mark.parametrize(
     ("m", "n", "shift"),
     [(130, 515, 0.0), (4, 129, -50.0), (2, 200, -50.0), (4, 256, -50.0), (3, 47, 0.0),
-     (7, 4096, 0.0), (5, 4097, 3.0), (3, 9000, 0.0), (64, 1, 0.0), (1, 64, 0.0), (33, 8, 100.0)],
+     (7, 4096, 0.0), (5, 4097, 3.0), (3, 9000, 0.0), (64, 1, 0.0), (1, 64, 0.0), (33, 8, 100.0),
+     # one row per workgroup of 2..16 waves (whole and ragged), then the streaming kernel
+     (3, 1024, 0.0), (2, 2048, 0.0), (2, 2056, 0.0), (2, 16384, 0.0), (2, 16388, 0.0), (2, 33000, 0.0)],
 )
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_softmax_matches_oracle(gpu_device, m: int, n: int, shift: float, dtype: str) -> None:
@@ -64,7 +66,8 @@ def test_softmax_nonfinite_and_one_column(gpu_device, dtype: str) -> None:
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-@pytest.mark.parametrize("shape", [(32, 128), (64, 256), (16, 129), (33, 257), (2, 65), (1, 127), (5, 2)])
+@pytest.mark.parametrize("shape", [(32, 128), (64, 256), (16, 129), (33, 257), (2, 65), (1, 127), (5, 2),
+                                   (4, 4096), (2, 9000)])
 def test_softmax_in_place_is_the_out_of_place_result(gpu_device, shape, dtype: str) -> None:
     # test_cpu_utils_softmax.py:58-76: in place is bit-equal, the input of the
     # out-of-place call is left alone.
@@ -97,7 +100,8 @@ def test_softmax_config2_full_size(gpu_device, dtype: str) -> None:
 # RMSNorm
 
 
-@pytest.mark.parametrize(("m", "n"), [(17, 333), (8, 4096), (3, 5000), (64, 64), (5, 3), (2, 12000)])
+@pytest.mark.parametrize(("m", "n"), [(17, 333), (8, 4096), (3, 5000), (64, 64), (5, 3), (2, 12000),
+                                     (4, 1024), (3, 16384), (2, 16400)])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("scale", [2.0, 1e-4])
 def test_rms_norm_matches_oracle(gpu_device, m: int, n: int, dtype: str, scale: float) -> None:
@@ -130,7 +134,8 @@ def test_rms_norm_config2_full_size(gpu_device, dtype: str) -> None:
 # GroupNorm / LayerNorm
 
 
-@pytest.mark.parametrize(("m", "c", "groups"), [(32, 256, 16), (33, 256, 4), (64, 512, 512), (5, 96, 3), (2, 65, 5), (4, 8192, 1)])
+@pytest.mark.parametrize(("m", "c", "groups"), [(32, 256, 16), (33, 256, 4), (64, 512, 512), (5, 96, 3), (2, 65, 5), (4, 8192, 1),
+                                                 (3, 2048, 2), (2, 16384, 1), (2, 20000, 1)])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_group_norm_matches_oracle(gpu_device, m: int, c: int, groups: int, dtype: str) -> None:
     x = tensor((RNG.normal(0, 3, (m, c)) + 1.5).astype(np.float32), dtype, gpu_device)
