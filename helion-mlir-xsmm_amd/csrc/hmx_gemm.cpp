@@ -19,7 +19,7 @@ constexpr TileChoice kBf16Tiles[] = {{256, 256, 64}, {128, 128, 64}};
 constexpr TileChoice kF32Tiles[] = {{128, 128, 32}};
 // The f32 tile long-K split-K products of whole 256 x 256 tiles take (see
 // make_plan): one workgroup per CU reading each operand once.
-constexpr TileChoice kF32Big = {256, 256, 16};
+constexpr TileChoice kF32Big = {256, 256, 32};
 constexpr int kCus = 256;  // MI355X compute units
 
 int layout_code(int b_layout) {

@@ -262,7 +262,7 @@ void dispatch_f32(const GemmArgs& g, int la, int lb, bool guard, dim3 grid, hipS
 void launch_gemm_f32(const GemmArgs& g, int tile_bm, int la, int lb, bool guard, dim3 grid,
                      hipStream_t s) {
   if (tile_bm == 256)
-    dispatch_f32<F32Cfg<256, 256, 16>>(g, la, lb, guard, grid, s);
+    dispatch_f32<F32Cfg<256, 256, 32>>(g, la, lb, guard, grid, s);
   else
     dispatch_f32<F32Cfg<128, 128, 32>>(g, la, lb, guard, grid, s);
 }
