@@ -307,7 +307,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, float* lds, int spli
 // (packed B layouts at 256 x 256 only).
 void launch_gemm_bf16(const GemmArgs& g, int tile_bm, int la, int lb, bool guard, dim3 grid,
                       hipStream_t s);
-// hmx_gemm_dma.hip: direct-to-LDS bf16 kernel; whole 256 x 256 tiles, A
+// hmx_gemm_dma.hip: direct-to-LDS bf16 kernels (64-wide K stages when K
+// chunks are whole 64-element stages, else 32-wide); whole 256 x 256 tiles, A
 // K-contiguous, B K-contiguous or row-major, identity / ReLU / SiLU epilogue.
 void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s);
 // hmx_gemm_f32.hip: f32 kernel, tiles 128 x 128 or (split-K partials only)

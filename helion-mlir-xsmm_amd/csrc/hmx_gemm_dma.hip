@@ -1,8 +1,10 @@
-// Direct-to-LDS bf16 GEMM kernel for gfx950 (v_mfma_f32_32x32x16_bf16):
+// Direct-to-LDS bf16 GEMM kernels for gfx950 (v_mfma_f32_32x32x16_bf16):
 // whole 256 x 256 tiles of row-major A and a B that is either K-contiguous
-// ([N, K]) or row-major ([K, N]). Operand tiles go from memory straight into LDS (`buffer_load_dwordx4 ... lds`), with no VGPR
-// staging and no LDS write instructions. Four LDS stages of BK = 32 keep
-// three tiles in flight.
+// ([N, K]) or row-major ([K, N]). Operand tiles go from memory straight into
+// LDS (`buffer_load_dwordx4 ... lds`), with no VGPR staging and no LDS write
+// instructions. Two variants: 64-wide K stages (two stages of 64 KiB, below)
+// for K chunks of whole 64-element stages, and 32-wide K tiles (four stages
+// of 32 KiB, three in flight) otherwise.
 //
 // LDS tiles are unpadded: one such load fills 1 KiB of LDS contiguously
 // (lane l at byte 16 l), so bank conflicts are avoided by XOR-swizzling
@@ -26,6 +28,8 @@
 // otherwise wait for every outstanding LDS load (vmcnt(0)) before any LDS
 // read, which leaves nothing in flight. Loads complete in issue order, so the
 // compiler's own waits for other memory operations stay correct.
+#include <cstdlib>
+
 #include "hmx_gemm_common.hpp"
 
 namespace hmx {
@@ -58,6 +62,7 @@ __device__ __forceinline__ void wait_vmem() {
 
 __device__ __forceinline__ int swz_k(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
 __device__ __forceinline__ int swz_n(int r) { return ((r & 3) << 1) ^ ((r & 3) << 2); }
+__device__ __forceinline__ int swz64(int r) { return (r >> 1) & 7; }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
@@ -216,31 +221,212 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(GemmArgs g) {
   epilogue_direct<FM, FN, WM, WN, false, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
 }
 
-template <int LB, bool BF16>
+// ---------------------------------------------------------------------------
+// 64-wide K stages. The same operand handling with BK = 64 in two LDS stages
+// of 64 KiB: every K-contiguous load fetches whole 128-byte pieces of 8 rows,
+// so a cache line is requested once even when no other workgroup shares it
+// (split-K over long K streams each workgroup's own rows: with 32-wide tiles
+// each 64-byte half of a line was a separate request for the same line), and
+// a step has one barrier per 64 MFMAs.
+// K-contiguous tiles: [256 rows][64 k], 128-byte rows; 16-byte chunk c of row
+// r sits in slot c ^ swz64(r), swz64(r) = (r >> 1) & 7, so a fragment read
+// (row lane % 32, one chunk) meets distinct banks across 16 lanes. Row-major
+// B: [64 k][256 n], 512-byte rows swizzled as in the 32-wide kernel.
+//
+// Step t (64 MFMA slots, k-steps of 16): slots 0-7, 16-23 and 32-39 read the
+// next k-step's fragments (two register sets alternate); before slot 44 the
+// wave waits for its loads of stage t + 1 and its reads of stage t, and the
+// barrier both publishes stage t + 1 and frees stage t; slots 44-59 issue the
+// loads of stage t + 2 into it and slots 56-63 read stage t + 1's first
+// fragments. The loads of a stage have ~one step to land.
+template <int LB, int ACT, bool BF16>
+__global__ __launch_bounds__(256, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
+  constexpr bool BT = LB == L_RCONTIG;             // B row-major [K, N]
+  constexpr int BM = 256, BN = 256, BK = 64;
+  constexpr int ROWB = BK * 2;                     // bytes per K-contiguous tile row
+  constexpr int NROWB = BN * 2;                    // bytes per row-major B tile row
+  constexpr int A_BYTES = BM * ROWB;               // 32 KiB
+  constexpr int STAGE = A_BYTES + BN * BK * 2;     // 64 KiB
+  constexpr int FM = 4, FN = 4, WM = 128, WN = 128;
+  constexpr int LOADS = 16;                        // DMA instructions per wave per stage
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
+
+  int tm, tn;
+  tile_coords(g.tiles_m, g.tiles_n, tm, tn);
+  const int split = blockIdx.y, batch = blockIdx.z;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t k_begin = (int64_t)split * g.k_chunk;
+  const int64_t k_end = min(g.k, k_begin + g.k_chunk);
+  const int ktiles = (int)((k_end - k_begin) / BK);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const i32x4_t srd_a = make_srd((const uint16_t*)g.a.p + batch * g.stride_a, g.a.bytes);
+  const i32x4_t srd_b = make_srd((const uint16_t*)g.b.p + batch * g.stride_b, g.b.bytes);
+  // K-contiguous operands: wave w loads tile rows 64 w .. 64 w + 63, 8 rows
+  // per load: lane l fills slot l % 8 of row 64 w + 8 q + l / 8 of load q,
+  // whose swizzle is (l / 16) | 4 (q & 1). Byte offsets below 2^31: the
+  // operands' byte ranges are.
+  const int rr = lane >> 3, slot = lane & 7;
+  auto kc_voff = [&](int64_t ld, int par) {
+    return (int32_t)((rr * ld + (slot ^ ((rr >> 1) | (par << 2))) * 8) * 2);
+  };
+  const int32_t voff_a0 = kc_voff(g.a.ld, 0), voff_a1 = kc_voff(g.a.ld, 1);
+  const int32_t soff_a = (int32_t)((m0 + wave * 64) * g.a.ld * 2);
+  const int32_t blk_a = (int32_t)(8 * g.a.ld * 2);
+  // B: K-contiguous as A; row-major: wave w loads K rows 16 w .. 16 w + 15
+  // in pairs 16 w + 2 q, 16 w + 2 q + 1, lane l filling slot l % 32 of row
+  // l / 32 of the pair.
+  int32_t voff_b0, voff_b1, soff_b, blk_b;
+  if constexpr (BT) {
+    const int r = lane >> 5, c = lane & 31;
+    voff_b0 = (int32_t)((r * g.b.ld + (c ^ swz_n(r)) * 8) * 2);      // even q
+    voff_b1 = (int32_t)((r * g.b.ld + (c ^ swz_n(r + 2)) * 8) * 2);  // odd q
+    soff_b = (int32_t)((wave * 16 * g.b.ld + n0) * 2);
+    blk_b = (int32_t)(2 * g.b.ld * 2);
+  } else {
+    voff_b0 = kc_voff(g.b.ld, 0);
+    voff_b1 = kc_voff(g.b.ld, 1);
+    soff_b = (int32_t)((n0 + wave * 64) * g.b.ld * 2);
+    blk_b = (int32_t)(8 * g.b.ld * 2);
+  }
+  const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + wave * 8 * 1024;
+
+  // DMA q (< 16) of stage t: A for q < 8, then B.
+  auto dma = [&](int t, int q) {
+    const int64_t k0 = k_begin + (int64_t)min(t, ktiles - 1) * BK;
+    const uint32_t st = lds_w + (uint32_t)((t & 1) * STAGE);
+    if (q < 8) {
+      lds_dma16(srd_a, (q & 1) ? voff_a1 : voff_a0, soff_a + q * blk_a + (int32_t)(k0 * 2), st + q * 1024);
+    } else {
+      const int qb = q - 8;
+      const int32_t kb = BT ? (int32_t)(k0 * g.b.ld * 2) : (int32_t)(k0 * 2);
+      lds_dma16(srd_b, (qb & 1) ? voff_b1 : voff_b0, soff_b + qb * blk_b + kb,
+                st + A_BYTES + qb * 1024);
+    }
+  };
+
+  f32x16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Fragment reads. A (and K-contiguous B): row lane % 32 of the fragment,
+  // chunk 2 ks + lane / 32 (ks < 4).
+  const int frow = lane & 31, fk = lane >> 5, fswz = swz64(frow);
+  const uint8_t* a_frag = lds + (wm * WM + frow) * ROWB;
+  const uint8_t* b_frag = lds + A_BYTES + (wn * WN + frow) * ROWB;
+  int b_tr[FN];
+  {
+    const int gi = lane >> 4, sl = lane & 15;
+    const int v = (2 * (gi & 1) + ((sl & 3) >> 1)) ^ swz_n(sl >> 2);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      b_tr[j] = A_BYTES + (8 * (gi >> 1) + (sl >> 2)) * NROWB + (wn * 16 + ((4 * j) ^ v)) * 16 + 8 * (sl & 1);
+  }
+  auto a_read = [&](int stage, int ks, int i) -> bf16x8_t {
+    return *(const bf16x8_t*)(a_frag + stage * STAGE + i * 32 * ROWB + ((2 * ks + fk) ^ fswz) * 16);
+  };
+  auto b_read = [&](int stage, int ks, int j) -> bf16x8_t {
+    if constexpr (BT) {
+      const uint8_t* p = lds + stage * STAGE + b_tr[j] + 16 * ks * NROWB;
+      return __builtin_shufflevector(lds_read_tr(p), lds_read_tr(p + 4 * NROWB), 0, 1, 2, 3, 4, 5, 6, 7);
+    } else {
+      return *(const bf16x8_t*)(b_frag + stage * STAGE + j * 32 * ROWB + ((2 * ks + fk) ^ fswz) * 16);
+    }
+  };
+
+  // The host launches this kernel only with at least one K stage per split.
+  bf16x8_t fa[2][FM], fb[2][FN];
+#pragma unroll
+  for (int q = 0; q < LOADS; ++q) dma(0, q);
+#pragma unroll
+  for (int q = 0; q < LOADS; ++q) dma(1, q);
+  wait_vmem<LOADS>();  // stage 0 landed
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < FM; ++i) fa[0][i] = a_read(0, 0, i);
+#pragma unroll
+  for (int j = 0; j < FN; ++j) fb[0][j] = b_read(0, 0, j);
+
+  for (int t = 0; t < ktiles; ++t) {
+    const int cur = t & 1, nxt = cur ^ 1;
+#pragma unroll
+    for (int x = 0; x < 64; ++x) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int ks = x >> 4, sub = x & 15, f = x & 7;
+      if (x == 44) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (ks < 3 && sub < 8) {
+        const int set = (ks + 1) & 1;
+        if (f < 4) fa[set][f] = a_read(cur, ks + 1, f);
+        else fb[set][f - 4] = b_read(cur, ks + 1, f - 4);
+      }
+      if (x >= 44 && x < 60) dma(t + 2, x - 44);
+      if (x >= 56) {
+        if (f < 4) fa[0][f] = a_read(nxt, 0, f);
+        else fb[0][f - 4] = b_read(nxt, 0, f - 4);
+      }
+      const int i = sub >> 2, j = sub & 3, set = ks & 1;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  wait_vmem<0>();  // no load into LDS outlives the loop
+  epilogue_direct<FM, FN, WM, WN, false, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
+}
+
+template <int LB, bool BF16, bool K64>
 void launch_bf16_dma_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
-  switch (g.act) {
-    case HMX_EPI_RELU: gemm_bf16_dma_kernel<LB, ACT_RELU, BF16><<<grid, 256, 0, s>>>(g); break;
-    case HMX_EPI_SILU: gemm_bf16_dma_kernel<LB, ACT_SILU, BF16><<<grid, 256, 0, s>>>(g); break;
-    default: gemm_bf16_dma_kernel<LB, ACT_ID, BF16><<<grid, 256, 0, s>>>(g); break;
+  if constexpr (K64) {
+    switch (g.act) {
+      case HMX_EPI_RELU: gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16><<<grid, 256, 0, s>>>(g); break;
+      case HMX_EPI_SILU: gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16><<<grid, 256, 0, s>>>(g); break;
+      default: gemm_bf16_dma64_kernel<LB, ACT_ID, BF16><<<grid, 256, 0, s>>>(g); break;
+    }
+  } else {
+    switch (g.act) {
+      case HMX_EPI_RELU: gemm_bf16_dma_kernel<LB, ACT_RELU, BF16><<<grid, 256, 0, s>>>(g); break;
+      case HMX_EPI_SILU: gemm_bf16_dma_kernel<LB, ACT_SILU, BF16><<<grid, 256, 0, s>>>(g); break;
+      default: gemm_bf16_dma_kernel<LB, ACT_ID, BF16><<<grid, 256, 0, s>>>(g); break;
+    }
   }
 }
 
-template <int LB>
+template <int LB, bool K64>
 void launch_bf16_dma_b(const GemmArgs& g, dim3 grid, hipStream_t s) {
   if (g.c_dtype == HMX_DTYPE_BF16)
-    launch_bf16_dma_c<LB, true>(g, grid, s);
+    launch_bf16_dma_c<LB, true, K64>(g, grid, s);
   else
-    launch_bf16_dma_c<LB, false>(g, grid, s);
+    launch_bf16_dma_c<LB, false, K64>(g, grid, s);
+}
+
+// The 64-wide kernel takes every K chunk of whole 64-element stages unless the
+// environment sets HMX_GEMM_DMA64=0 (which keeps the 32-wide kernel, for
+// comparison).
+bool dma64_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("HMX_GEMM_DMA64");
+    return !(e && e[0] == '0');
+  }();
+  return on;
 }
 
 }  // namespace
 
 void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {
-  if (lb == L_RCONTIG)
-    launch_bf16_dma_b<L_RCONTIG>(g, grid, s);
-  else
-    launch_bf16_dma_b<L_KCONTIG>(g, grid, s);
+  const bool k64 = g.k_chunk % 64 == 0 && g.k % 64 == 0 && dma64_enabled();
+  if (lb == L_RCONTIG) {
+    if (k64) launch_bf16_dma_b<L_RCONTIG, true>(g, grid, s);
+    else launch_bf16_dma_b<L_RCONTIG, false>(g, grid, s);
+  } else {
+    if (k64) launch_bf16_dma_b<L_KCONTIG, true>(g, grid, s);
+    else launch_bf16_dma_b<L_KCONTIG, false>(g, grid, s);
+  }
 }
-
 
 }  // namespace hmx
