@@ -143,9 +143,10 @@ def test_plans_of_the_baseline_configs(lib: ctypes.CDLL) -> None:
     # Fused linear, 8192 x 11008 x 4096 (B row-major here): 1376 tiles, no split.
     assert _plan(lib, bf16, 8192, 11008, 4096)[:4] == (1, 256, 256, 64)
     # Split-K bmm [16, 256, 65536] @ [16, 65536, 256]: one 256 x 256 tile per
-    # slice (each operand read once) x 16 splits = one workgroup per CU.
+    # slice (each operand read once) x 16 splits = one workgroup per CU; the
+    # f32 tile is 32 deep so each A row is read in whole 128-byte lines.
     s, tm, tn, tk, ws = _plan(lib, f32, 256, 256, 65536, batch=16)
-    assert (s, tm, tn, tk) == (16, 256, 256, 16) and ws == 16 * 16 * 256 * 256 * 4
+    assert (s, tm, tn, tk) == (16, 256, 256, 32) and ws == 16 * 16 * 256 * 256 * 4
     assert _plan(lib, bf16, 256, 256, 65536, batch=16)[:4] == (16, 256, 256, 64)
     # Too few K tiles to fill the GPU by splitting: the small tile.
     assert _plan(lib, f32, 256, 256, 4096, batch=16)[1:3] == (128, 128)
