@@ -14,9 +14,10 @@ softmax, softmax_f32, rmsnorm, rmsnorm_f32, bmm, bmm_bf16, matmul_f32.
 Timing: W untimed steps, then K steps bracketed by ``torch.cuda.synchronize()``
 and HIP events recorded on the stream the kernels run on (torch's current
 stream, which the library launches on); ``value`` spans all K steps. Each
-step also has its own event pair: ``roofline.achieved`` is the algorithmic
-work per launch of the dominant kernel over the mean of those pairs (its
-average launch duration); ``roofline.traffic`` is the HBM bytes per launch measured with
+step also has its own event pair, recorded by the step's first and last
+kernels themselves (``hmx_time_launches``): ``roofline.achieved`` is the
+algorithmic work per launch of the dominant kernel over the mean of those
+pairs (its average launch duration, as a kernel trace measures it); ``roofline.traffic`` is the HBM bytes per launch measured with
 rocprofv3 counters (``profiles/traffic.json``), or null when not measured.
 ``cpu_baseline`` times the CPU oracle (``oracle/restate.py``, numpy) on the
 host cores on a bounded sample of the same workload.
@@ -78,6 +79,7 @@ class Workload:
     dtype: str
     kernel: str  # the dominant kernel's name (rocprof)
     launches_per_step: int = 1
+    library_kernels: bool = True  # a step enqueues libhmx kernels
     config: dict
 
     def step(self) -> object:
@@ -119,7 +121,7 @@ class Gemm(Workload):
         self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_BF16_TFLOPS
         self.work = 2.0 * m * n * k
         self.dtype = "bf16"
-        self.kernel = "gemm_bf16_kernel" if prepacked else "gemm_bf16_dma_kernel"
+        self.kernel = "gemm_bf16_kernel" if prepacked else "gemm_bf16_dma64_kernel"
         self.config = {"workload": self.description, "m": m, "n": n, "k": k, "a": "bf16 row-major",
                        "b": "bf16 row-major" if not prepacked else "bf16 [N/32,K/32,16,32,2]",
                        "c": out_dtype_name, "seed": 2, "values": "U[-1,1]"}
@@ -162,7 +164,7 @@ class Linear(Workload):
         self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_BF16_TFLOPS
         self.work = 2.0 * 8192 * 11008 * 4096
         self.dtype = "bf16"
-        self.kernel = "gemm_bf16_dma_kernel"
+        self.kernel = "gemm_bf16_dma64_kernel"
         self.config = {"workload": self.description, "m": 8192, "n": 11008, "k": 4096, "seed": 3}
 
     def step(self):
@@ -247,10 +249,10 @@ class Bmm(Workload):
                             f"S={self.plan['splits']} (config 5)")
         if dtype_name == "f32":
             self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_F32_TFLOPS
-            self.kernel = "gemm_f32_kernel"
+            self.kernel = "gemm_f32_kernel + splitk_reduce_kernel"
         else:
             self.unit, self.bound, self.peak = "GB/s", "hbm", PEAK_HBM_GBS
-            self.kernel = "gemm_bf16_kernel"
+            self.kernel = "gemm_bf16_dma64_kernel + splitk_reduce_kernel"
         self.flops = 2.0 * 16 * 256 * 256 * 65536
         esz = 4 if dtype_name == "f32" else 2
         self.bytes = 16 * (256 * 65536 * 2) * esz + 16 * 256 * 256 * 4
@@ -323,6 +325,7 @@ class Copy(Workload):
         self.work = 2.0 * self.x.numel() * 2
         self.dtype = "bf16"
         self.kernel = "copy"
+        self.library_kernels = False
         self.config = {"workload": self.description, "bytes_read": self.x.numel() * 2, "bytes_written": self.x.numel() * 2}
 
     def step(self):
@@ -351,26 +354,47 @@ def make(name: str, device) -> Workload:
 
 def measure(w: Workload, steps: int, warmup: int) -> dict:
     """Step time (ms) over ``steps`` timed steps, and the average duration of
-    one step's launches, both from HIP events on the stream the library
+    one step's kernels, both from HIP events on the stream the library
     launches on (torch's current stream).
 
-    Each timed step is bracketed by its own pair of events, so ``launch_ms``
-    (the mean of the pairs) is the GPU time of the step's kernels without the
-    host's time between steps; ``ms`` spans the first event to the last.
+    ``ms`` spans the whole timed region (first event to last). For each step,
+    a pair of events is armed in the library (``hmx_time_launches``): the
+    first kernel of the step records the start event as it begins and its last
+    kernel the stop event as it ends, so ``launch_ms`` (the mean of the pairs)
+    is the GPU time of the step's kernels without dispatch latency or host
+    time -- what a kernel trace reports. Workloads that launch no library
+    kernel (the calibration copy) bracket the step with plain event records.
     """
     import torch
+
+    from helion_mlir_backend._compiler import native
 
     for _ in range(warmup):
         w.step()
     torch.cuda.synchronize()
+    begin = torch.cuda.Event(enable_timing=True)
+    finish = torch.cuda.Event(enable_timing=True)
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    armed = w.library_kernels
+    if armed:
+        for ev in starts + ends:  # creates the events; the kernels re-record them
+            ev.record()
+        torch.cuda.synchronize()
+    begin.record()
     for i in range(steps):
-        starts[i].record()
-        w.step()
-        ends[i].record()
+        if armed:
+            native.time_launches(starts[i], ends[i])
+            w.step()
+        else:
+            starts[i].record()
+            w.step()
+            ends[i].record()
+    if armed:
+        native.time_launches(None, None)
+    finish.record()
     torch.cuda.synchronize()
-    ms = starts[0].elapsed_time(ends[-1]) / steps
+    ms = begin.elapsed_time(finish) / steps
     launch_ms = sum(a.elapsed_time(b) for a, b in zip(starts, ends)) / steps
     scale = 1e12 if w.unit == "TFLOP/s" else 1e9
     value = w.work / (ms * 1e-3) / scale

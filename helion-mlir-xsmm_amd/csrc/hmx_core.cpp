@@ -1,4 +1,5 @@
-// libhmx core: error reporting, ABI version and the device check.
+// libhmx core: error reporting, ABI version, the device check and the
+// per-thread timing events of hmx_time_launches.
 #include <string.h>
 
 #include <string>
@@ -9,7 +10,10 @@ namespace hmx {
 
 namespace {
 thread_local char g_error[1024] = {0};
+thread_local LaunchEvents g_events = {nullptr, nullptr};
 }
+
+LaunchEvents& launch_events() { return g_events; }
 
 int set_error(int status, const char* fmt, ...) {
   va_list args;
@@ -35,6 +39,12 @@ extern "C" {
 const char* hmx_last_error(void) { return hmx::g_error; }
 
 int hmx_abi_version(void) { return HMX_ABI_VERSION; }
+
+int hmx_time_launches(void* start_event, void* stop_event) {
+  hmx::g_events.start = (hipEvent_t)start_event;
+  hmx::g_events.stop = (hipEvent_t)stop_event;
+  return HMX_OK;
+}
 
 int hmx_device_check(int* compute_units) {
   int device = 0;

@@ -304,7 +304,8 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
   auto s = (hipStream_t)stream;
   if (ab_dtype == HMX_DTYPE_BF16) {
     const TileChoice t = plan.tile;
-    if (t.bm == 256 && !guard && la == L_KCONTIG && (lb_run == L_KCONTIG || lb_run == L_RCONTIG) &&
+    if (t.bm == 256 && !guard && la == L_KCONTIG &&
+        (lb_run == L_KCONTIG || lb_run == L_RCONTIG || gemm_bf16_dma_vnni_ok(g, lb_run)) &&
         dma_direct_ok(g) && dma_enabled())
       launch_gemm_bf16_dma(g, lb_run, grid, s);
     else

@@ -353,9 +353,9 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm_bf16_kernel(GemmArgs g) {
 template <class Cfg, int LA, int LB>
 void launch_bf16(const GemmArgs& g, bool guard, dim3 grid, hipStream_t s) {
   if (guard)
-    gemm_bf16_kernel<Cfg, LA, LB, true><<<grid, Cfg::NT, 0, s>>>(g);
+    launch(gemm_bf16_kernel<Cfg, LA, LB, true>, grid, Cfg::NT, s, g);
   else
-    gemm_bf16_kernel<Cfg, LA, LB, false><<<grid, Cfg::NT, 0, s>>>(g);
+    launch(gemm_bf16_kernel<Cfg, LA, LB, false>, grid, Cfg::NT, s, g);
 }
 
 // Row-major or transposed A and B (L_KCONTIG / L_RCONTIG).

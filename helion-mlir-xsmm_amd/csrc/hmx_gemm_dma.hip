@@ -242,6 +242,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(GemmArgs g) {
 template <int LB, int ACT, bool BF16>
 __global__ __launch_bounds__(256, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
   constexpr bool BT = LB == L_RCONTIG;             // B row-major [K, N]
+  constexpr bool VN = LB == L_VNNI_PANELS;         // B in K-pair (VNNI) panels
   constexpr int BM = 256, BN = 256, BK = 64;
   constexpr int ROWB = BK * 2;                     // bytes per K-contiguous tile row
   constexpr int NROWB = BN * 2;                    // bytes per row-major B tile row
@@ -279,8 +280,33 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
   // B: K-contiguous as A; row-major: wave w loads K rows 16 w .. 16 w + 15
   // in pairs 16 w + 2 q, 16 w + 2 q + 1, lane l filling slot l % 32 of row
   // l / 32 of the pair.
+  // VNNI panels of width P ([N/P, Kp/2, P, 2]; the blocked VNNI layout is
+  // P = 32): a stage is 32 K pairs x 256 columns. For P <= 256 it is 256 / P
+  // runs of 32 pair rows x P columns, each one contiguous 128 P bytes of its
+  // panel; for wider panels, 32 pair rows of 256 columns (1 KiB each, 4 P
+  // bytes apart). Either way load q of wave w copies 1 KiB, the (8 w + q)-th
+  // of the stage in that order, to LDS unchanged: [256 / PL][32][PL][2] with
+  // PL = min(P, 256). Its byte offset is vn_off[q] + (k0 / 2) * 4 P.
   int32_t voff_b0, voff_b1, soff_b, blk_b;
-  if constexpr (BT) {
+  int32_t vn_off[8];
+  const int64_t P = g.b.panel;
+  const int PL = (int)min<int64_t>(P, 256);
+  if constexpr (VN) {
+    voff_b0 = voff_b1 = lane * 16;
+    soff_b = blk_b = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int64_t idx = wave * 8 + q;
+      int64_t off;
+      if (P <= 256) {
+        const int64_t b = idx * 1024, run = 128 * P;
+        off = ((n0 / P + b / run) * (g.b.kpad / 2)) * 4 * P + b % run;
+      } else {
+        off = ((n0 / P) * (g.b.kpad / 2) + idx) * 4 * P + (n0 % P) * 4;
+      }
+      vn_off[q] = (int32_t)off;
+    }
+  } else if constexpr (BT) {
     const int r = lane >> 5, c = lane & 31;
     voff_b0 = (int32_t)((r * g.b.ld + (c ^ swz_n(r)) * 8) * 2);      // even q
     voff_b1 = (int32_t)((r * g.b.ld + (c ^ swz_n(r + 2)) * 8) * 2);  // odd q
@@ -300,6 +326,9 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
     const uint32_t st = lds_w + (uint32_t)((t & 1) * STAGE);
     if (q < 8) {
       lds_dma16(srd_a, (q & 1) ? voff_a1 : voff_a0, soff_a + q * blk_a + (int32_t)(k0 * 2), st + q * 1024);
+    } else if constexpr (VN) {
+      const int qb = q - 8;
+      lds_dma16(srd_b, voff_b0, vn_off[qb] + (int32_t)((k0 / 2) * 4 * P), st + A_BYTES + qb * 1024);
     } else {
       const int qb = q - 8;
       const int32_t kb = BT ? (int32_t)(k0 * g.b.ld * 2) : (int32_t)(k0 * 2);
@@ -329,11 +358,29 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
     for (int j = 0; j < FN; ++j)
       b_tr[j] = A_BYTES + (8 * (gi >> 1) + (sl >> 2)) * NROWB + (wn * 16 + ((4 * j) ^ v)) * 16 + 8 * (sl & 1);
   }
+  // VNNI B: column n = wn * 128 + 32 j + lane % 32 needs K pairs
+  // 8 ks + 4 (lane / 32) .. + 3 (4 * PL bytes apart), i.e. K values
+  // 16 ks + 8 (lane / 32) .. + 7 -- the MFMA's operand.
+  int b_vn[FN];
+  const int pair_pitch = 4 * PL;
+  if constexpr (VN) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = wn * WN + 32 * j + frow;
+      b_vn[j] = A_BYTES + (n / PL) * 32 * pair_pitch + (n % PL) * 4 + 4 * fk * pair_pitch;
+    }
+  }
   auto a_read = [&](int stage, int ks, int i) -> bf16x8_t {
     return *(const bf16x8_t*)(a_frag + stage * STAGE + i * 32 * ROWB + ((2 * ks + fk) ^ fswz) * 16);
   };
   auto b_read = [&](int stage, int ks, int j) -> bf16x8_t {
-    if constexpr (BT) {
+    if constexpr (VN) {
+      const uint8_t* p = lds + stage * STAGE + b_vn[j] + 8 * ks * pair_pitch;
+      const uint4 v = make_uint4(*(const uint32_t*)p, *(const uint32_t*)(p + pair_pitch),
+                                 *(const uint32_t*)(p + 2 * pair_pitch),
+                                 *(const uint32_t*)(p + 3 * pair_pitch));
+      return __builtin_bit_cast(bf16x8_t, v);
+    } else if constexpr (BT) {
       const uint8_t* p = lds + stage * STAGE + b_tr[j] + 16 * ks * NROWB;
       return __builtin_shufflevector(lds_read_tr(p), lds_read_tr(p + 4 * NROWB), 0, 1, 2, 3, 4, 5, 6, 7);
     } else {
@@ -384,15 +431,15 @@ template <int LB, bool BF16, bool K64>
 void launch_bf16_dma_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
   if constexpr (K64) {
     switch (g.act) {
-      case HMX_EPI_RELU: gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16><<<grid, 256, 0, s>>>(g); break;
-      case HMX_EPI_SILU: gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16><<<grid, 256, 0, s>>>(g); break;
-      default: gemm_bf16_dma64_kernel<LB, ACT_ID, BF16><<<grid, 256, 0, s>>>(g); break;
+      case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16>, grid, 256, s, g); break;
+      case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16>, grid, 256, s, g); break;
+      default: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16>, grid, 256, s, g); break;
     }
-  } else {
+  } else if constexpr (LB != L_VNNI_PANELS) {
     switch (g.act) {
-      case HMX_EPI_RELU: gemm_bf16_dma_kernel<LB, ACT_RELU, BF16><<<grid, 256, 0, s>>>(g); break;
-      case HMX_EPI_SILU: gemm_bf16_dma_kernel<LB, ACT_SILU, BF16><<<grid, 256, 0, s>>>(g); break;
-      default: gemm_bf16_dma_kernel<LB, ACT_ID, BF16><<<grid, 256, 0, s>>>(g); break;
+      case HMX_EPI_RELU: launch(gemm_bf16_dma_kernel<LB, ACT_RELU, BF16>, grid, 256, s, g); break;
+      case HMX_EPI_SILU: launch(gemm_bf16_dma_kernel<LB, ACT_SILU, BF16>, grid, 256, s, g); break;
+      default: launch(gemm_bf16_dma_kernel<LB, ACT_ID, BF16>, grid, 256, s, g); break;
     }
   }
 }
@@ -418,7 +465,21 @@ bool dma64_enabled() {
 
 }  // namespace
 
+bool gemm_bf16_dma_vnni_ok(const GemmArgs& g, int lb) {
+  if (lb != L_VNNI_PANELS && lb != L_BLOCKED_VNNI) return false;
+  const int64_t p = lb == L_BLOCKED_VNNI ? 32 : g.b.panel;
+  return g.k_chunk % 64 == 0 && g.k % 64 == 0 && g.b.kpad % 2 == 0 && p % 32 == 0 &&
+         (256 % p == 0 || p % 256 == 0) && dma64_enabled();
+}
+
 void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {
+  if (lb == L_VNNI_PANELS || lb == L_BLOCKED_VNNI) {
+    // The blocked VNNI layout [N/32, Kp/32, 16, 32, 2] is VNNI panels of 32.
+    GemmArgs v = g;
+    if (lb == L_BLOCKED_VNNI) v.b.panel = 32;
+    launch_bf16_dma_b<L_VNNI_PANELS, true>(v, grid, s);
+    return;
+  }
   const bool k64 = g.k_chunk % 64 == 0 && g.k % 64 == 0 && dma64_enabled();
   if (lb == L_RCONTIG) {
     if (k64) launch_bf16_dma_b<L_RCONTIG, true>(g, grid, s);

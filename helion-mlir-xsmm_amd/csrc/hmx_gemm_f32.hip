@@ -230,9 +230,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 template <class Cfg, int LA, int LB>
 void launch_f32(const GemmArgs& g, bool guard, dim3 grid, hipStream_t s) {
   if (guard)
-    gemm_f32_kernel<Cfg, LA, LB, true><<<grid, Cfg::NT, 0, s>>>(g);
+    launch(gemm_f32_kernel<Cfg, LA, LB, true>, grid, Cfg::NT, s, g);
   else
-    gemm_f32_kernel<Cfg, LA, LB, false><<<grid, Cfg::NT, 0, s>>>(g);
+    launch(gemm_f32_kernel<Cfg, LA, LB, false>, grid, Cfg::NT, s, g);
 }
 
 template <class Cfg>
@@ -272,10 +272,10 @@ void launch_splitk_reduce(const float* partials, int splits, int64_t batch, cons
   const int64_t total = batch * r.m * r.n;
   if (vec4) {
     const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(total / 4, 256), 16384);
-    splitk_reduce_kernel<4><<<blocks, 256, 0, s>>>(partials, splits, batch, r);
+    launch(splitk_reduce_kernel<4>, blocks, 256, s, partials, splits, batch, r);
   } else {
     const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(total, 256), 16384);
-    splitk_reduce_kernel<1><<<blocks, 256, 0, s>>>(partials, splits, batch, r);
+    launch(splitk_reduce_kernel<1>, blocks, 256, s, partials, splits, batch, r);
   }
 }
 

@@ -2,6 +2,7 @@
 // error message, argument checks and launch-error capture.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -18,6 +19,32 @@ void clear_error();
 
 // The HIP error of the last launch on this thread, as an hmx status.
 int check_launch(const char* what);
+
+// Timing events armed on this thread by hmx_time_launches (null when not).
+struct LaunchEvents {
+  hipEvent_t start;
+  hipEvent_t stop;
+};
+LaunchEvents& launch_events();
+
+// Enqueues kernel<<<grid, block, 0, stream>>>(args...), each argument
+// converted to the kernel's parameter type. While timing events are armed on
+// this thread the launch goes through hipExtLaunchKernelGGL instead: the first
+// such launch records `start` as it begins and every one records `stop` as it
+// ends.
+template <typename... KArgs, typename... Args>
+inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t stream,
+                   Args... args) {
+  LaunchEvents& ev = launch_events();
+  if (ev.start == nullptr && ev.stop == nullptr) {
+    kernel<<<grid, block, 0, stream>>>(static_cast<KArgs>(args)...);
+    return;
+  }
+  hipEvent_t start = ev.start;
+  ev.start = nullptr;
+  hipExtLaunchKernelGGL<KArgs...>(kernel, grid, block, 0, stream, start, ev.stop, 0,
+                                  static_cast<KArgs>(args)...);
+}
 
 // Enqueues dst[c, r] = src[r, c] for 16-bit elements, src [rows, cols] with
 // row stride ld, dst [cols, rows] contiguous (hmx_pack.hip).

@@ -153,7 +153,8 @@ void launch_transpose16(const void* src, void* dst, int64_t rows, int64_t cols, 
                         hipStream_t stream) {
   const bool vec = aligned16(src) && aligned16(dst) && ld % 8 == 0 && rows % 8 == 0;
   const dim3 grid((unsigned)ceil_div(cols, 256), (unsigned)ceil_div(rows, 64));
-  transpose16_kernel<<<grid, 256, 0, stream>>>((const uint16_t*)src, (uint16_t*)dst, rows, cols, ld, vec);
+  launch(transpose16_kernel, grid, 256, stream, (const uint16_t*)src, (uint16_t*)dst, rows, cols,
+         ld, vec);
 }
 
 }  // namespace hmx
@@ -203,8 +204,8 @@ extern "C" int hmx_pack(int kind, int dtype, const void* src, int64_t rows, int6
   }
   const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(a.total, 256), 65536);
   if (dtype == HMX_DTYPE_BF16)
-    pack_kernel<uint16_t><<<blocks, 256, 0, s>>>(a);
+    launch(pack_kernel<uint16_t>, blocks, 256, s, a);
   else
-    pack_kernel<float><<<blocks, 256, 0, s>>>(a);
+    launch(pack_kernel<float>, blocks, 256, s, a);
   return check_launch("pack");
 }

@@ -609,12 +609,12 @@ int hmx_softmax_rows(int dtype, const void* x, void* y, int64_t m, int64_t n,
     constexpr int EPV = decltype(epv_c)::value;
     const RowShape r = row_shape(n, EPV);
     if (r.vpl == 0) {
-      softmax_stream<T, EPV><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, (T*)y, m, n);
+      launch(softmax_stream<T, EPV>, unit_grid(m), kBlock, s, (const T*)x, (T*)y, m, n);
       return;
     }
     with_shape<EPV>(r, [&](auto vpl_c, auto whole_c) {
-      softmax_cached<T, EPV, decltype(vpl_c)::value, decltype(whole_c)::value>
-          <<<dim3((unsigned)row_grid(m, r)), row_block(r), 0, s>>>((const T*)x, (T*)y, m, n, r.wpr);
+      launch(softmax_cached<T, EPV, decltype(vpl_c)::value, decltype(whole_c)::value>,
+             dim3((unsigned)row_grid(m, r)), row_block(r), s, (const T*)x, (T*)y, m, n, r.wpr);
     });
   });
   return check_launch("softmax");
@@ -634,24 +634,24 @@ int hmx_rmsnorm_rows(int dtype, const void* x, const void* w, int w_dtype, void*
   with_type(dtype, rows_vectorizable(x, y, n, dtype), [&](auto tp, auto epv_c) {
     using T = std::remove_pointer_t<decltype(tp)>;
     constexpr int EPV = decltype(epv_c)::value;
-    auto launch = [&](auto wp) {
+    auto with_weight = [&](auto wp) {
       using W = std::remove_pointer_t<decltype(wp)>;
       const RowShape r = row_shape(n, EPV);
       if (r.vpl == 0) {
-        rmsnorm_stream<T, W, EPV><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, (const W*)w, w_vec,
-                                                                   (T*)y, m, n, eps);
+        launch(rmsnorm_stream<T, W, EPV>, unit_grid(m), kBlock, s, (const T*)x, (const W*)w, w_vec,
+               (T*)y, m, n, eps);
         return;
       }
       with_shape<EPV>(r, [&](auto vpl_c, auto whole_c) {
-        rmsnorm_cached<T, W, EPV, decltype(vpl_c)::value, decltype(whole_c)::value>
-            <<<dim3((unsigned)row_grid(m, r)), row_block(r), 0, s>>>(
-                (const T*)x, (const W*)w, w_vec, (T*)y, m, n, eps, r.wpr);
+        launch(rmsnorm_cached<T, W, EPV, decltype(vpl_c)::value, decltype(whole_c)::value>,
+               dim3((unsigned)row_grid(m, r)), row_block(r), s, (const T*)x, (const W*)w, w_vec,
+               (T*)y, m, n, eps, r.wpr);
       });
     };
     if (w != nullptr && w_dtype == HMX_DTYPE_BF16)
-      launch((uint16_t*)nullptr);
+      with_weight((uint16_t*)nullptr);
     else
-      launch((float*)nullptr);
+      with_weight((float*)nullptr);
   });
   return check_launch("rms_norm");
 }
@@ -679,12 +679,12 @@ int hmx_group_norm_rows(int dtype, const void* x, const void* w, const void* b,
     constexpr int EPV = decltype(epv_c)::value;
     const RowShape r = row_shape(group_size, EPV);
     if (r.vpl == 0) {
-      group_norm_stream<T, EPV><<<unit_grid(units), kBlock, 0, s>>>((const T*)x, (T*)y, a);
+      launch(group_norm_stream<T, EPV>, unit_grid(units), kBlock, s, (const T*)x, (T*)y, a);
       return;
     }
     with_shape<EPV>(r, [&](auto vpl_c, auto whole_c) {
-      group_norm_cached<T, EPV, decltype(vpl_c)::value, decltype(whole_c)::value>
-          <<<dim3((unsigned)row_grid(units, r)), row_block(r), 0, s>>>((const T*)x, (T*)y, a, r.wpr);
+      launch(group_norm_cached<T, EPV, decltype(vpl_c)::value, decltype(whole_c)::value>,
+             dim3((unsigned)row_grid(units, r)), row_block(r), s, (const T*)x, (T*)y, a, r.wpr);
     });
   });
   return check_launch("group_norm");
@@ -706,11 +706,14 @@ static int row_reduce_launch(const char* name, int mode, int dtype, const void* 
     using T = std::remove_pointer_t<decltype(tp)>;
     constexpr int EPV = decltype(epv_c)::value;
     if (mode == 0)
-      row_reduce<T, EPV, 0><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, vec, (T*)y, m, n, act, act_arg);
+      launch(row_reduce<T, EPV, 0>, unit_grid(m), kBlock, s, (const T*)x, vec, (T*)y, m, n, act,
+             act_arg);
     else if (mode == 1)
-      row_reduce<T, EPV, 1><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, vec, (T*)y, m, n, act, act_arg);
+      launch(row_reduce<T, EPV, 1>, unit_grid(m), kBlock, s, (const T*)x, vec, (T*)y, m, n, act,
+             act_arg);
     else
-      row_reduce<T, EPV, 2><<<unit_grid(m), kBlock, 0, s>>>((const T*)x, vec, (T*)y, m, n, act, act_arg);
+      launch(row_reduce<T, EPV, 2>, unit_grid(m), kBlock, s, (const T*)x, vec, (T*)y, m, n, act,
+             act_arg);
   });
   return check_launch(name);
 }
@@ -740,9 +743,9 @@ int hmx_column_sum(int dtype, const void* x, float* y, int64_t m, int64_t n, voi
   auto s = (hipStream_t)stream;
   const dim3 grid((unsigned)ceil_div(n, 256));
   if (dtype == HMX_DTYPE_BF16)
-    column_sum_kernel<uint16_t><<<grid, 256, 0, s>>>((const uint16_t*)x, y, m, n);
+    launch(column_sum_kernel<uint16_t>, grid, 256, s, (const uint16_t*)x, y, m, n);
   else
-    column_sum_kernel<float><<<grid, 256, 0, s>>>((const float*)x, y, m, n);
+    launch(column_sum_kernel<float>, grid, 256, s, (const float*)x, y, m, n);
   return check_launch("column_sum");
 }
 
@@ -759,8 +762,8 @@ int hmx_elementwise(int op, int dtype, const void* x, void* y, int64_t numel, fl
     using T = std::remove_pointer_t<decltype(tp)>;
     constexpr int EPV = decltype(epv_c)::value;
     const int64_t blocks = std::min<int64_t>(ceil_div(numel, 256 * EPV), 8192);
-    elementwise_kernel<T, EPV><<<dim3((unsigned)blocks), 256, 0, s>>>((const T*)x, (T*)y,
-                                                                       numel, op, arg);
+    launch(elementwise_kernel<T, EPV>, dim3((unsigned)blocks), 256, s, (const T*)x, (T*)y, numel,
+           op, arg);
   });
   return check_launch("elementwise");
 }

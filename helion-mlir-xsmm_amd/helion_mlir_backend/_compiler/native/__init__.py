@@ -61,6 +61,7 @@ SIGNATURES: dict[str, list[object]] = {
     "hmx_last_error": [],
     "hmx_abi_version": [],
     "hmx_device_check": [_IP],
+    "hmx_time_launches": [_P, _P],
     "hmx_gemm": [
         _I, _I,  # ab_dtype, c_dtype
         _P, _L, _I,  # a, lda, trans_a
@@ -154,6 +155,17 @@ def call(name: str, *args: object) -> None:
     fn = getattr(lib(), name)
     _calls[0] += 1
     check(fn(*args), name)
+
+
+def time_launches(start: "torch.cuda.Event | None", stop: "torch.cuda.Event | None") -> None:
+    """Arms timing events for the kernels this thread enqueues next
+    (``hmx_time_launches``): ``start`` is recorded as the first kernel begins,
+    ``stop`` as each kernel ends. ``None, None`` disarms. The events must have
+    been created (recorded once) with ``enable_timing=True``."""
+    handles = [None if e is None else e.cuda_event for e in (start, stop)]
+    if any(h == 0 for h in handles):
+        raise ValueError("time_launches: record each event once before arming it")
+    check(lib().hmx_time_launches(*handles), "hmx_time_launches")
 
 
 def count_call() -> None:

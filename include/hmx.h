@@ -9,8 +9,9 @@
  *     Python side). Nothing is allocated inside: split-K partials go to the
  *     caller's `workspace`.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream)
- *     and runs asynchronously. Functions keep no mutable global state, so
- *     they may be called from several threads at once.
+ *     and runs asynchronously. Functions keep no mutable global state (only
+ *     per-thread error messages and timing events), so they may be called
+ *     from several threads at once.
  *   - Operands are dense: row-major with the given leading dimension, or a
  *     packed layout described by its HMX_B_* code. bf16 travels as raw bits.
  *   - Arguments a kernel cannot take are refused with HMX_ERR_INVALID before
@@ -102,6 +103,17 @@ int hmx_abi_version(void);
  * writes its compute-unit count. Stands in for the target check of
  * resolve_target (helion_mlir_backend/_compiler/targets/__init__.py:61-85). */
 int hmx_device_check(int* compute_units);
+
+/* Profiling hook; no counterpart in the reference (its kernels run on the
+ * CPU, timed by callers with perf_counter). Arms hipEvent_t timing events for
+ * the calling thread: the next kernel any entry point enqueues records
+ * `start_event` when it begins, and every kernel enqueued while armed records
+ * `stop_event` when it ends (hipExtLaunchKernelGGL), so the pair spans exactly
+ * the kernels of the calls made in between, without their dispatch latency.
+ * Both NULL disarms. The events must have been created with timing enabled
+ * and belong to the device the calls run on. Per-thread state, like the
+ * error message. */
+int hmx_time_launches(void* start_event, void* stop_event);
 
 /*
  * GEMM with fused epilogue:

@@ -313,6 +313,22 @@ def test_matmul_bench_panels(gpu_device, dtype) -> None:
     _check(got, R.matmul(to_np(a), to_np(b), out=dtype), k, to_np(a), to_np(b), dtype)
 
 
+@pytest.mark.parametrize("panel", [32, 64, 128, 256, 512])
+def test_matmul_prepacked_vnni_whole_tiles(gpu_device, panel) -> None:
+    # Whole 256 x 256 tiles with K a multiple of 64: the direct-to-LDS kernel
+    # reads the VNNI panels in place (panels narrower and wider than a tile),
+    # with the fused bias + SiLU epilogue.
+    m, k, n = 512, 320, 768
+    a = tensor(RNG.normal(0, 1, (m, k)).astype(np.float32), "bf16", gpu_device)
+    w = tensor(RNG.normal(0, 1, (n, k)).astype(np.float32), "bf16", gpu_device)
+    bias = tensor(RNG.normal(0, 1, n).astype(np.float32), "bf16", gpu_device)
+    got = to_np(U.matmul_prepacked_b(a, U.pack_b_vnni_t(w, panel), n, bias, torch.nn.functional.silu))
+    ref = R.matmul(to_np(a), to_np(w), False, True, to_np(bias), act="silu", out="bf16")
+    _check(got, ref, k, to_np(a), to_np(w), "bf16")
+    plain = U.matmul(a, w, trans_b=True, bias=bias, epilogue=torch.nn.functional.silu)
+    assert torch.equal(torch.from_numpy(got), plain.cpu().float())
+
+
 def test_matmul_config3_prepacked_layouts(gpu_device) -> None:
     cfg = W.config3(scale=4)  # 1024^3, the config-3 distribution
     a, b = cfg["a"].to(gpu_device), cfg["b"].to(gpu_device)
