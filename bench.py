@@ -121,7 +121,7 @@ class Gemm(Workload):
         self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_BF16_TFLOPS
         self.work = 2.0 * m * n * k
         self.dtype = "bf16"
-        self.kernel = "gemm_bf16_kernel" if prepacked else "gemm_bf16_dma64_kernel"
+        self.kernel = "gemm_bf16_dma64_kernel"
         self.config = {"workload": self.description, "m": m, "n": n, "k": k, "a": "bf16 row-major",
                        "b": "bf16 row-major" if not prepacked else "bf16 [N/32,K/32,16,32,2]",
                        "c": out_dtype_name, "seed": 2, "values": "U[-1,1]"}
