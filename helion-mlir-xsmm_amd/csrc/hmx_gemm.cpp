@@ -316,7 +316,11 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
     // identity epilogue.
     if (plan.tile.bm == 256 && (plan.splits < 2 || la != L_KCONTIG))
       return set_error(HMX_ERR_INVALID, "gemm: internal f32 plan without split-K");
-    launch_gemm_f32(g, plan.tile.bm, la, lb, guard, grid, s);
+    if (plan.tile.bm == 256 && !guard && (lb == L_KCONTIG || lb == L_RCONTIG) &&
+        g.k_chunk % 32 == 0 && dma_enabled())
+      launch_gemm_f32_dma(g, lb, grid, s);
+    else
+      launch_gemm_f32(g, plan.tile.bm, la, lb, guard, grid, s);
   }
   int st = check_launch("gemm");
   if (st != HMX_OK || plan.splits <= 1) return st;

@@ -316,6 +316,10 @@ void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s);
 bool gemm_bf16_dma_vnni_ok(const GemmArgs& g, int lb);
 // hmx_gemm_f32.hip: f32 kernel, tiles 128 x 128 or (split-K partials only)
 // 256 x 256; and the fixed-order split-K reduction into C.
+// hmx_gemm_dma.hip: direct-to-LDS f32 kernel; whole 256 x 256 tiles of
+// split-K partials (identity epilogue, f32 C), A K-contiguous, B K-contiguous
+// or row-major, K chunks of whole 32-element stages.
+void launch_gemm_f32_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s);
 void launch_gemm_f32(const GemmArgs& g, int tile_bm, int la, int lb, bool guard, dim3 grid,
                      hipStream_t s);
 void launch_splitk_reduce(const float* partials, int splits, int64_t batch, const GemmArgs& r,

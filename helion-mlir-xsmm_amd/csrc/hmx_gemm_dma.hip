@@ -427,6 +427,171 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
   epilogue_direct<FM, FN, WM, WN, false, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
 }
 
+// ---------------------------------------------------------------------------
+// f32 direct-to-LDS kernel (v_mfma_f32_32x32x2_f32) for whole 256 x 256 tiles
+// of long-K split-K products: row-major A, B [N, K] or [K, N], f32 partials
+// with the identity epilogue. The register-staged f32 kernel has to hold the
+// next tile's loads, two waves' fragments and 128 accumulators per wave in
+// 256 registers, and the compiler sinks the loads to where they are stored;
+// here the loads go straight to LDS, so four waves (one per SIMD, 128 x 128
+// outputs each, 256 accumulators in AGPRs) keep two fragment sets in VGPRs.
+//
+// Stages are 32 K deep (one 128-byte line of each A row), two of 64 KiB:
+// K-contiguous tiles [256 rows][32 k] with 16-byte chunk c of row r in slot
+// c ^ swz64(r), as the bf16 kernel; row-major B [32 k][256 n], 1 KiB rows with
+// chunk c of row k in slot c ^ (8 ((k >> 2) & 1)), so the two half-waves of a
+// fragment read (rows k and k + 4, same columns) meet different banks.
+//
+// A step is K = 8 (four MFMAs of K = 2 for each of the 16 fragment pairs, 64
+// slots); a stage is four steps. Slots 0-7 of each step read the next step's
+// fragments (two register sets alternate). Before step 3 the wave waits for
+// its loads of stage t + 1 and its reads of stage t, and the barrier both
+// publishes t + 1 and frees t; step 3 then reads t + 1's first fragments
+// (slots 0-7) and issues the 16 loads of stage t + 2 into t's buffer (slots
+// 8-23), three steps ahead of their use.
+template <int LB>
+__global__ __launch_bounds__(256, 1) void gemm_f32_dma_kernel(GemmArgs g) {
+  constexpr bool BT = LB == L_RCONTIG;             // B row-major [K, N]
+  constexpr int BM = 256, BN = 256, BK = 32;
+  constexpr int ROWB = BK * 4;                     // bytes per K-contiguous tile row
+  constexpr int NROWB = BN * 4;                    // bytes per row-major B tile row
+  constexpr int A_BYTES = BM * ROWB;               // 32 KiB
+  constexpr int STAGE = A_BYTES + BN * BK * 4;     // 64 KiB
+  constexpr int FM = 4, FN = 4, WM = 128, WN = 128;
+  constexpr int LOADS = 16;                        // DMA instructions per wave per stage
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
+
+  int tm, tn;
+  tile_coords(g.tiles_m, g.tiles_n, tm, tn);
+  const int split = blockIdx.y, batch = blockIdx.z;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t k_begin = (int64_t)split * g.k_chunk;
+  const int64_t k_end = min(g.k, k_begin + g.k_chunk);
+  const int ktiles = (int)((k_end - k_begin) / BK);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const i32x4_t srd_a = make_srd((const float*)g.a.p + batch * g.stride_a, g.a.bytes);
+  const i32x4_t srd_b = make_srd((const float*)g.b.p + batch * g.stride_b, g.b.bytes);
+  // K-contiguous operands: wave w loads tile rows 64 w .. 64 w + 63, 8 rows
+  // of 128 bytes per load (lane l: slot l % 8 of row 64 w + 8 q + l / 8,
+  // swizzle (l / 16) | 4 (q & 1)). Byte offsets below 2^31: the operands'
+  // byte ranges are.
+  const int rr = lane >> 3, slot = lane & 7;
+  auto kc_voff = [&](int64_t ld, int par) {
+    return (int32_t)((rr * ld + (slot ^ ((rr >> 1) | (par << 2))) * 4) * 4);
+  };
+  const int32_t voff_a0 = kc_voff(g.a.ld, 0), voff_a1 = kc_voff(g.a.ld, 1);
+  const int32_t soff_a = (int32_t)((m0 + wave * 64) * g.a.ld * 4);
+  const int32_t blk_a = (int32_t)(8 * g.a.ld * 4);
+  // B: K-contiguous as A; row-major: wave w loads K rows 8 w .. 8 w + 7, one
+  // 1 KiB row per load (lane l: slot l), swizzled by bit 2 of the row.
+  int32_t voff_b0, voff_b1, soff_b, blk_b;
+  if constexpr (BT) {
+    voff_b0 = (int32_t)((n0 + lane * 4) * 4);          // loads 0-3: rows 8 w + 0..3
+    voff_b1 = (int32_t)((n0 + (lane ^ 8) * 4) * 4);    // loads 4-7: rows 8 w + 4..7
+    soff_b = (int32_t)(wave * 8 * g.b.ld * 4);
+    blk_b = (int32_t)(g.b.ld * 4);
+  } else {
+    voff_b0 = kc_voff(g.b.ld, 0);
+    voff_b1 = kc_voff(g.b.ld, 1);
+    soff_b = (int32_t)((n0 + wave * 64) * g.b.ld * 4);
+    blk_b = (int32_t)(8 * g.b.ld * 4);
+  }
+  const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + wave * 8 * 1024;
+
+  // DMA q (< 16) of stage t: A for q < 8, then B.
+  auto dma = [&](int t, int q) {
+    const int64_t k0 = k_begin + (int64_t)min(t, ktiles - 1) * BK;
+    const uint32_t st = lds_w + (uint32_t)((t & 1) * STAGE);
+    if (q < 8) {
+      lds_dma16(srd_a, (q & 1) ? voff_a1 : voff_a0, soff_a + q * blk_a + (int32_t)(k0 * 4), st + q * 1024);
+    } else {
+      const int qb = q - 8;
+      const int32_t kb = BT ? (int32_t)(k0 * g.b.ld * 4) : (int32_t)(k0 * 4);
+      const int32_t voff = BT ? (qb < 4 ? voff_b0 : voff_b1) : ((qb & 1) ? voff_b1 : voff_b0);
+      lds_dma16(srd_b, voff, soff_b + qb * blk_b + kb, st + A_BYTES + qb * 1024);
+    }
+  };
+
+  f32x16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Fragment reads of step k8 (0, 8, 16, 24 within a stage): lane l feeds
+  // MFMA s (< 4) the values at K = k8 + 4 (l / 32) + s, row / column l % 32
+  // of the fragment.
+  const int frow = lane & 31, fk = lane >> 5, fswz = swz64(frow);
+  const uint8_t* a_frag = lds + (wm * WM + frow) * ROWB;
+  const uint8_t* b_frag = lds + A_BYTES + (wn * WN + frow) * ROWB;
+  // Row-major B: column n = wn * 128 + 32 j + l % 32 sits in chunk n / 4 of
+  // its row, stored in slot (n / 4) ^ 8 (l / 32) for the rows this lane reads.
+  int b_rc[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int n = wn * WN + 32 * j + frow;
+    b_rc[j] = A_BYTES + 4 * fk * NROWB + (((n >> 2) ^ (8 * fk)) << 4) + (n & 3) * 4;
+  }
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+  auto a_read = [&](int stage, int k8, int i) -> f32x4v {
+    return *(const f32x4v*)(a_frag + stage * STAGE + i * 32 * ROWB + (((k8 >> 2) + fk) ^ fswz) * 16);
+  };
+  auto b_read = [&](int stage, int k8, int j) -> f32x4v {
+    if constexpr (BT) {
+      const uint8_t* p = lds + stage * STAGE + b_rc[j] + k8 * NROWB;
+      return f32x4v{*(const float*)p, *(const float*)(p + NROWB), *(const float*)(p + 2 * NROWB),
+                    *(const float*)(p + 3 * NROWB)};
+    } else {
+      return *(const f32x4v*)(b_frag + stage * STAGE + j * 32 * ROWB + (((k8 >> 2) + fk) ^ fswz) * 16);
+    }
+  };
+
+  // The host launches this kernel only with at least one K stage per split.
+  f32x4v fa[2][FM], fb[2][FN];
+#pragma unroll
+  for (int q = 0; q < LOADS; ++q) dma(0, q);
+#pragma unroll
+  for (int q = 0; q < LOADS; ++q) dma(1, q);
+  wait_vmem<LOADS>();  // stage 0 landed
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < FM; ++i) fa[0][i] = a_read(0, 0, i);
+#pragma unroll
+  for (int j = 0; j < FN; ++j) fb[0][j] = b_read(0, 0, j);
+
+  for (int t = 0; t < ktiles; ++t) {
+    const int cur = t & 1, nxt = cur ^ 1;
+#pragma unroll
+    for (int step = 0; step < 4; ++step) {
+      const int set = step & 1;
+      if (step == 3) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+      for (int x = 0; x < 64; ++x) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (x < 8) {
+          // The next step's fragments: this stage's, or t + 1's first.
+          const int stg = step < 3 ? cur : nxt, k8 = step < 3 ? 8 * (step + 1) : 0;
+          if (x < 4) fa[set ^ 1][x] = a_read(stg, k8, x);
+          else fb[set ^ 1][x - 4] = b_read(stg, k8, x - 4);
+        } else if (step == 3 && x < 8 + LOADS) {
+          dma(t + 2, x - 8);
+        }
+        const int s = x >> 4, idx = x & 15, i = idx >> 2, j = idx & 3;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[set][i][s], fb[set][j][s], acc[i][j], 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  wait_vmem<0>();  // no load into LDS outlives the loop
+  epilogue_direct<FM, FN, WM, WN, false, ACT_ID, false>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
+}
+
 template <int LB, bool BF16, bool K64>
 void launch_bf16_dma_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
   if constexpr (K64) {
@@ -488,6 +653,13 @@ void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {
     if (k64) launch_bf16_dma_b<L_KCONTIG, true>(g, grid, s);
     else launch_bf16_dma_b<L_KCONTIG, false>(g, grid, s);
   }
+}
+
+void launch_gemm_f32_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {
+  if (lb == L_RCONTIG)
+    launch(gemm_f32_dma_kernel<L_RCONTIG>, grid, 256, s, g);
+  else
+    launch(gemm_f32_dma_kernel<L_KCONTIG>, grid, 256, s, g);
 }
 
 }  // namespace hmx
