@@ -233,14 +233,17 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(GemmArgs g) {
 // (row lane % 32, one chunk) meets distinct banks across 16 lanes. Row-major
 // B: [64 k][256 n], 512-byte rows swizzled as in the 32-wide kernel.
 //
-// Step t (64 MFMA slots, k-steps of 16): slots 0-7, 16-23 and 32-39 read the
-// next k-step's fragments (two register sets alternate); before slot 44 the
-// wave waits for its loads of stage t + 1 and its reads of stage t, and the
-// barrier both publishes stage t + 1 and frees stage t; slots 44-59 issue the
-// loads of stage t + 2 into it and slots 56-63 read stage t + 1's first
-// fragments. The loads of a stage have ~one step to land.
-template <int LB, int ACT, bool BF16>
-__global__ __launch_bounds__(256, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
+// NW = 8 waves (the default: two per SIMD, 128 x 64 outputs each) or 4 (one
+// per SIMD, 128 x 128). Step t is four k-steps of 16, NS = FM * FN MFMA
+// slots each (32 or 64 slots per step). The first FM + FN slots of k-steps
+// 0-2 read the next k-step's fragments (two register sets alternate); before
+// slot BAR (24 or 44) the wave waits for its loads of stage t + 1 and its
+// reads of stage t, and the barrier both publishes stage t + 1 and frees
+// stage t; the next LOADS slots issue the loads of stage t + 2 into it and the
+// last FM + FN slots read stage t + 1's first fragments. The loads of a stage
+// have ~one step to land.
+template <int LB, int ACT, bool BF16, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
   constexpr bool BT = LB == L_RCONTIG;             // B row-major [K, N]
   constexpr bool VN = LB == L_VNNI_PANELS;         // B in K-pair (VNNI) panels
   constexpr int BM = 256, BN = 256, BK = 64;
@@ -248,8 +251,15 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
   constexpr int NROWB = BN * 2;                    // bytes per row-major B tile row
   constexpr int A_BYTES = BM * ROWB;               // 32 KiB
   constexpr int STAGE = A_BYTES + BN * BK * 2;     // 64 KiB
-  constexpr int FM = 4, FN = 4, WM = 128, WN = 128;
-  constexpr int LOADS = 16;                        // DMA instructions per wave per stage
+  // NW = 4: one wave per SIMD, 2 x 2 waves of 128 x 128 outputs; NW = 8: two
+  // per SIMD, 2 x 4 waves of 128 x 64.
+  constexpr int WM = 128, WN = NW == 4 ? 128 : 64, FM = WM / 32, FN = WN / 32;
+  constexpr int LA = 32 / NW, LBN = 32 / NW;       // 1 KiB loads of A / B per wave per stage
+  constexpr int LOADS = LA + LBN;
+  constexpr int NS = FM * FN, SLOTS = 4 * NS;      // MFMAs per k-step / per stage
+  constexpr int NF = FM + FN;                      // fragment reads per k-step
+  constexpr int BAR = NW == 4 ? 44 : 24;           // slot of the stage's wait + barrier
+  static_assert(BAR >= 2 * NS + NF && BAR + LOADS <= SLOTS, "slot plan");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
 
   int tm, tn;
@@ -262,41 +272,41 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / (NW / 2), wn = wave % (NW / 2);
 
   const i32x4_t srd_a = make_srd((const uint16_t*)g.a.p + batch * g.stride_a, g.a.bytes);
   const i32x4_t srd_b = make_srd((const uint16_t*)g.b.p + batch * g.stride_b, g.b.bytes);
-  // K-contiguous operands: wave w loads tile rows 64 w .. 64 w + 63, 8 rows
-  // per load: lane l fills slot l % 8 of row 64 w + 8 q + l / 8 of load q,
-  // whose swizzle is (l / 16) | 4 (q & 1). Byte offsets below 2^31: the
-  // operands' byte ranges are.
+  // K-contiguous operands: wave w loads tile rows R w .. R w + R - 1 (R =
+  // 256 / NW), 8 rows per load: lane l fills slot l % 8 of row R w + 8 q + l / 8
+  // of load q, whose swizzle is (l / 16) | 4 (q & 1). Byte offsets below 2^31:
+  // the operands' byte ranges are.
   const int rr = lane >> 3, slot = lane & 7;
   auto kc_voff = [&](int64_t ld, int par) {
     return (int32_t)((rr * ld + (slot ^ ((rr >> 1) | (par << 2))) * 8) * 2);
   };
   const int32_t voff_a0 = kc_voff(g.a.ld, 0), voff_a1 = kc_voff(g.a.ld, 1);
-  const int32_t soff_a = (int32_t)((m0 + wave * 64) * g.a.ld * 2);
+  const int32_t soff_a = (int32_t)((m0 + wave * (256 / NW)) * g.a.ld * 2);
   const int32_t blk_a = (int32_t)(8 * g.a.ld * 2);
-  // B: K-contiguous as A; row-major: wave w loads K rows 16 w .. 16 w + 15
-  // in pairs 16 w + 2 q, 16 w + 2 q + 1, lane l filling slot l % 32 of row
-  // l / 32 of the pair.
+  // B: K-contiguous as A; row-major: wave w loads K rows Q w .. Q w + Q - 1
+  // (Q = 64 / NW) in pairs Q w + 2 q, Q w + 2 q + 1, lane l filling slot
+  // l % 32 of row l / 32 of the pair.
   // VNNI panels of width P ([N/P, Kp/2, P, 2]; the blocked VNNI layout is
   // P = 32): a stage is 32 K pairs x 256 columns. For P <= 256 it is 256 / P
   // runs of 32 pair rows x P columns, each one contiguous 128 P bytes of its
   // panel; for wider panels, 32 pair rows of 256 columns (1 KiB each, 4 P
-  // bytes apart). Either way load q of wave w copies 1 KiB, the (8 w + q)-th
-  // of the stage in that order, to LDS unchanged: [256 / PL][32][PL][2] with
+  // bytes apart). Either way load q of wave w copies 1 KiB, the
+  // (LBN w + q)-th of the stage in that order, to LDS unchanged: [256 / PL][32][PL][2] with
   // PL = min(P, 256). Its byte offset is vn_off[q] + (k0 / 2) * 4 P.
   int32_t voff_b0, voff_b1, soff_b, blk_b;
-  int32_t vn_off[8];
+  int32_t vn_off[LBN];
   const int64_t P = g.b.panel;
   const int PL = (int)min<int64_t>(P, 256);
   if constexpr (VN) {
     voff_b0 = voff_b1 = lane * 16;
     soff_b = blk_b = 0;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int64_t idx = wave * 8 + q;
+    for (int q = 0; q < LBN; ++q) {
+      const int64_t idx = wave * LBN + q;
       int64_t off;
       if (P <= 256) {
         const int64_t b = idx * 1024, run = 128 * P;
@@ -310,27 +320,27 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
     const int r = lane >> 5, c = lane & 31;
     voff_b0 = (int32_t)((r * g.b.ld + (c ^ swz_n(r)) * 8) * 2);      // even q
     voff_b1 = (int32_t)((r * g.b.ld + (c ^ swz_n(r + 2)) * 8) * 2);  // odd q
-    soff_b = (int32_t)((wave * 16 * g.b.ld + n0) * 2);
+    soff_b = (int32_t)((wave * (64 / NW) * g.b.ld + n0) * 2);
     blk_b = (int32_t)(2 * g.b.ld * 2);
   } else {
     voff_b0 = kc_voff(g.b.ld, 0);
     voff_b1 = kc_voff(g.b.ld, 1);
-    soff_b = (int32_t)((n0 + wave * 64) * g.b.ld * 2);
+    soff_b = (int32_t)((n0 + wave * (256 / NW)) * g.b.ld * 2);
     blk_b = (int32_t)(8 * g.b.ld * 2);
   }
-  const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + wave * 8 * 1024;
+  const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + wave * LA * 1024;
 
-  // DMA q (< 16) of stage t: A for q < 8, then B.
+  // DMA q (< LOADS) of stage t: A for q < LA, then B.
   auto dma = [&](int t, int q) {
     const int64_t k0 = k_begin + (int64_t)min(t, ktiles - 1) * BK;
     const uint32_t st = lds_w + (uint32_t)((t & 1) * STAGE);
-    if (q < 8) {
+    if (q < LA) {
       lds_dma16(srd_a, (q & 1) ? voff_a1 : voff_a0, soff_a + q * blk_a + (int32_t)(k0 * 2), st + q * 1024);
     } else if constexpr (VN) {
-      const int qb = q - 8;
+      const int qb = q - LA;
       lds_dma16(srd_b, voff_b0, vn_off[qb] + (int32_t)((k0 / 2) * 4 * P), st + A_BYTES + qb * 1024);
     } else {
-      const int qb = q - 8;
+      const int qb = q - LA;
       const int32_t kb = BT ? (int32_t)(k0 * g.b.ld * 2) : (int32_t)(k0 * 2);
       lds_dma16(srd_b, (qb & 1) ? voff_b1 : voff_b0, soff_b + qb * blk_b + kb,
                 st + A_BYTES + qb * 1024);
@@ -356,7 +366,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
     const int v = (2 * (gi & 1) + ((sl & 3) >> 1)) ^ swz_n(sl >> 2);
 #pragma unroll
     for (int j = 0; j < FN; ++j)
-      b_tr[j] = A_BYTES + (8 * (gi >> 1) + (sl >> 2)) * NROWB + (wn * 16 + ((4 * j) ^ v)) * 16 + 8 * (sl & 1);
+      b_tr[j] = A_BYTES + (8 * (gi >> 1) + (sl >> 2)) * NROWB + ((wn * (WN / 8) + 4 * j) ^ v) * 16 + 8 * (sl & 1);
   }
   // VNNI B: column n = wn * 128 + 32 j + lane % 32 needs K pairs
   // 8 ks + 4 (lane / 32) .. + 3 (4 * PL bytes apart), i.e. K values
@@ -404,21 +414,22 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
   for (int t = 0; t < ktiles; ++t) {
     const int cur = t & 1, nxt = cur ^ 1;
 #pragma unroll
-    for (int x = 0; x < 64; ++x) {
+    for (int x = 0; x < SLOTS; ++x) {
       __builtin_amdgcn_sched_barrier(0);
-      const int ks = x >> 4, sub = x & 15, f = x & 7;
-      if (x == 44) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if (ks < 3 && sub < 8) {
+      const int ks = x / NS, sub = x % NS;
+      if (x == BAR) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (ks < 3 && sub < NF) {
         const int set = (ks + 1) & 1;
-        if (f < 4) fa[set][f] = a_read(cur, ks + 1, f);
-        else fb[set][f - 4] = b_read(cur, ks + 1, f - 4);
+        if (sub < FM) fa[set][sub] = a_read(cur, ks + 1, sub);
+        else fb[set][sub - FM] = b_read(cur, ks + 1, sub - FM);
       }
-      if (x >= 44 && x < 60) dma(t + 2, x - 44);
-      if (x >= 56) {
-        if (f < 4) fa[0][f] = a_read(nxt, 0, f);
-        else fb[0][f - 4] = b_read(nxt, 0, f - 4);
+      if (x >= BAR && x < BAR + LOADS) dma(t + 2, x - BAR);
+      if (x >= SLOTS - NF) {
+        const int f = x - (SLOTS - NF);
+        if (f < FM) fa[0][f] = a_read(nxt, 0, f);
+        else fb[0][f - FM] = b_read(nxt, 0, f - FM);
       }
-      const int i = sub >> 2, j = sub & 3, set = ks & 1;
+      const int i = sub / FN, j = sub % FN, set = ks & 1;
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -592,13 +603,13 @@ __global__ __launch_bounds__(256, 1) void gemm_f32_dma_kernel(GemmArgs g) {
   epilogue_direct<FM, FN, WM, WN, false, ACT_ID, false>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
 }
 
-template <int LB, bool BF16, bool K64>
+template <int LB, bool BF16, bool K64, int NW = 4>
 void launch_bf16_dma_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
   if constexpr (K64) {
     switch (g.act) {
-      case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16>, grid, 256, s, g); break;
-      case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16>, grid, 256, s, g); break;
-      default: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16>, grid, 256, s, g); break;
+      case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, NW>, grid, NW * 64, s, g); break;
+      case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, NW>, grid, NW * 64, s, g); break;
+      default: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, NW>, grid, NW * 64, s, g); break;
     }
   } else if constexpr (LB != L_VNNI_PANELS) {
     switch (g.act) {
@@ -611,6 +622,20 @@ void launch_bf16_dma_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
 
 template <int LB, bool K64>
 void launch_bf16_dma_b(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  // Eight waves (two per SIMD) unless the environment sets HMX_GEMM_WAVES=4:
+  // the second wave of a SIMD issues MFMAs while the first waits at the
+  // stage barrier or on an LDS read (measured: 2-5 % faster on configs 3-5).
+  static const bool eight = [] {
+    const char* e = getenv("HMX_GEMM_WAVES");
+    return !(e && e[0] == '4');
+  }();
+  if (eight && K64) {
+    if (g.c_dtype == HMX_DTYPE_BF16)
+      launch_bf16_dma_c<LB, true, K64, 8>(g, grid, s);
+    else
+      launch_bf16_dma_c<LB, false, K64, 8>(g, grid, s);
+    return;
+  }
   if (g.c_dtype == HMX_DTYPE_BF16)
     launch_bf16_dma_c<LB, true, K64>(g, grid, s);
   else
