@@ -695,7 +695,9 @@ static int row_reduce_launch(const char* name, int mode, int dtype, const void* 
                              float act_arg, void* stream) {
   HMX_REQUIRE(valid_dtype(dtype), "%s: unknown dtype %d", name, dtype);
   HMX_REQUIRE(m >= 0 && n >= 0, "%s: invalid shape", name);
-  HMX_REQUIRE(x && y && (mode == 0 || vec), "%s: null operand", name);
+  // Rows of no columns read nothing: x and vec may then be null (an empty
+  // tensor's data pointer).
+  HMX_REQUIRE((x || n == 0) && y && (mode == 0 || vec || n == 0), "%s: null operand", name);
   HMX_REQUIRE(valid_activation(act), "%s: unknown activation %d", name, act);
   HMX_REQUIRE(m <= ((int64_t)1 << 31) * kRowsPerBlock, "%s: too many rows", name);
   if (m == 0) return HMX_OK;
@@ -738,7 +740,7 @@ int hmx_matvec(int dtype, const void* a, const void* x, void* y, int64_t m, int6
 int hmx_column_sum(int dtype, const void* x, float* y, int64_t m, int64_t n, void* stream) {
   HMX_REQUIRE(valid_dtype(dtype), "column_sum: unknown dtype %d", dtype);
   HMX_REQUIRE(m >= 0 && n >= 0, "column_sum: invalid shape");
-  HMX_REQUIRE(x && y, "column_sum: null operand");
+  HMX_REQUIRE((x || m == 0) && y, "column_sum: null operand");  // no rows: x is not read
   if (n == 0) return HMX_OK;
   auto s = (hipStream_t)stream;
   const dim3 grid((unsigned)ceil_div(n, 256));
