@@ -146,6 +146,23 @@ bool dma_enabled() {
   return on;
 }
 
+// Whole rounds: a GEMM of more 256 x 256 tiles than CUs whose last round
+// would keep at most half the CUs busy runs its first n1 tile columns (a whole
+// number of rounds) as 256 x 256 tiles and the remaining columns as 256 x 128
+// tiles, one round of half-size tiles, instead of a last round of full tiles
+// on few CUs. Returns n1, or 0 when the split does not apply. The environment
+// variable HMX_GEMM_ROUNDS=0 turns it off (for comparison).
+int64_t whole_round_columns(int64_t tiles_m, int64_t tiles_n) {
+  static const bool on = [] {
+    const char* e = getenv("HMX_GEMM_ROUNDS");
+    return !(e && e[0] == '0');
+  }();
+  const int64_t tiles = tiles_m * tiles_n, tail = tiles % kCus;
+  if (!on || tiles <= kCus || tail == 0 || tail > kCus / 2) return 0;
+  if ((tiles - tail) % tiles_m != 0) return 0;
+  return (tiles - tail) / tiles_m;
+}
+
 // The direct-to-LDS kernel finishes C with the register epilogue only:
 // identity, ReLU or SiLU, and 4-byte aligned column pairs for bf16 C.
 bool dma_direct_ok(const GemmArgs& g) {
@@ -306,9 +323,33 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
     const TileChoice t = plan.tile;
     if (t.bm == 256 && !guard && la == L_KCONTIG &&
         (lb_run == L_KCONTIG || lb_run == L_RCONTIG || gemm_bf16_dma_vnni_ok(g, lb_run)) &&
-        dma_direct_ok(g) && dma_enabled())
-      launch_gemm_bf16_dma(g, lb_run, grid, s);
-    else
+        dma_direct_ok(g) && dma_enabled()) {
+      const int64_t n1 = lb_run == L_KCONTIG && plan.splits == 1 && batch == 1 && g.k_chunk % 64 == 0
+                             ? whole_round_columns(tiles_m, tiles_n)
+                             : 0;
+      if (n1 > 0) {
+        GemmArgs head = g;
+        head.n = n1 * 256;
+        head.tiles_n = (int)n1;
+        launch_gemm_bf16_dma(head, lb_run, dim3((unsigned)(tiles_m * n1), 1, 1), s);
+        // The rest: B rows, C columns and the column vectors from n1 * 256 on.
+        const int64_t off = n1 * 256;
+        GemmArgs rest = g;
+        rest.n = n - off;
+        rest.tiles_n = (int)(rest.n / 128);
+        rest.b.p = (const uint16_t*)g.b.p + off * g.b.ld;
+        rest.b.rows = rest.n;
+        rest.b.bytes = (int32_t)(((rest.n - 1) * g.b.ld + k) * 2);
+        rest.c = (char*)g.c + off * dtype_bytes(g.c_dtype);
+        const int64_t vb = off * dtype_bytes(vec_dtype);
+        if (g.bias) rest.bias = (const char*)g.bias + vb;
+        if (g.scale) rest.scale = (const char*)g.scale + vb;
+        if (g.shift) rest.shift = (const char*)g.shift + vb;
+        launch_gemm_bf16_dma_narrow(rest, dim3((unsigned)(tiles_m * rest.tiles_n), 1, 1), s);
+      } else {
+        launch_gemm_bf16_dma(g, lb_run, grid, s);
+      }
+    } else
       launch_gemm_bf16(g, t.bm, la, lb_run, guard, grid, s);
   } else {
     // The 256 x 256 f32 tile is planned only for row-major A, B [N, K] or

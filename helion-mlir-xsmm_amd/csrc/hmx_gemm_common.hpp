@@ -311,6 +311,9 @@ void launch_gemm_bf16(const GemmArgs& g, int tile_bm, int la, int lb, bool guard
 // chunks are whole 64-element stages, else 32-wide); whole 256 x 256 tiles, A
 // K-contiguous, B K-contiguous or row-major, identity / ReLU / SiLU epilogue.
 void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s);
+// The 64-wide direct-to-LDS kernel on 256 x 128 tiles (four waves, B
+// [N, K]): the columns past the last whole round of 256 x 256 tiles.
+void launch_gemm_bf16_dma_narrow(const GemmArgs& g, dim3 grid, hipStream_t s);
 // Whether the 64-wide direct-to-LDS kernel reads this VNNI-packed B (VNNI
 // panels or blocked VNNI) in place.
 bool gemm_bf16_dma_vnni_ok(const GemmArgs& g, int lb);

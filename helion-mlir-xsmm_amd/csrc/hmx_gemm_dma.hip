@@ -242,24 +242,26 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(GemmArgs g) {
 // stage t; the next LOADS slots issue the loads of stage t + 2 into it and the
 // last FM + FN slots read stage t + 1's first fragments. The loads of a stage
 // have ~one step to land.
-template <int LB, int ACT, bool BF16, int NW>
+template <int LB, int ACT, bool BF16, int NW, int BN>
 __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
   constexpr bool BT = LB == L_RCONTIG;             // B row-major [K, N]
   constexpr bool VN = LB == L_VNNI_PANELS;         // B in K-pair (VNNI) panels
-  constexpr int BM = 256, BN = 256, BK = 64;
+  constexpr int BM = 256, BK = 64;
+  static_assert(BN == 256 || (BN == 128 && NW == 4 && LB == L_KCONTIG),
+                "256 x 128 tiles: four waves, K-contiguous B");
   constexpr int ROWB = BK * 2;                     // bytes per K-contiguous tile row
   constexpr int NROWB = BN * 2;                    // bytes per row-major B tile row
   constexpr int A_BYTES = BM * ROWB;               // 32 KiB
-  constexpr int STAGE = A_BYTES + BN * BK * 2;     // 64 KiB
-  // NW = 4: one wave per SIMD, 2 x 2 waves of 128 x 128 outputs; NW = 8: two
-  // per SIMD, 2 x 4 waves of 128 x 64.
-  constexpr int WM = 128, WN = NW == 4 ? 128 : 64, FM = WM / 32, FN = WN / 32;
-  constexpr int LA = 32 / NW, LBN = 32 / NW;       // 1 KiB loads of A / B per wave per stage
+  constexpr int STAGE = A_BYTES + BN * BK * 2;     // 64 KiB (48 KiB for 256 x 128 tiles)
+  // NW = 4: one wave per SIMD, 2 x 2 waves of 128 x BN / 2 outputs; NW = 8:
+  // two per SIMD, 2 x 4 waves of 128 x 64.
+  constexpr int WM = 128, WN = BN / (NW / 2), FM = WM / 32, FN = WN / 32;
+  constexpr int LA = 32 / NW, LBN = BN / 8 / NW;   // 1 KiB loads of A / B per wave per stage
   constexpr int LOADS = LA + LBN;
   constexpr int NS = FM * FN, SLOTS = 4 * NS;      // MFMAs per k-step / per stage
   constexpr int NF = FM + FN;                      // fragment reads per k-step
-  constexpr int BAR = NW == 4 ? 44 : 24;           // slot of the stage's wait + barrier
-  static_assert(BAR >= 2 * NS + NF && BAR + LOADS <= SLOTS, "slot plan");
+  constexpr int BAR = NS == 16 ? 44 : 24;          // slot of the stage's wait + barrier
+  static_assert(BAR >= 2 * NS + NF && BAR < SLOTS, "slot plan");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
 
   int tm, tn;
@@ -325,25 +327,27 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
   } else {
     voff_b0 = kc_voff(g.b.ld, 0);
     voff_b1 = kc_voff(g.b.ld, 1);
-    soff_b = (int32_t)((n0 + wave * (256 / NW)) * g.b.ld * 2);
+    soff_b = (int32_t)((n0 + wave * (BN / NW)) * g.b.ld * 2);
     blk_b = (int32_t)(8 * g.b.ld * 2);
   }
   const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + wave * LA * 1024;
+  const uint32_t lds_wb = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + A_BYTES + wave * LBN * 1024;
 
   // DMA q (< LOADS) of stage t: A for q < LA, then B.
   auto dma = [&](int t, int q) {
     const int64_t k0 = k_begin + (int64_t)min(t, ktiles - 1) * BK;
     const uint32_t st = lds_w + (uint32_t)((t & 1) * STAGE);
+    const uint32_t sb = lds_wb + (uint32_t)((t & 1) * STAGE);
     if (q < LA) {
       lds_dma16(srd_a, (q & 1) ? voff_a1 : voff_a0, soff_a + q * blk_a + (int32_t)(k0 * 2), st + q * 1024);
     } else if constexpr (VN) {
       const int qb = q - LA;
-      lds_dma16(srd_b, voff_b0, vn_off[qb] + (int32_t)((k0 / 2) * 4 * P), st + A_BYTES + qb * 1024);
+      lds_dma16(srd_b, voff_b0, vn_off[qb] + (int32_t)((k0 / 2) * 4 * P), sb + qb * 1024);
     } else {
       const int qb = q - LA;
       const int32_t kb = BT ? (int32_t)(k0 * g.b.ld * 2) : (int32_t)(k0 * 2);
       lds_dma16(srd_b, (qb & 1) ? voff_b1 : voff_b0, soff_b + qb * blk_b + kb,
-                st + A_BYTES + qb * 1024);
+                sb + qb * 1024);
     }
   };
 
@@ -423,7 +427,10 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
         if (sub < FM) fa[set][sub] = a_read(cur, ks + 1, sub);
         else fb[set][sub - FM] = b_read(cur, ks + 1, sub - FM);
       }
-      if (x >= BAR && x < BAR + LOADS) dma(t + 2, x - BAR);
+      // The stage's loads, spread evenly over the slots after the barrier.
+#pragma unroll
+      for (int q = (x - BAR) * LOADS / (SLOTS - BAR); q < (x + 1 - BAR) * LOADS / (SLOTS - BAR); ++q)
+        if (x >= BAR) dma(t + 2, q);
       if (x >= SLOTS - NF) {
         const int f = x - (SLOTS - NF);
         if (f < FM) fa[0][f] = a_read(nxt, 0, f);
@@ -607,9 +614,9 @@ template <int LB, bool BF16, bool K64, int NW = 4>
 void launch_bf16_dma_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
   if constexpr (K64) {
     switch (g.act) {
-      case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, NW>, grid, NW * 64, s, g); break;
-      case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, NW>, grid, NW * 64, s, g); break;
-      default: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, NW>, grid, NW * 64, s, g); break;
+      case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, NW, 256>, grid, NW * 64, s, g); break;
+      case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, NW, 256>, grid, NW * 64, s, g); break;
+      default: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, NW, 256>, grid, NW * 64, s, g); break;
     }
   } else if constexpr (LB != L_VNNI_PANELS) {
     switch (g.act) {
@@ -660,6 +667,22 @@ bool gemm_bf16_dma_vnni_ok(const GemmArgs& g, int lb) {
   const int64_t p = lb == L_BLOCKED_VNNI ? 32 : g.b.panel;
   return g.k_chunk % 64 == 0 && g.k % 64 == 0 && g.b.kpad % 2 == 0 && p % 32 == 0 &&
          (256 % p == 0 || p % 256 == 0) && dma64_enabled();
+}
+
+template <bool BF16>
+void launch_bf16_dma_narrow(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  switch (g.act) {
+    case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<L_KCONTIG, ACT_RELU, BF16, 4, 128>, grid, 256, s, g); break;
+    case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<L_KCONTIG, ACT_SILU, BF16, 4, 128>, grid, 256, s, g); break;
+    default: launch(gemm_bf16_dma64_kernel<L_KCONTIG, ACT_ID, BF16, 4, 128>, grid, 256, s, g); break;
+  }
+}
+
+void launch_gemm_bf16_dma_narrow(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  if (g.c_dtype == HMX_DTYPE_BF16)
+    launch_bf16_dma_narrow<true>(g, grid, s);
+  else
+    launch_bf16_dma_narrow<false>(g, grid, s);
 }
 
 void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {
