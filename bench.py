@@ -164,7 +164,8 @@ class Linear(Workload):
         self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_BF16_TFLOPS
         self.work = 2.0 * 8192 * 11008 * 4096
         self.dtype = "bf16"
-        self.kernel = "gemm_bf16_dma64_kernel"
+        # 256x256 tiles over the first 10240 columns (five rounds), then 256x128 tiles over the last 768.
+        self.kernel = "gemm_bf16_dma64_kernel (256x256, then 256x128 tail)"
         self.config = {"workload": self.description, "m": 8192, "n": 11008, "k": 4096, "seed": 3}
 
     def step(self):
@@ -249,7 +250,7 @@ class Bmm(Workload):
                             f"S={self.plan['splits']} (config 5)")
         if dtype_name == "f32":
             self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_F32_TFLOPS
-            self.kernel = "gemm_f32_kernel + splitk_reduce_kernel"
+            self.kernel = "gemm_f32_dma_kernel + splitk_reduce_kernel"
         else:
             self.unit, self.bound, self.peak = "GB/s", "hbm", PEAK_HBM_GBS
             self.kernel = "gemm_bf16_dma64_kernel + splitk_reduce_kernel"
