@@ -16,7 +16,7 @@ struct TileChoice {
 
 // Instantiated workgroup tiles, largest first.
 constexpr TileChoice kBf16Tiles[] = {{256, 256, 64}, {128, 128, 64}};
-constexpr TileChoice kF32Tiles[] = {{128, 128, 32}};
+constexpr TileChoice kF32Tiles[] = {{128, 128, 32}, {64, 64, 32}};
 // The f32 tile long-K split-K products of whole 256 x 256 tiles take (see
 // make_plan): one workgroup per CU reading each operand once.
 constexpr TileChoice kF32Big = {256, 256, 32};
@@ -92,6 +92,13 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
     for (int i = 0; i < count; ++i) {
       const int64_t tiles = ceil_div(m, table[i].bm) * ceil_div(n, table[i].bn) * batch;
       if (tiles >= kCus) { pick = i; break; }
+    }
+    // f32: 128 x 128 tiles also when split-K fills the CUs with them (half the
+    // operand traffic of 64 x 64 tiles); 64 x 64 tiles for products too small
+    // for either (512^3: 16 workgroups of 128 x 128, too few K tiles to split).
+    if (!bf16 && pick > 0) {
+      const int64_t t128 = ceil_div(m, 128) * ceil_div(n, 128) * batch;
+      if (t128 * auto_splits(table[0], t128, m, n, k, batch, 4, max_ws) >= kCus) pick = 0;
     }
     // Long-K bf16 products of whole 256 x 256 tiles that split-K can spread
     // over every CU take the big tile: it reads each operand once (half the

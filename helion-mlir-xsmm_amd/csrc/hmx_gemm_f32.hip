@@ -263,8 +263,10 @@ void launch_gemm_f32(const GemmArgs& g, int tile_bm, int la, int lb, bool guard,
                      hipStream_t s) {
   if (tile_bm == 256)
     dispatch_f32<F32Cfg<256, 256, 32>>(g, la, lb, guard, grid, s);
-  else
+  else if (tile_bm == 128)
     dispatch_f32<F32Cfg<128, 128, 32>>(g, la, lb, guard, grid, s);
+  else
+    dispatch_f32<F32Cfg<64, 64, 32>>(g, la, lb, guard, grid, s);
 }
 
 void launch_splitk_reduce(const float* partials, int splits, int64_t batch, const GemmArgs& r,

@@ -150,8 +150,13 @@ def test_plans_of_the_baseline_configs(lib: ctypes.CDLL) -> None:
     assert _plan(lib, bf16, 256, 256, 65536, batch=16)[:4] == (16, 256, 256, 64)
     # Too few K tiles to fill the GPU by splitting: the small tile.
     assert _plan(lib, f32, 256, 256, 4096, batch=16)[1:3] == (128, 128)
-    # The f32 512^3 plumbing case: 16 tiles, partials would cost more than they save.
-    assert _plan(lib, f32, 512, 512, 512)[0] == 1
+    # The f32 512^3 plumbing case: 16 tiles of 128 x 128 and too few K tiles to
+    # split them, so 64 x 64 tiles (64 workgroups), no split.
+    assert _plan(lib, f32, 512, 512, 512)[:3] == (1, 64, 64)
+    # Split-K fills the CUs with 128 x 128 tiles: they stay.
+    assert _plan(lib, f32, 256, 256, 4096, batch=16)[:3] == (4, 128, 128)
+    # A request below every f32 tile gets the smallest.
+    assert _plan(lib, f32, 512, 512, 512, tiles=(32, 32, 32))[1:4] == (64, 64, 32)
 
 
 def test_plan_honours_requests_and_limits(lib: ctypes.CDLL) -> None:
