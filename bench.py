@@ -11,14 +11,16 @@ reports them under ``components``. Other workloads (``--workload``) exist for
 profiling one kernel at a time: gemm, gemm_f32c, gemm_prepacked, linear,
 softmax, softmax_f32, rmsnorm, rmsnorm_f32, bmm, bmm_bf16, matmul_f32.
 
-Timing: W untimed steps, then K steps bracketed by ``torch.cuda.synchronize()``
+Timing: W untimed steps (and more, untimed, until the GPU has run 50 ms of
+them: its clocks ramp up under load), then K steps bracketed by ``torch.cuda.synchronize()``
 and HIP events recorded on the stream the kernels run on (torch's current
-stream, which the library launches on); ``value`` spans all K steps. Each
-step also has its own event pair, recorded by the step's first and last
-kernels themselves (``hmx_time_launches``): ``roofline.achieved`` is the
-algorithmic work per launch of the dominant kernel over the mean of those
-pairs (its average launch duration, as a kernel trace measures it); ``roofline.traffic`` is the HBM bytes per launch measured with
-rocprofv3 counters (``profiles/traffic.json``), or null when not measured.
+stream, which the library launches on); ``value`` spans all K steps. A second
+pass of K steps gives each step its own event pair, recorded by the step's
+first and last kernels themselves (``hmx_time_launches``):
+``roofline.achieved`` is the algorithmic work per launch of the dominant
+kernel over the mean of those pairs (its average launch duration, as a kernel
+trace measures it). ``roofline.traffic`` is the HBM bytes per launch measured
+with rocprofv3 counters (``profiles/traffic.json``), or null when not measured.
 ``cpu_baseline`` times the CPU oracle (``oracle/restate.py``, numpy) on the
 host cores on a bounded sample of the same workload.
 """
@@ -353,18 +355,32 @@ def make(name: str, device) -> Workload:
     }[name]()
 
 
+# Untimed load before the timed region (seconds of back-to-back steps).
+SETTLE_S = 0.05
+
+
 def measure(w: Workload, steps: int, warmup: int) -> dict:
     """Step time (ms) over ``steps`` timed steps, and the average duration of
     one step's kernels, both from HIP events on the stream the library
     launches on (torch's current stream).
 
-    ``ms`` spans the whole timed region (first event to last). For each step,
-    a pair of events is armed in the library (``hmx_time_launches``): the
-    first kernel of the step records the start event as it begins and its last
-    kernel the stop event as it ends, so ``launch_ms`` (the mean of the pairs)
-    is the GPU time of the step's kernels without dispatch latency or host
-    time -- what a kernel trace reports. Workloads that launch no library
-    kernel (the calibration copy) bracket the step with plain event records.
+    ``ms`` spans the timed region: a pair of events around exactly ``steps``
+    back-to-back steps, with nothing else on the stream. Before it, after the
+    ``warmup`` steps, untimed steps continue until the GPU has been busy for
+    SETTLE_S: the clocks ramp up over the first ~10 ms of load (a timed
+    region started right after 10 warmup steps of the 4096^3 GEMM measures
+    ~130 us per step, the next one ~116 us).
+
+    ``launch_ms`` comes from a second pass of ``steps`` steps after it. For
+    each step a pair of events is armed in the library
+    (``hmx_time_launches``): the first kernel of the step records the start
+    event as it begins and its last kernel the stop event as it ends, so
+    ``launch_ms`` (the mean of the pairs) is the GPU time of the step's
+    kernels without host time -- what a kernel trace reports. Kernels that
+    record events are dispatched later than plain launches (a 16 us kernel
+    then takes ~43 us per step instead of 16 us), which is why the step time
+    comes from the uninstrumented pass. Workloads that launch no library
+    kernel (the calibration copy) bracket each step with plain event records.
     """
     import torch
 
@@ -373,8 +389,22 @@ def measure(w: Workload, steps: int, warmup: int) -> dict:
     for _ in range(warmup):
         w.step()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    chunk = 1
+    while time.perf_counter() - t0 < SETTLE_S:
+        for _ in range(chunk):
+            w.step()
+        torch.cuda.synchronize()
+        chunk = min(2 * chunk, 1024)
     begin = torch.cuda.Event(enable_timing=True)
     finish = torch.cuda.Event(enable_timing=True)
+    begin.record()
+    for _ in range(steps):
+        w.step()
+    finish.record()
+    torch.cuda.synchronize()
+    ms = begin.elapsed_time(finish) / steps
+
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     armed = w.library_kernels
@@ -382,7 +412,6 @@ def measure(w: Workload, steps: int, warmup: int) -> dict:
         for ev in starts + ends:  # creates the events; the kernels re-record them
             ev.record()
         torch.cuda.synchronize()
-    begin.record()
     for i in range(steps):
         if armed:
             native.time_launches(starts[i], ends[i])
@@ -393,9 +422,7 @@ def measure(w: Workload, steps: int, warmup: int) -> dict:
             ends[i].record()
     if armed:
         native.time_launches(None, None)
-    finish.record()
     torch.cuda.synchronize()
-    ms = begin.elapsed_time(finish) / steps
     launch_ms = sum(a.elapsed_time(b) for a, b in zip(starts, ends)) / steps
     scale = 1e12 if w.unit == "TFLOP/s" else 1e9
     value = w.work / (ms * 1e-3) / scale

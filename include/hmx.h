@@ -109,7 +109,8 @@ int hmx_device_check(int* compute_units);
  * the calling thread: the next kernel any entry point enqueues records
  * `start_event` when it begins, and every kernel enqueued while armed records
  * `stop_event` when it ends (hipExtLaunchKernelGGL), so the pair spans exactly
- * the kernels of the calls made in between, without their dispatch latency.
+ * the kernels of the calls made in between, without host time. Armed
+ * launches are dispatched later than plain ones: time throughput disarmed.
  * Both NULL disarms. The events must have been created with timing enabled
  * and belong to the device the calls run on. Per-thread state, like the
  * error message. */
