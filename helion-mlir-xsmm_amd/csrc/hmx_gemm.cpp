@@ -329,7 +329,7 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
   if (ab_dtype == HMX_DTYPE_BF16) {
     const TileChoice t = plan.tile;
     if (t.bm == 256 && !guard && la == L_KCONTIG &&
-        (lb_run == L_KCONTIG || lb_run == L_RCONTIG || gemm_bf16_dma_vnni_ok(g, lb_run)) &&
+        (lb_run == L_KCONTIG || lb_run == L_RCONTIG || gemm_bf16_dma_packed_ok(g, lb_run)) &&
         dma_direct_ok(g) && dma_enabled()) {
       const int64_t n1 = lb_run == L_KCONTIG && plan.splits == 1 && batch == 1 && g.k_chunk % 64 == 0
                              ? whole_round_columns(tiles_m, tiles_n)

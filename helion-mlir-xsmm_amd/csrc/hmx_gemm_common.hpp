@@ -309,16 +309,17 @@ void launch_gemm_bf16(const GemmArgs& g, int tile_bm, int la, int lb, bool guard
                       hipStream_t s);
 // hmx_gemm_dma.hip: direct-to-LDS bf16 kernels (64-wide K stages when K
 // chunks are whole 64-element stages, else 32-wide); whole 256 x 256 tiles, A
-// K-contiguous, B K-contiguous or row-major, identity / ReLU / SiLU epilogue.
+// K-contiguous, B K-contiguous, row-major or (64-wide only) packed, identity /
+// ReLU / SiLU epilogue.
 void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s);
 // The 64-wide direct-to-LDS kernel on 256 x 128 tiles (four waves, B
 // [N, K]): the columns past the last whole round of 256 x 256 tiles.
 void launch_gemm_bf16_dma_narrow(const GemmArgs& g, dim3 grid, hipStream_t s);
-// Whether the 64-wide direct-to-LDS kernel reads this VNNI-packed B (VNNI
-// panels or blocked VNNI) in place.
-bool gemm_bf16_dma_vnni_ok(const GemmArgs& g, int lb);
-// hmx_gemm_f32.hip: f32 kernel, tiles 128 x 128 or (split-K partials only)
-// 256 x 256; and the fixed-order split-K reduction into C.
+// Whether the 64-wide direct-to-LDS kernel reads this packed B in place
+// (VNNI panels, blocked VNNI, K-major panels, 32 x 32 blocks).
+bool gemm_bf16_dma_packed_ok(const GemmArgs& g, int lb);
+// hmx_gemm_f32.hip: f32 kernel, tiles 64 x 64, 128 x 128 or (split-K
+// partials only) 256 x 256; and the fixed-order split-K reduction into C.
 // hmx_gemm_dma.hip: direct-to-LDS f32 kernel; whole 256 x 256 tiles of
 // split-K partials (identity epilogue, f32 C), A K-contiguous, B K-contiguous
 // or row-major, K chunks of whole 32-element stages.

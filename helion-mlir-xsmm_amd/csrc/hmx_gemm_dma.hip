@@ -244,7 +244,11 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(GemmArgs g) {
 // have ~one step to land.
 template <int LB, int ACT, bool BF16, int NW, int BN>
 __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
-  constexpr bool BT = LB == L_RCONTIG;             // B row-major [K, N]
+  // B [K, N] row-major, or packed in K-major panels of P columns ([N/P, K, P])
+  // or 32 x 32 blocks ([N/32, K/32, 32 k, 32 n]): each lands in LDS as the
+  // same row-major [64 k][256 n] tile.
+  constexpr bool BPK = LB == L_PANELS || LB == L_BLOCKED;
+  constexpr bool BT = LB == L_RCONTIG || BPK;
   constexpr bool VN = LB == L_VNNI_PANELS;         // B in K-pair (VNNI) panels
   constexpr int BM = 256, BK = 64;
   static_assert(BN == 256 || (BN == 128 && NW == 4 && LB == L_KCONTIG),
@@ -318,6 +322,22 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
       }
       vn_off[q] = (int32_t)off;
     }
+  } else if constexpr (BPK) {
+    // Element (k, n) sits at col(n) + row(k): col(n) = (n / P) K P + n % P,
+    // row(k) = k P (panels); col(n) = (n / 32) (K / 32) 1024 + n % 32,
+    // row(k) = (k / 32) 1024 + (k % 32) 32 (blocks). A lane's 8 columns stay
+    // in one panel or block (P % 8 == 0), and the two rows of a load (k even,
+    // k + 1) are one row stride apart, so the lane offset holds col(n) and the
+    // row within the pair, the scalar offset row(k).
+    const int r = lane >> 5, c = lane & 31;
+    auto col = [&](int64_t n) -> int64_t {
+      if constexpr (LB == L_PANELS) return (n / P) * g.b.kpad * P + n % P;
+      else return (n >> 5) * (g.b.kpad >> 5) * 1024 + (n & 31);
+    };
+    const int64_t rs = LB == L_PANELS ? P : 32;
+    voff_b0 = (int32_t)((col(n0 + (c ^ swz_n(r)) * 8) + r * rs) * 2);
+    voff_b1 = (int32_t)((col(n0 + (c ^ swz_n(r + 2)) * 8) + r * rs) * 2);
+    soff_b = blk_b = 0;
   } else if constexpr (BT) {
     const int r = lane >> 5, c = lane & 31;
     voff_b0 = (int32_t)((r * g.b.ld + (c ^ swz_n(r)) * 8) * 2);      // even q
@@ -343,6 +363,11 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
     } else if constexpr (VN) {
       const int qb = q - LA;
       lds_dma16(srd_b, voff_b0, vn_off[qb] + (int32_t)((k0 / 2) * 4 * P), sb + qb * 1024);
+    } else if constexpr (BPK) {
+      const int qb = q - LA;
+      const int64_t kr = k0 + wave * (64 / NW) + 2 * qb;  // even
+      const int64_t row = LB == L_PANELS ? kr * P : (kr >> 5) * 1024 + (kr & 31) * 32;
+      lds_dma16(srd_b, (qb & 1) ? voff_b1 : voff_b0, (int32_t)(row * 2), sb + qb * 1024);
     } else {
       const int qb = q - LA;
       const int32_t kb = BT ? (int32_t)(k0 * g.b.ld * 2) : (int32_t)(k0 * 2);
@@ -662,11 +687,13 @@ bool dma64_enabled() {
 
 }  // namespace
 
-bool gemm_bf16_dma_vnni_ok(const GemmArgs& g, int lb) {
+bool gemm_bf16_dma_packed_ok(const GemmArgs& g, int lb) {
+  if (!(g.k_chunk % 64 == 0 && g.k % 64 == 0 && dma64_enabled())) return false;
+  if (lb == L_PANELS) return g.b.panel % 8 == 0;
+  if (lb == L_BLOCKED) return true;
   if (lb != L_VNNI_PANELS && lb != L_BLOCKED_VNNI) return false;
   const int64_t p = lb == L_BLOCKED_VNNI ? 32 : g.b.panel;
-  return g.k_chunk % 64 == 0 && g.k % 64 == 0 && g.b.kpad % 2 == 0 && p % 32 == 0 &&
-         (256 % p == 0 || p % 256 == 0) && dma64_enabled();
+  return g.b.kpad % 2 == 0 && p % 32 == 0 && (256 % p == 0 || p % 256 == 0);
 }
 
 template <bool BF16>
@@ -691,6 +718,14 @@ void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {
     GemmArgs v = g;
     if (lb == L_BLOCKED_VNNI) v.b.panel = 32;
     launch_bf16_dma_b<L_VNNI_PANELS, true>(v, grid, s);
+    return;
+  }
+  if (lb == L_PANELS) {
+    launch_bf16_dma_b<L_PANELS, true>(g, grid, s);
+    return;
+  }
+  if (lb == L_BLOCKED) {
+    launch_bf16_dma_b<L_BLOCKED, true>(g, grid, s);
     return;
   }
   const bool k64 = g.k_chunk % 64 == 0 && g.k % 64 == 0 && dma64_enabled();

@@ -344,6 +344,24 @@ def test_matmul_prepacked_vnni_whole_tiles(gpu_device, panel) -> None:
     assert torch.equal(torch.from_numpy(got), plain.cpu().float())
 
 
+@pytest.mark.parametrize("layout", ["panels16", "panels64", "panels256", "panels384", "panels768", "blocked"])
+def test_matmul_prepacked_rowmajor_whole_tiles(gpu_device, layout) -> None:
+    # Whole 256 x 256 tiles with K a multiple of 64: the direct-to-LDS kernel
+    # reads K-major panels [N/P, K, P] (narrower than a tile, one tile, tiles
+    # straddling two panels, wider than a tile) and 32 x 32 blocks in place,
+    # with the fused bias + SiLU epilogue.
+    m, k, n = 512, 320, 768
+    a = tensor(RNG.normal(0, 1, (m, k)).astype(np.float32), "bf16", gpu_device)
+    b = tensor(RNG.normal(0, 1, (k, n)).astype(np.float32), "bf16", gpu_device)
+    bias = tensor(RNG.normal(0, 1, n).astype(np.float32), "bf16", gpu_device)
+    packed = U.pack_b_blocked(b) if layout == "blocked" else U.pack_b_panels(b, int(layout[6:]))
+    got = to_np(U.matmul_prepacked_b(a, packed, n, bias, torch.nn.functional.silu))
+    ref = R.matmul(to_np(a), to_np(b), bias=to_np(bias), act="silu", out="bf16")
+    _check(got, ref, k, to_np(a), to_np(b), "bf16")
+    plain = U.matmul(a, b, bias=bias, epilogue=torch.nn.functional.silu)
+    assert torch.equal(torch.from_numpy(got), plain.cpu().float())
+
+
 def test_matmul_config3_prepacked_layouts(gpu_device) -> None:
     cfg = W.config3(scale=4)  # 1024^3, the config-3 distribution
     a, b = cfg["a"].to(gpu_device), cfg["b"].to(gpu_device)
