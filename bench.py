@@ -80,7 +80,6 @@ class Workload:
     work: float  # algorithmic flops or bytes per step
     dtype: str
     kernel: str  # the dominant kernel's name (rocprof)
-    launches_per_step: int = 1
     library_kernels: bool = True  # a step enqueues libhmx kernels
     config: dict
 
@@ -261,7 +260,6 @@ class Bmm(Workload):
         self.bytes = 16 * (256 * 65536 * 2) * esz + 16 * 256 * 256 * 4
         self.work = self.flops if self.unit == "TFLOP/s" else self.bytes
         self.dtype = dtype_name
-        self.launches_per_step = 2  # the split GEMM and the fixed-order reduction
         self.config = {"workload": self.description, "batch": 16, "m": 256, "n": 256, "k": 65536,
                        "splits": self.plan["splits"], "seed": 4, "values": "U[-1,1]"}
 
@@ -315,7 +313,7 @@ class MatmulF32(Workload):
 
 class Copy(Workload):
     """A plain device copy of known size (torch's copy kernel): the calibration
-    point for the rocprofv3 FETCH_SIZE / WRITE_SIZE counters, not a hot-path op."""
+    point for the rocprofv3 traffic counters, not a hot-path op."""
 
     def __init__(self, device) -> None:
         import torch
@@ -430,8 +428,9 @@ def measure(w: Workload, steps: int, warmup: int) -> dict:
 
 
 def traffic_of(name: str) -> float | None:
-    """HBM bytes per launch of the workload's dominant kernel, from the
-    rocprofv3 FETCH_SIZE/WRITE_SIZE runs recorded in profiles/traffic.json."""
+    """HBM bytes per launch of the step's kernels, from the rocprofv3 counter
+    runs recorded in profiles/traffic.json (L2-to-memory read requests by size,
+    WRITE_SIZE)."""
     path = ROOT / "profiles" / "traffic.json"
     try:
         entry = json.loads(path.read_text()).get(name)
