@@ -9,7 +9,9 @@ HBM. The default workload is BASELINE config 3, the bf16 GEMM 4096^3
 measures config 2's softmax and RMSNorm (bf16, [32768, 4096]) in HBM GB/s and
 reports them under ``components``. Other workloads (``--workload``) exist for
 profiling one kernel at a time: gemm, gemm_f32c, gemm_prepacked, linear,
-softmax, softmax_f32, rmsnorm, rmsnorm_f32, bmm, bmm_bf16, matmul_f32.
+softmax, softmax_f32, rmsnorm, rmsnorm_f32, bmm, bmm_bf16, matmul_f32, and the
+rest of the memory-bound API on BASELINE tensors: layernorm, groupnorm,
+row_sum, column_sum, row_dot, matvec, relu, pack_vnni.
 
 Timing: W untimed steps (and more, untimed, until the GPU has run 50 ms of
 them: its clocks ramp up under load), then K steps bracketed by ``torch.cuda.synchronize()``
@@ -233,6 +235,97 @@ class RowOp(Workload):
                           f"{rows} of {self.x.shape[0]} rows, {reps} reps, {_cpu_model()}"}
 
 
+class MemOp(Workload):
+    """The rest of the memory-bound API, each on a BASELINE tensor: LayerNorm,
+    GroupNorm (32 groups), row_sum, column_sum, row_dot, matvec and relu on
+    config 2's X ([32768, 4096] bf16), and the VNNI weight pack
+    (``pack_b_vnni_t``, 64-column panels) of config 4's W ([11008, 4096] bf16).
+    ``work`` is one HBM read of each input and one write of each output."""
+
+    def __init__(self, device, op: str) -> None:
+        import torch
+
+        import helion_mlir_utils as U
+        import hmx_workloads as W
+
+        self.U, self.op = U, op
+        g = torch.Generator().manual_seed(5)
+        if op == "pack_vnni":
+            self.cpu = {"w": W.config4()["w"]}
+            self.w = self.cpu["w"].to(device)
+            n, k = map(int, self.w.shape)
+            self.work = 2.0 * n * k * 2
+            self.description = f"pack_b_vnni_t [{n}, {k}] bf16, 64-column panels (config 4's weight)"
+            self.kernel = "pack_kernel"
+            self.config = {"workload": self.description, "n": n, "k": k, "panel": 64, "seed": 3}
+        else:
+            cfg = W.config2(torch.bfloat16)
+            x = cfg["x"]
+            m, n = map(int, x.shape)
+            vec = torch.randn(n, generator=g)
+            self.cpu = {"x": x, "w": cfg["weight"].float(), "b": vec * 0.1, "v": vec}
+            self.x = x.to(device)
+            self.w32 = self.cpu["w"].to(device)
+            self.b32 = self.cpu["b"].to(device)
+            self.v32 = vec.to(device)
+            self.v16 = vec.to(torch.bfloat16).reshape(n, 1).to(device)
+            rw = 2.0 * m * n  # X once, bf16
+            self.work = {"layernorm": 2 * rw + 8 * n, "groupnorm": 2 * rw + 8 * n, "row_sum": rw + 2 * m,
+                         "column_sum": rw + 4 * n, "row_dot": rw + 4 * n + 2 * m, "matvec": rw + 2 * n + 2 * m,
+                         "relu": 2 * rw}[op]
+            self.kernel = {"layernorm": "group_norm_cached", "groupnorm": "group_norm_cached",
+                           "row_sum": "row_reduce", "column_sum": "column_sum_kernel", "row_dot": "row_reduce",
+                           "matvec": "row_reduce", "relu": "elementwise_kernel"}[op]
+            self.description = f"{op} [{m}, {n}] bf16 (config 2's X)"
+            self.config = {"workload": self.description, "m": m, "n": n, "seed": 1, "values": "N(0, std 2)"}
+        self.name = op
+        self.unit, self.bound, self.peak = "GB/s", "hbm", PEAK_HBM_GBS
+        self.dtype = "bf16"
+
+    def step(self):
+        U = self.U
+        if self.op == "pack_vnni":
+            return U.pack_b_vnni_t(self.w, 64)
+        if self.op == "layernorm":
+            return U.layer_norm(self.x, self.w32, self.b32, 1e-5)
+        if self.op == "groupnorm":
+            return U.group_norm(self.x, 32, self.w32, self.b32, 1e-5)
+        if self.op == "row_sum":
+            return U.row_sum(self.x)
+        if self.op == "column_sum":
+            return U.column_sum(self.x)
+        if self.op == "row_dot":
+            return U.row_dot(self.x, self.v32)
+        if self.op == "matvec":
+            return U.matvec(self.x, self.v16)
+        return U.relu(self.x)
+
+    def cpu_baseline(self) -> dict:
+        from oracle import restate as R
+
+        if self.op == "pack_vnni":
+            rows = 1024
+            w = self.cpu["w"][:rows].float().numpy()
+            rate, reps = _time_cpu(lambda: R.pack_b_vnni_t(w, 64), self.work * rows / self.w.shape[0])
+            return {"value": rate / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                    "sample": f"oracle.restate.pack_b_vnni_t on the first {rows} of {self.w.shape[0]} rows, "
+                              f"{reps} reps, {_cpu_model()}"}
+        rows = 4096
+        x = self.cpu["x"][:rows].float().numpy()
+        w, b, v = (self.cpu[k].numpy() for k in ("w", "b", "v"))
+        fn = {"layernorm": lambda: R.group_norm(x, 1, w, b, 1e-5, out="bf16"),
+              "groupnorm": lambda: R.group_norm(x, 32, w, b, 1e-5, out="bf16"),
+              "row_sum": lambda: R.row_sum(x, out="bf16"),
+              "column_sum": lambda: R.column_sum(x),
+              "row_dot": lambda: R.row_dot(x, v, out="bf16"),
+              "matvec": lambda: R.matvec(x, v, out="bf16"),
+              "relu": lambda: R.relu(x, out="bf16")}[self.op]
+        rate, reps = _time_cpu(fn, self.work * rows / self.x.shape[0])
+        return {"value": rate / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"oracle.restate ({self.op}) on the first {rows} of {self.x.shape[0]} rows, {reps} reps, "
+                          f"{_cpu_model()}"}
+
+
 class Bmm(Workload):
     def __init__(self, device, dtype_name: str) -> None:
         import torch
@@ -336,6 +429,9 @@ class Copy(Workload):
         return {"value": None, "unit": "GB/s", "cores": 0, "kind": "port", "sample": "none (calibration workload)"}
 
 
+MEM_OPS = ("layernorm", "groupnorm", "row_sum", "column_sum", "row_dot", "matvec", "relu", "pack_vnni")
+
+
 def make(name: str, device) -> Workload:
     return {
         "gemm": lambda: Gemm(device),
@@ -350,6 +446,7 @@ def make(name: str, device) -> Workload:
         "bmm_bf16": lambda: Bmm(device, "bf16"),
         "matmul_f32": lambda: MatmulF32(device),
         "copy": lambda: Copy(device),
+        **{op: (lambda op=op: MemOp(device, op)) for op in MEM_OPS},
     }[name]()
 
 

@@ -94,6 +94,66 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
   }
 }
 
+// VNNI panels of a transposed bf16 weight W [N, K] (row stride ld, K even):
+// dst[jp][c][n] (32-bit words, [N_pad/P][K_pad/2][P]) = the K pair
+// (W[jp P + n][2c], W[jp P + n][2c + 1]), zero past N and K. Viewing W's rows
+// as words, a panel is the transpose of a [P, K/2] word matrix, so each
+// workgroup transposes a 64 x 64 word tile through LDS: four threads read 64
+// contiguous bytes of each of 64 rows, four threads write 64 contiguous bytes
+// of each of 64 output rows (P a multiple of 64: a tile's columns stay in one
+// panel). VEC: rows keep 16-byte alignment (ld % 8 == 0, 16-byte aligned W).
+template <bool VEC>
+__global__ __launch_bounds__(256) void pack_vnni_t_kernel(const uint16_t* __restrict__ w,
+                                                          uint32_t* __restrict__ dst, int64_t n_rows,
+                                                          int64_t k, int64_t ld, int64_t kp_words,
+                                                          int64_t panel) {
+  constexpr int PITCH = 65;
+  __shared__ uint32_t tile[64 * PITCH];
+  const int t = threadIdx.x;
+  const int64_t n0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+  const int64_t kw = k / 2;  // words per source row
+  {
+    const int nl = t >> 2, cq = (t & 3) * 16;
+    const int64_t n = n0 + nl;
+    const uint32_t* row = (const uint32_t*)(w + n * ld);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t c = c0 + cq + 4 * q;
+      uint32_t v[4] = {0u, 0u, 0u, 0u};
+      if (n < n_rows) {
+        if (VEC && c + 4 <= kw) {
+          const uint4 u = *(const uint4*)(row + c);
+          v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (c + e < kw) v[e] = row[c + e];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tile[nl * PITCH + cq + 4 * q + e] = v[e];
+    }
+  }
+  __syncthreads();
+  {
+    const int cl = t >> 2, nq = (t & 3) * 16;
+    const int64_t c = c0 + cl;
+    if (c < kp_words) {
+      const int64_t jp = n0 / panel;
+      uint32_t* out = dst + (jp * kp_words + c) * panel + (n0 % panel) + nq;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint4 u;
+        u.x = tile[(nq + 4 * q) * PITCH + cl];
+        u.y = tile[(nq + 4 * q + 1) * PITCH + cl];
+        u.z = tile[(nq + 4 * q + 2) * PITCH + cl];
+        u.w = tile[(nq + 4 * q + 3) * PITCH + cl];
+        *(uint4*)(out + 4 * q) = u;
+      }
+    }
+  }
+}
+
 // Transpose of 16-bit elements, [rows, cols] (row stride ld) -> [cols, rows]
 // contiguous. Each lane moves an 8 x 8 block: eight 16-byte row loads, a
 // register transpose (v_perm_b32), eight 16-byte stores; a wave covers a
@@ -201,6 +261,20 @@ extern "C" int hmx_pack(int kind, int dtype, const void* src, int64_t rows, int6
       cols_pad == lcols && rows > 0 && cols > 0) {
     launch_transpose16(src, dst, rows, cols, ld, s);
     return check_launch("pack transpose");
+  }
+  if (kind == HMX_PACK_B_VNNI_PANELS_T && dtype == HMX_DTYPE_BF16 && panel % 64 == 0 && rows > 0 &&
+      cols % 2 == 0 && ld % 2 == 0 && ((uintptr_t)src & 3) == 0 && aligned16(dst) &&
+      ceil_div(rows_pad / 2, 64) <= 65535) {
+    // rows = N, cols = K of the stored W; rows_pad = K_pad, cols_pad = N_pad.
+    const dim3 grid((unsigned)(cols_pad / 64), (unsigned)ceil_div(rows_pad / 2, 64));
+    const bool vec = ld % 8 == 0 && aligned16(src);
+    if (vec)
+      launch(pack_vnni_t_kernel<true>, grid, 256, s, (const uint16_t*)src, (uint32_t*)dst, rows, cols, ld,
+             rows_pad / 2, panel);
+    else
+      launch(pack_vnni_t_kernel<false>, grid, 256, s, (const uint16_t*)src, (uint32_t*)dst, rows, cols, ld,
+             rows_pad / 2, panel);
+    return check_launch("pack VNNI panels");
   }
   const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(a.total, 256), 65536);
   if (dtype == HMX_DTYPE_BF16)

@@ -353,7 +353,26 @@ struct GroupNormArgs {
   int extra_op;
   int act;
   float act_arg;
+  // w, b and extra are 16-byte aligned: with vectorizable rows (gs a
+  // multiple of EPV), each row vector's EPV channels load as one piece.
+  bool vec_ok;
 };
+
+// `fill` for a null vector, else EPV consecutive values from index i (a
+// multiple of EPV) of a 16-byte aligned f32 or bf16 vector, with 16-byte loads
+// where the run fills them.
+template <int EPV>
+__device__ __forceinline__ void load_vec_any(const void* p, int dtype, int64_t i, float (&out)[EPV],
+                                             float fill) {
+  if (!p) {
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) out[e] = fill;
+  } else if (dtype == HMX_DTYPE_F32) {
+    load_vec_run<float, EPV>((const float*)p, i + EPV, i, true, out);
+  } else {
+    load_vec_run<uint16_t, EPV>((const uint16_t*)p, i + EPV, i, true, out);
+  }
+}
 
 __device__ __forceinline__ float group_norm_out(const GroupNormArgs& a, float centered,
                                                 float r, int64_t ch) {
@@ -388,6 +407,25 @@ __global__ __launch_bounds__(kMaxBlock) void group_norm_cached(const T* x, T* y,
   const float r = rsqrtf(row_sum_all(q, red_var, wpr) / (float)n + a.eps);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
+    if constexpr (EPV > 1) {
+      const int64_t col0 = col_of<EPV>(j, p.li, p.tpr, 0);
+      if (a.vec_ok && (WHOLE || col0 + EPV <= n)) {
+        // The same arithmetic as group_norm_out, on whole vectors of w, b, extra.
+        float wv[EPV], bv[EPV], ev[EPV];
+        load_vec_any<EPV>(a.w, a.vec_dtype, g * n + col0, wv, 1.f);
+        load_vec_any<EPV>(a.b, a.vec_dtype, g * n + col0, bv, 0.f);
+        load_vec_any<EPV>(a.extra_op != HMX_EXTRA_NONE ? a.extra : nullptr, a.vec_dtype, g * n + col0, ev, 0.f);
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+          float yv = (v[j * EPV + e] - mean) * r * wv[e];
+          yv += bv[e];
+          if (a.extra_op == HMX_EXTRA_ADD) yv += ev[e];
+          if (a.extra_op == HMX_EXTRA_MUL) yv *= ev[e];
+          v[j * EPV + e] = apply_activation(a.act, yv, a.act_arg);
+        }
+        continue;
+      }
+    }
 #pragma unroll
     for (int e = 0; e < EPV; ++e) {
       const int64_t col = col_of<EPV>(j, p.li, p.tpr, e);
@@ -472,15 +510,70 @@ __global__ __launch_bounds__(kBlock) void row_reduce(const T* x,
 
 // Column sums: one thread per column walks all rows (each row read by a wave
 // as one contiguous run); f32 accumulation in row order.
-template <typename T>
-__global__ __launch_bounds__(256) void column_sum_kernel(const T* x,
-                                                         float* __restrict__ y, int64_t m,
-                                                         int64_t n) {
-  const int64_t col = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (col >= n) return;
-  float s = 0.f;
-  for (int64_t r = 0; r < m; ++r) s += Elem<T>::load(x + r * n + col);
-  y[col] = s + 0.f;
+// Column sums in two passes, so that every CU streams rows and the result
+// does not depend on scheduling. Pass 1: workgroup (b, c) sums the rows of
+// chunk c for the 64 columns of block b: 64 / EPV threads across the columns
+// (one 16-byte vector each, a whole 128- or 256-byte line per row) times
+// 256 / (64 / EPV) threads down the rows, which are then added in thread
+// order through LDS; the chunk's sums go to `part` ([chunks, n] f32), or
+// straight to y (+ 0.0) when there is one chunk. Pass 2 adds the chunks in
+// chunk order.
+constexpr int kColBlock = 64;
+
+template <typename T, int EPV>
+__global__ __launch_bounds__(256) void column_partial_kernel(const T* x, float* __restrict__ part,
+                                                             int64_t m, int64_t n, int64_t rows_per_chunk,
+                                                             bool final) {
+  constexpr int TC = kColBlock / EPV, TR = 256 / TC;
+  __shared__ float sums[TR][kColBlock];
+  const int tc = threadIdx.x % TC, tr = threadIdx.x / TC;
+  const int64_t col = (int64_t)blockIdx.x * kColBlock + tc * EPV;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per_chunk;
+  const int64_t r1 = min(m, r0 + rows_per_chunk);
+  float acc[EPV];
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) acc[e] = 0.f;
+  if (col < n) {
+    int64_t r = r0 + tr;
+    // Four rows in flight per thread.
+    for (; r + 3 * TR < r1; r += 4 * TR) {
+      float v[4][EPV];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) load_chunk<T, EPV>(x + (r + u * TR) * n, n, col, v[u], 0.f);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) acc[e] += v[u][e];
+    }
+    for (; r < r1; r += TR) {
+      float v[EPV];
+      load_chunk<T, EPV>(x + r * n, n, col, v, 0.f);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) acc[e] += v[e];
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < EPV; ++e) sums[tr][tc * EPV + e] = acc[e];
+  __syncthreads();
+  if (threadIdx.x < kColBlock) {
+    const int64_t c = (int64_t)blockIdx.x * kColBlock + threadIdx.x;
+    float s = sums[0][threadIdx.x];
+    for (int q = 1; q < TR; ++q) s += sums[q][threadIdx.x];
+    if (c < n) {
+      if (final) part[c] = s + 0.f;
+      else part[blockIdx.y * n + c] = s;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void column_final_kernel(const float* __restrict__ part,
+                                                           float* __restrict__ y, int64_t chunks,
+                                                           int64_t n) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= n) return;
+  float s = part[c];
+  for (int64_t q = 1; q < chunks; ++q) s += part[q * n + c];
+  y[c] = s + 0.f;
 }
 
 // Elementwise ops over 16-byte vectors (EPV elements), scalar tail.
@@ -680,7 +773,8 @@ int hmx_group_norm_rows(int dtype, const void* x, const void* w, const void* b,
   HMX_REQUIRE(units <= kMaxGrid, "group_norm: too many rows");
   if (units == 0) return HMX_OK;
   GroupNormArgs a{w, b, extra, vec_dtype, units, groups, group_size, eps,
-                  extra_op, activation, activation_arg};
+                  extra_op, activation, activation_arg,
+                  aligned16(w) && aligned16(b) && aligned16(extra)};
   auto s = (hipStream_t)stream;
   with_type(dtype, rows_vectorizable(x, y, group_size, dtype), [&](auto tp, auto epv_c) {
     using T = std::remove_pointer_t<decltype(tp)>;
@@ -745,17 +839,45 @@ int hmx_matvec(int dtype, const void* a, const void* x, void* y, int64_t m, int6
   return row_reduce_launch("matvec", 2, dtype, a, x, y, m, k, HMX_EPI_IDENTITY, 0.f, stream);
 }
 
-int hmx_column_sum(int dtype, const void* x, float* y, int64_t m, int64_t n, void* stream) {
+// Row chunks of a column sum: about 2048 workgroups, at least 256 rows each.
+static void column_chunks(int64_t m, int64_t n, int64_t& chunks, int64_t& rows_per_chunk) {
+  const int64_t blocks = std::max<int64_t>(1, ceil_div(n, kColBlock));
+  chunks = std::max<int64_t>(1, std::min(ceil_div(2048, blocks), ceil_div(m, 256)));
+  rows_per_chunk = ceil_div(m, chunks);
+  chunks = rows_per_chunk > 0 ? ceil_div(m, rows_per_chunk) : 1;
+}
+
+int hmx_column_sum_plan(int64_t m, int64_t n, int64_t* workspace_bytes) {
+  HMX_REQUIRE(m >= 0 && n >= 0 && workspace_bytes, "column_sum_plan: invalid arguments");
+  int64_t chunks, rows;
+  column_chunks(m, n, chunks, rows);
+  *workspace_bytes = chunks > 1 ? chunks * n * (int64_t)sizeof(float) : 0;
+  return HMX_OK;
+}
+
+int hmx_column_sum(int dtype, const void* x, float* y, int64_t m, int64_t n, void* workspace,
+                   int64_t workspace_bytes, void* stream) {
   HMX_REQUIRE(valid_dtype(dtype), "column_sum: unknown dtype %d", dtype);
   HMX_REQUIRE(m >= 0 && n >= 0, "column_sum: invalid shape");
   HMX_REQUIRE((x || m == 0) && y, "column_sum: null operand");  // no rows: x is not read
   if (n == 0) return HMX_OK;
+  int64_t chunks, rows;
+  column_chunks(m, n, chunks, rows);
+  HMX_REQUIRE(chunks <= 65535 && ceil_div(n, kColBlock) <= kMaxGrid, "column_sum: too many columns");
+  const int64_t need = chunks > 1 ? chunks * n * (int64_t)sizeof(float) : 0;
+  HMX_REQUIRE(need == 0 || (workspace && workspace_bytes >= need),
+              "column_sum: workspace of %lld bytes needed (hmx_column_sum_plan), %lld given",
+              (long long)need, (long long)workspace_bytes);
   auto s = (hipStream_t)stream;
-  const dim3 grid((unsigned)ceil_div(n, 256));
-  if (dtype == HMX_DTYPE_BF16)
-    launch(column_sum_kernel<uint16_t>, grid, 256, s, (const uint16_t*)x, y, m, n);
-  else
-    launch(column_sum_kernel<float>, grid, 256, s, (const float*)x, y, m, n);
+  float* part = chunks > 1 ? (float*)workspace : y;
+  const dim3 grid((unsigned)ceil_div(n, kColBlock), (unsigned)chunks);
+  with_type(dtype, rows_vectorizable(x, x, n, dtype), [&](auto tp, auto epv_c) {
+    using T = std::remove_pointer_t<decltype(tp)>;
+    constexpr int EPV = decltype(epv_c)::value;
+    launch(column_partial_kernel<T, EPV>, grid, 256, s, (const T*)x, part, m, n, rows, chunks == 1);
+  });
+  if (chunks > 1)
+    launch(column_final_kernel, dim3((unsigned)ceil_div(n, 256)), 256, s, (const float*)part, y, chunks, n);
   return check_launch("column_sum");
 }
 

@@ -25,6 +25,7 @@ import torch
 from ..support.errors import UnsupportedTargetError
 
 LIBRARY_ENV = "HMX_LIBRARY"
+ABI_VERSION = 2  # HMX_ABI_VERSION of include/hmx.h
 NATIVE_CALL_ENV = "HELION_MLIR_NATIVE_CALL"
 _DEFAULT = Path(__file__).resolve().parents[3] / "csrc" / "libhmx.so"
 
@@ -83,7 +84,8 @@ SIGNATURES: dict[str, list[object]] = {
     "hmx_rmsnorm_rows": [_I, _P, _P, _I, _P, _L, _L, _F, _P],
     "hmx_group_norm_rows": [_I, _P, _P, _P, _P, _I, _P, _L, _L, _L, _F, _I, _I, _F, _P],
     "hmx_row_sum": [_I, _P, _P, _L, _L, _I, _F, _P],
-    "hmx_column_sum": [_I, _P, _P, _L, _L, _P],
+    "hmx_column_sum": [_I, _P, _P, _L, _L, _P, _L, _P],
+    "hmx_column_sum_plan": [_L, _L, _P],
     "hmx_row_dot": [_I, _P, _P, _P, _L, _L, _I, _F, _P],
     "hmx_matvec": [_I, _P, _P, _P, _L, _L, _P],
     "hmx_elementwise": [_I, _I, _P, _P, _L, _F, _P],
@@ -121,8 +123,8 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.argtypes = argtypes
             fn.restype = _RESTYPES.get(name, ctypes.c_int)
-        if handle.hmx_abi_version() != 1:
-            raise RuntimeError(f"{path}: ABI version {handle.hmx_abi_version()}, expected 1")
+        if handle.hmx_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{path}: ABI version {handle.hmx_abi_version()}, expected {ABI_VERSION}")
         _lib.append(handle)
         return handle
 

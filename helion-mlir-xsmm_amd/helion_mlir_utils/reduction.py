@@ -7,6 +7,7 @@ element of ``x`` is read once, f32 accumulation, one rounding.
 
 from __future__ import annotations
 
+import ctypes
 from typing import Callable
 
 import torch
@@ -84,8 +85,14 @@ def column_sum(x: Tensor) -> Tensor:
     out = output_pool.empty((n,), dtype=torch.float32, device=x.device)
     if n == 0:
         return out
+    ws_bytes = ctypes.c_int64()
+    native.check(native.lib().hmx_column_sum_plan(m, n, ctypes.byref(ws_bytes)), "hmx_column_sum_plan")
+    # Row-chunk partials (kept alive by `ws` until the call is enqueued; torch's
+    # stream-ordered allocator keeps them until the kernels have run).
+    ws = torch.empty(ws_bytes.value, dtype=torch.uint8, device=x.device) if ws_bytes.value else None
     with on_device(x.device) as stream:
-        native.call("hmx_column_sum", native.dtype_code(x.dtype), x.data_ptr(), out.data_ptr(), m, n, stream)
+        native.call("hmx_column_sum", native.dtype_code(x.dtype), x.data_ptr(), out.data_ptr(), m, n,
+                    native.ptr(ws), ws_bytes.value, stream)
     return out
 
 

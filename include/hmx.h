@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 1
+#define HMX_ABI_VERSION 2
 
 /* Status codes. */
 #define HMX_OK 0
@@ -187,10 +187,15 @@ int hmx_group_norm_rows(int dtype, const void* x, const void* w, const void* b,
 int hmx_row_sum(int dtype, const void* x, void* y, int64_t m, int64_t n,
                 int activation, float activation_arg, void* stream);
 
-/* y[j] = sum_i x[i, j] of contiguous [M, N] into f32 y [N]. Stands in for
- * column_sum (helion_mlir_utils/reduction.py:124-163). */
+/* y[j] = sum_i x[i, j] of contiguous [M, N] into f32 y [N], in two passes
+ * (row chunks into f32 partials in `workspace`, then the chunks added in
+ * order, so results do not depend on timing). Stands in for column_sum
+ * (helion_mlir_utils/reduction.py:124-163). */
 int hmx_column_sum(int dtype, const void* x, float* y, int64_t m, int64_t n,
-                   void* stream);
+                   void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The workspace hmx_column_sum needs for [M, N] (0: none). Host-only. */
+int hmx_column_sum_plan(int64_t m, int64_t n, int64_t* workspace_bytes);
 
 /* y[i] = act(sum_j x[i, j] * v[j]), v f32 [N], y [M] in dtype. Stands in for
  * row_dot (helion_mlir_utils/reduction.py:166-212). */

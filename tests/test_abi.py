@@ -60,7 +60,7 @@ def test_binding_covers_the_header() -> None:
 
 
 def test_abi_version(lib: ctypes.CDLL) -> None:
-    assert lib.hmx_abi_version() == 1
+    assert lib.hmx_abi_version() == native.ABI_VERSION == 2
 
 
 @pytest.mark.parametrize(
@@ -157,6 +157,26 @@ def test_plans_of_the_baseline_configs(lib: ctypes.CDLL) -> None:
     assert _plan(lib, f32, 256, 256, 4096, batch=16)[:3] == (4, 128, 128)
     # A request below every f32 tile gets the smallest.
     assert _plan(lib, f32, 512, 512, 512, tiles=(32, 32, 32))[1:4] == (64, 64, 32)
+
+
+def test_column_sum_plan_and_workspace_check(lib: ctypes.CDLL) -> None:
+    def plan(m: int, n: int) -> int:
+        ws = ctypes.c_int64(-1)
+        assert lib.hmx_column_sum_plan(m, n, ctypes.byref(ws)) == 0
+        return ws.value
+
+    # 64 column blocks x 32 chunks of 1024 rows: [32, 4096] f32 partials.
+    assert plan(32768, 4096) == 32 * 4096 * 4
+    # Enough column blocks (or too few rows) for one pass: no workspace.
+    assert plan(16, 100000) == 0
+    assert plan(0, 10) == 0
+    # 300 rows, one column block: two chunks of 150 rows.
+    assert plan(300, 8) == 2 * 8 * 4
+    # A workspace below the plan is refused before anything is enqueued.
+    x = ctypes.c_void_p(256)
+    y = ctypes.c_void_p(512)
+    st = lib.hmx_column_sum(native.DTYPE_F32, x, y, 32768, 4096, ctypes.c_void_p(1024), 4096, None)
+    assert st == native.ERR_INVALID and "workspace" in native.last_error()
 
 
 def test_plan_honours_requests_and_limits(lib: ctypes.CDLL) -> None:

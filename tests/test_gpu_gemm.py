@@ -286,6 +286,18 @@ def test_pack_kernels_match_oracle(gpu_device, rows, cols, dtype) -> None:
         np.testing.assert_array_equal(to_np(U.pack_a_panels(x, 16)), R.pack_a_panels(xs, 16))
 
 
+@pytest.mark.parametrize(("n", "k"), [(1000, 4096), (130, 70), (64, 2), (257, 520)])
+@pytest.mark.parametrize("panel", [64, 128, 256])
+def test_pack_vnni_t_tiled_transpose(gpu_device, n, k, panel) -> None:
+    # pack_b_vnni_t with panels of a multiple of 64 columns runs the tiled
+    # word transpose: 16-byte row loads when K % 8 == 0, 4-byte loads
+    # otherwise (K = 70), zero padding past N and K, bit-exact.
+    w = tensor(RNG.normal(0, 1, (n + 1, k)).astype(np.float32), "bf16", gpu_device)
+    np.testing.assert_array_equal(to_np(U.pack_b_vnni_t(w[:n], panel)), R.pack_b_vnni_t(to_np(w[:n]), panel))
+    # A row-offset view (its base moves by one row of K values).
+    np.testing.assert_array_equal(to_np(U.pack_b_vnni_t(w[1:], panel)), R.pack_b_vnni_t(to_np(w[1:]), panel))
+
+
 @pytest.mark.parametrize("mkn", [(64, 256, 128), (40, 66, 100), (64, 4096, 64), (300, 128, 64), (33, 64, 70)])
 @pytest.mark.parametrize("panel", [64, 128])
 def test_matmul_prepacked_vnni(gpu_device, mkn, panel) -> None:

@@ -184,6 +184,20 @@ def test_reductions_match_oracle(gpu_device, m: int, n: int, dtype: str) -> None
     assert_close(got, R.matvec(xs, to_np(xv), out=dtype), rtol, atol)
 
 
+@pytest.mark.parametrize(("m", "n"), [(5000, 300), (70000, 64), (4096, 4096), (1025, 517), (257, 1)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_column_sum_row_chunks(gpu_device, m: int, n: int, dtype: str) -> None:
+    # Several row chunks (partials in the workspace, added in chunk order),
+    # ragged column blocks, and a row-offset view whose rows lose 16-byte
+    # alignment when n is odd (the scalar loads).
+    x = tensor(RNG.normal(0, 1, (m, n)).astype(np.float32), dtype, gpu_device)
+    got = U.column_sum(x)
+    assert torch.equal(got, U.column_sum(x))
+    xs = to_np(x)
+    assert_close(to_np(got), R.column_sum(xs), 1e-4, 1e-4 * np.sqrt(m))
+    assert_close(to_np(U.column_sum(x[1:])), R.column_sum(xs[1:]), 1e-4, 1e-4 * np.sqrt(m))
+
+
 @pytest.mark.parametrize("numel", [1, 7, 4096, 1000003])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_elementwise_matches_oracle(gpu_device, numel: int, dtype: str) -> None:
