@@ -4,8 +4,9 @@
 // A row (or one (row, group) unit) is read once from HBM with 16-byte loads
 // (`global_load_dwordx4`) into registers, reduced, and written once with
 // non-temporal stores: one HBM read and one write per element, the floor for
-// these ops. Short rows (at most two vectors per lane of one wave) take one
-// wave each, four rows per 256-thread workgroup. Longer rows take a whole
+// these ops. Rows of at most 64 vectors take the smallest power-of-two group
+// of lanes that holds them (several rows per wave), rows of up to 128
+// vectors one wave each (four rows per 256-thread workgroup). Longer rows take a whole
 // workgroup of WPR waves (up to 16) holding two or more vectors per lane and
 // combine the per-wave reductions through LDS: a [32768, 4096] f32 softmax
 // runs 32768 workgroups of 8 waves with 8 values per lane, which measures
@@ -92,45 +93,43 @@ __device__ __forceinline__ int64_t col_of(int j, int li, int tpr, int e) {
   return ((int64_t)j * tpr + li) * EPV + e;
 }
 
-// Where a thread of a cached-row kernel sits: `wpr` waves per row and
-// blockDim.x / (64 * wpr) rows per workgroup (wpr == 1: one wave per row;
-// wpr > 1: one row per workgroup).
+// Where a thread of a cached-row kernel sits: `tpr` threads per row, a power
+// of two. tpr <= 64: 64 / tpr rows per wave (aligned lane groups) and
+// blockDim.x / tpr rows per workgroup; tpr > 64: tpr / 64 waves per row, one
+// row per workgroup.
 struct RowPos {
   int64_t row;
   int li;   // index among the row's threads
   int tpr;  // threads per row
-  int wpr;
 };
 
-__device__ __forceinline__ RowPos row_pos(int wpr) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
-  const int rows = blockDim.x / (wpr * kWave);
-  return RowPos{(int64_t)blockIdx.x * rows + wave / wpr, (wave % wpr) * kWave + lane,
-                wpr * kWave, wpr};
+__device__ __forceinline__ RowPos row_pos(int tpr) {
+  return RowPos{(int64_t)blockIdx.x * (blockDim.x / tpr) + threadIdx.x / tpr, (int)(threadIdx.x % tpr), tpr};
 }
 
-// Sum / max over all threads of a row: xor butterflies in each wave, then
-// (wpr > 1) the waves' partials through LDS, combined in wave order by every
-// thread, so all threads hold the same value. Each call site passes its own
-// `slot` array (kMaxWavesPerRow floats): no slot is written twice.
-__device__ __forceinline__ float row_sum_all(float v, float* slot, int wpr) {
-  v = wave_sum(v);
-  if (wpr > 1) {
+// Sum / max over all threads of a row: xor butterflies within the row's lane
+// group (offsets below min(tpr, 64)), then (tpr > 64) the waves' partials
+// through LDS, combined in wave order by every thread, so all threads hold the
+// same value. Each call site passes its own `slot` array (kMaxWavesPerRow
+// floats): no slot is written twice.
+__device__ __forceinline__ float row_sum_all(float v, float* slot, int tpr) {
+  for (int off = (tpr < kWave ? tpr : kWave) >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  if (tpr > kWave) {
     if ((threadIdx.x & (kWave - 1)) == 0) slot[threadIdx.x >> 6] = v;
     __syncthreads();
     v = slot[0];
-    for (int q = 1; q < wpr; ++q) v += slot[q];
+    for (int q = 1; q < tpr / kWave; ++q) v += slot[q];
   }
   return v;
 }
 
-__device__ __forceinline__ float row_max_all(float v, float* slot, int wpr) {
-  v = wave_max(v);
-  if (wpr > 1) {
+__device__ __forceinline__ float row_max_all(float v, float* slot, int tpr) {
+  for (int off = (tpr < kWave ? tpr : kWave) >> 1; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  if (tpr > kWave) {
     if ((threadIdx.x & (kWave - 1)) == 0) slot[threadIdx.x >> 6] = v;
     __syncthreads();
     v = slot[0];
-    for (int q = 1; q < wpr; ++q) v = fmaxf(v, slot[q]);
+    for (int q = 1; q < tpr / kWave; ++q) v = fmaxf(v, slot[q]);
   }
   return v;
 }
@@ -208,20 +207,20 @@ __device__ __forceinline__ int64_t unit_index() {
 // Softmax: max, sum of exp(x - max), then exp(x - max) * (1 / sum), as
 // helion_mlir_utils/normalization.py:47-72 computes it (f32 inside, one
 // rounding), with the row held in registers between the passes. The grid
-// holds exactly the rows (wpr > 1: one workgroup per row), so no thread that
+// holds exactly the rows (tpr > 64: one workgroup per row), so no thread that
 // reaches a barrier has returned early.
 template <typename T, int EPV, int VPL, bool WHOLE>
 __global__ __launch_bounds__(kMaxBlock) void softmax_cached(const T* x, T* y, int64_t m,
-                                                            int64_t n, int wpr) {
+                                                            int64_t n, int tpr) {
   __shared__ float red_max[kMaxWavesPerRow], red_sum[kMaxWavesPerRow];
-  const RowPos p = row_pos(wpr);
+  const RowPos p = row_pos(tpr);
   if (p.row >= m) return;
   float v[VPL * EPV];
   load_row<T, EPV, VPL, WHOLE>(x + p.row * n, n, p.li, p.tpr, v, -INFINITY);
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) mx = fmaxf(mx, v[i]);
-  mx = row_max_all(mx, red_max, wpr);
+  mx = row_max_all(mx, red_max, tpr);
   const float ml = mx * kLog2e;
   float sum = 0.f;
 #pragma unroll
@@ -229,7 +228,7 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_cached(const T* x, T* y, in
     v[i] = exp_shifted(v[i], ml);
     if (WHOLE || col_of<EPV>(i / EPV, p.li, p.tpr, i % EPV) < n) sum += v[i];
   }
-  sum = row_sum_all(sum, red_sum, wpr);
+  sum = row_sum_all(sum, red_sum, tpr);
   const float inv = 1.f / sum;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) v[i] *= inv;
@@ -278,16 +277,16 @@ __global__ __launch_bounds__(kBlock) void softmax_stream(const T* x,
 template <typename T, typename W, int EPV, int VPL, bool WHOLE>
 __global__ __launch_bounds__(kMaxBlock) void rmsnorm_cached(const T* x, const W* __restrict__ w,
                                                             bool w_vec, T* y, int64_t m,
-                                                            int64_t n, float eps, int wpr) {
+                                                            int64_t n, float eps, int tpr) {
   __shared__ float red_sum[kMaxWavesPerRow];
-  const RowPos p = row_pos(wpr);
+  const RowPos p = row_pos(tpr);
   if (p.row >= m) return;
   float v[VPL * EPV];
   load_row<T, EPV, VPL, WHOLE>(x + p.row * n, n, p.li, p.tpr, v, 0.f);
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) ss = __builtin_fmaf(v[i], v[i], ss);
-  ss = row_sum_all(ss, red_sum, wpr);
+  ss = row_sum_all(ss, red_sum, tpr);
   const float r = rsqrtf(ss / (float)n + eps);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
@@ -385,9 +384,9 @@ __device__ __forceinline__ float group_norm_out(const GroupNormArgs& a, float ce
 
 template <typename T, int EPV, int VPL, bool WHOLE>
 __global__ __launch_bounds__(kMaxBlock) void group_norm_cached(const T* x, T* y, GroupNormArgs a,
-                                                               int wpr) {
+                                                               int tpr) {
   __shared__ float red_mean[kMaxWavesPerRow], red_var[kMaxWavesPerRow];
-  const RowPos p = row_pos(wpr);
+  const RowPos p = row_pos(tpr);
   const int64_t unit = p.row;
   if (unit >= a.units) return;
   const int64_t g = unit % a.groups;
@@ -397,14 +396,14 @@ __global__ __launch_bounds__(kMaxBlock) void group_norm_cached(const T* x, T* y,
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) s += v[i];
-  const float mean = row_sum_all(s, red_mean, wpr) / (float)n;
+  const float mean = row_sum_all(s, red_mean, tpr) / (float)n;
   float q = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) {
     const float c = v[i] - mean;
     if (WHOLE || col_of<EPV>(i / EPV, p.li, p.tpr, i % EPV) < n) q += c * c;
   }
-  const float r = rsqrtf(row_sum_all(q, red_var, wpr) / (float)n + a.eps);
+  const float r = rsqrtf(row_sum_all(q, red_var, tpr) / (float)n + a.eps);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     if constexpr (EPV > 1) {
@@ -603,39 +602,46 @@ __global__ __launch_bounds__(256) void elementwise_kernel(const T* x,
 // Host dispatch.
 
 // Layout of a cached row kernel for rows of n elements in vectors of epv:
-// one wave per row (four rows per workgroup) while a row is at most two
-// vectors per lane; longer rows get a workgroup of wpr waves with two vectors
-// per lane, wpr doubling up to 16, then more vectors per lane up to
-// kMaxPerLane values. vpl == 0: the row needs the streaming kernel.
+// rows of at most 64 vectors take the smallest power-of-two lane group that
+// holds them (one vector per lane; e.g. GroupNorm's 128-channel bf16 groups:
+// four groups per wave); rows of up to 128 vectors one wave (two vectors per
+// lane); longer rows a workgroup of tpr / 64 waves with two vectors per
+// lane, doubling up to 16 waves, then more vectors per lane up to kMaxPerLane
+// values. vpl == 0: the row needs the streaming kernel.
 struct RowShape {
-  int wpr;
+  int tpr;  // threads per row (a power of two; up to 64 * kMaxWavesPerRow)
   int vpl;
-  bool whole;  // n == wpr * 64 * vpl * epv with 16-byte vectors: no guards
+  bool whole;  // n == tpr * vpl * epv with 16-byte vectors: no guards
 };
 
 RowShape row_shape(int64_t n, int epv) {
   const int64_t vecs = ceil_div(n, epv);
-  RowShape r{1, 0, false};
-  if (vecs <= 2 * kWave) {
-    r.vpl = vecs <= kWave ? 1 : 2;
+  RowShape r{kWave, 0, false};
+  if (vecs <= kWave) {
+    // The smallest lane group holding the row: 64 / tpr rows per wave.
+    r.vpl = 1;
+    r.tpr = 1;
+    while (r.tpr < vecs) r.tpr *= 2;
+  } else if (vecs <= 2 * kWave) {
+    r.vpl = 2;
   } else {
-    r.wpr = 2;
-    while (r.wpr < kMaxWavesPerRow && (int64_t)r.wpr * kWave * 2 < vecs) r.wpr *= 2;
+    r.tpr = 2 * kWave;
+    while (r.tpr < kMaxWavesPerRow * kWave && (int64_t)r.tpr * 2 < vecs) r.tpr *= 2;
     for (int vpl = 2; vpl * epv <= kMaxPerLane; vpl *= 2)
-      if ((int64_t)r.wpr * kWave * vpl >= vecs) {
+      if ((int64_t)r.tpr * vpl >= vecs) {
         r.vpl = vpl;
         break;
       }
   }
-  r.whole = r.vpl > 0 && epv > 1 && n == (int64_t)r.wpr * kWave * r.vpl * epv;
+  r.whole = r.vpl > 0 && epv > 1 && n == (int64_t)r.tpr * r.vpl * epv;
   return r;
 }
 
 // Workgroups and threads per workgroup of a cached kernel over `units` rows.
 int64_t row_grid(int64_t units, const RowShape& r) {
-  return r.wpr == 1 ? ceil_div(units, kRowsPerBlock) : units;
+  return r.tpr <= kWave ? ceil_div(units, kBlock / r.tpr) : units;
 }
-unsigned row_block(const RowShape& r) { return r.wpr == 1 ? kBlock : r.wpr * kWave; }
+unsigned row_block(const RowShape& r) { return r.tpr <= kWave ? kBlock : r.tpr; }
 
 template <int V>
 using IntC = std::integral_constant<int, V>;
@@ -715,7 +721,7 @@ int hmx_softmax_rows(int dtype, const void* x, void* y, int64_t m, int64_t n,
     }
     with_shape<EPV>(r, [&](auto vpl_c, auto whole_c) {
       launch(softmax_cached<T, EPV, decltype(vpl_c)::value, decltype(whole_c)::value>,
-             dim3((unsigned)row_grid(m, r)), row_block(r), s, (const T*)x, (T*)y, m, n, r.wpr);
+             dim3((unsigned)row_grid(m, r)), row_block(r), s, (const T*)x, (T*)y, m, n, r.tpr);
     });
   });
   return check_launch("softmax");
@@ -746,7 +752,7 @@ int hmx_rmsnorm_rows(int dtype, const void* x, const void* w, int w_dtype, void*
       with_shape<EPV>(r, [&](auto vpl_c, auto whole_c) {
         launch(rmsnorm_cached<T, W, EPV, decltype(vpl_c)::value, decltype(whole_c)::value>,
                dim3((unsigned)row_grid(m, r)), row_block(r), s, (const T*)x, (const W*)w, w_vec,
-               (T*)y, m, n, eps, r.wpr);
+               (T*)y, m, n, eps, r.tpr);
       });
     };
     if (w != nullptr && w_dtype == HMX_DTYPE_BF16)
@@ -786,7 +792,7 @@ int hmx_group_norm_rows(int dtype, const void* x, const void* w, const void* b,
     }
     with_shape<EPV>(r, [&](auto vpl_c, auto whole_c) {
       launch(group_norm_cached<T, EPV, decltype(vpl_c)::value, decltype(whole_c)::value>,
-             dim3((unsigned)row_grid(units, r)), row_block(r), s, (const T*)x, (T*)y, a, r.wpr);
+             dim3((unsigned)row_grid(units, r)), row_block(r), s, (const T*)x, (T*)y, a, r.tpr);
     });
   });
   return check_launch("group_norm");

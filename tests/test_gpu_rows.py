@@ -15,6 +15,7 @@ import pytest
 import torch
 
 import helion_mlir_utils as U
+from helion_mlir_backend._compiler import native
 import hmx_workloads as W
 from oracle import restate as R
 from tests.helpers import assert_close, max_rel_error, tensor, to_np
@@ -150,6 +151,37 @@ def test_group_norm_matches_oracle(gpu_device, m: int, c: int, groups: int, dtyp
     inplace = U.group_norm(y, groups, w, b, 1e-5, in_place=True)
     assert inplace.data_ptr() == pointer
     assert torch.equal(inplace, U.group_norm(x, groups, w, b, 1e-5))
+
+
+@pytest.mark.parametrize("groups", [32, 64, 512])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_group_norm_lane_groups(gpu_device, groups: int, dtype: str) -> None:
+    # Groups of 128, 64 and 8 channels: several groups per wave (lane groups of
+    # 4-32 lanes), 1001 rows so the last wave is partly filled.
+    m, c = 1001, 4096
+    x = tensor((RNG.normal(0, 3, (m, c)) + 1.5).astype(np.float32), dtype, gpu_device)
+    w = tensor(RNG.normal(0, 1, c).astype(np.float32), dtype, gpu_device)
+    b = tensor(RNG.normal(0, 1, c).astype(np.float32), dtype, gpu_device)
+    got = to_np(U.group_norm(x, groups, w, b, 1e-5))
+    ref = R.group_norm(to_np(x), groups, to_np(w), to_np(b), 1e-5, out=dtype)
+    rtol, atol = _tol(dtype)
+    assert_close(got, ref, rtol, atol * 10)
+
+
+@pytest.mark.parametrize(("dtype", "c"), [("bf16", 4096), ("f32", 4096), ("bf16", 1000)])
+def test_group_norm_bf16_vectors_through_the_abi(gpu_device, dtype: str, c: int) -> None:
+    # bf16 weight, bias and extra operand (the C ABI takes either vector
+    # dtype), loaded a row vector at a time where the rows allow it.
+    m, groups = 33, 8
+    x = tensor(RNG.normal(0, 2, (m, c)).astype(np.float32), dtype, gpu_device)
+    w, b, e = (tensor(RNG.normal(0, 1, c).astype(np.float32), "bf16", gpu_device) for _ in range(3))
+    y = torch.empty_like(x)
+    native.call("hmx_group_norm_rows", native.dtype_code(x.dtype), x.data_ptr(), w.data_ptr(), b.data_ptr(),
+                e.data_ptr(), native.DTYPE_BF16, y.data_ptr(), m, groups, c // groups, 1e-5, native.EXTRA_ADD,
+                native.EPI_RELU, 0.0, torch.cuda.current_stream().cuda_stream)
+    ref = R.group_norm(to_np(x), groups, to_np(w), to_np(b), 1e-5, to_np(e), "add", "relu", out=dtype)
+    rtol, atol = _tol(dtype)
+    assert_close(to_np(y), ref, rtol, atol * 10)
 
 
 def test_group_norm_epilogues_and_layer_norm(gpu_device) -> None:
