@@ -98,10 +98,10 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
 // dst[jp][c][n] (32-bit words, [N_pad/P][K_pad/2][P]) = the K pair
 // (W[jp P + n][2c], W[jp P + n][2c + 1]), zero past N and K. Viewing W's rows
 // as words, a panel is the transpose of a [P, K/2] word matrix, so each
-// workgroup transposes a 64 x 64 word tile through LDS: four threads read 64
-// contiguous bytes of each of 64 rows, four threads write 64 contiguous bytes
-// of each of 64 output rows (P a multiple of 64: a tile's columns stay in one
-// panel). VEC: rows keep 16-byte alignment (ld % 8 == 0, 16-byte aligned W).
+// workgroup transposes a 64 x 64 word tile through LDS: each load (store)
+// instruction has 16 threads cover one row's 256 bytes, 16 rows per pass,
+// four passes (P a multiple of 64: a tile's columns stay in one panel).
+// VEC: rows keep 16-byte alignment (ld % 8 == 0, 16-byte aligned W).
 template <bool VEC>
 __global__ __launch_bounds__(256) void pack_vnni_t_kernel(const uint16_t* __restrict__ w,
                                                           uint32_t* __restrict__ dst, int64_t n_rows,
@@ -109,47 +109,41 @@ __global__ __launch_bounds__(256) void pack_vnni_t_kernel(const uint16_t* __rest
                                                           int64_t panel) {
   constexpr int PITCH = 65;
   __shared__ uint32_t tile[64 * PITCH];
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, q4 = (t & 15) * 4;
   const int64_t n0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
   const int64_t kw = k / 2;  // words per source row
-  {
-    const int nl = t >> 2, cq = (t & 3) * 16;
-    const int64_t n = n0 + nl;
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int nl = pass * 16 + (t >> 4);
+    const int64_t n = n0 + nl, c = c0 + q4;
     const uint32_t* row = (const uint32_t*)(w + n * ld);
+    uint32_t v[4] = {0u, 0u, 0u, 0u};
+    if (n < n_rows) {
+      if (VEC && c + 4 <= kw) {
+        const uint4 u = *(const uint4*)(row + c);
+        v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+      } else {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t c = c0 + cq + 4 * q;
-      uint32_t v[4] = {0u, 0u, 0u, 0u};
-      if (n < n_rows) {
-        if (VEC && c + 4 <= kw) {
-          const uint4 u = *(const uint4*)(row + c);
-          v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (c + e < kw) v[e] = row[c + e];
-        }
+        for (int e = 0; e < 4; ++e)
+          if (c + e < kw) v[e] = row[c + e];
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) tile[nl * PITCH + cq + 4 * q + e] = v[e];
     }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[nl * PITCH + q4 + e] = v[e];
   }
   __syncthreads();
-  {
-    const int cl = t >> 2, nq = (t & 3) * 16;
+  const int64_t jp = n0 / panel;
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int cl = pass * 16 + (t >> 4);
     const int64_t c = c0 + cl;
     if (c < kp_words) {
-      const int64_t jp = n0 / panel;
-      uint32_t* out = dst + (jp * kp_words + c) * panel + (n0 % panel) + nq;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        uint4 u;
-        u.x = tile[(nq + 4 * q) * PITCH + cl];
-        u.y = tile[(nq + 4 * q + 1) * PITCH + cl];
-        u.z = tile[(nq + 4 * q + 2) * PITCH + cl];
-        u.w = tile[(nq + 4 * q + 3) * PITCH + cl];
-        *(uint4*)(out + 4 * q) = u;
-      }
+      uint4 u;
+      u.x = tile[q4 * PITCH + cl];
+      u.y = tile[(q4 + 1) * PITCH + cl];
+      u.z = tile[(q4 + 2) * PITCH + cl];
+      u.w = tile[(q4 + 3) * PITCH + cl];
+      *(uint4*)(dst + (jp * kp_words + c) * panel + (n0 % panel) + q4) = u;
     }
   }
 }

@@ -570,8 +570,17 @@ __global__ __launch_bounds__(256) void column_final_kernel(const float* __restri
                                                            int64_t n) {
   const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= n) return;
-  float s = part[c];
-  for (int64_t q = 1; q < chunks; ++q) s += part[q * n + c];
+  // Loads in batches of 8 (independent, in flight together), added in order.
+  float s = 0.f;
+  int64_t q = 0;
+  for (; q + 8 <= chunks; q += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = part[(q + u) * n + c];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; q < chunks; ++q) s += part[q * n + c];
   y[c] = s + 0.f;
 }
 
