@@ -1,10 +1,12 @@
 // Layout conversion kernels for gfx950: zero padding and the blocked, VNNI
 // and panel packings of GEMM operands.
 //
-// Every kind is a gather: one thread per destination element computes the
-// logical element (i, j) it holds and reads it from the source (zero past the
-// source's extent), so destination writes are fully coalesced. The logical
-// matrix L is the source or, for the *_T kinds, its transpose.
+// The logical matrix L is the source or, for the *_T kinds, its transpose.
+// Every kind runs as 64 x 64 tiles of L staged through LDS (pack_tiled_kernel)
+// and written in 16-byte destination runs; VNNI panels of a transposed weight
+// with panels of a multiple of 64 columns take a word-transpose kernel; a
+// one-element-per-thread gather (pack_kernel) remains for grids too tall for
+// the tiles.
 #include "hmx_device.hpp"
 
 namespace hmx {
@@ -91,6 +93,150 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
     T v = T(0);
     if (i < a.lrows && j < a.lcols) v = src[a.transposed ? j * a.ld + i : i * a.ld + j];
     dst[d] = v;
+  }
+}
+
+// Destination index of logical element (i, j): the inverse of dst_coords.
+__device__ __forceinline__ int64_t dst_index(const PackArgs& a, int64_t i, int64_t j) {
+  const int64_t rp = a.rows_pad, cp = a.cols_pad, pn = a.panel;
+  switch (a.kind) {
+    case HMX_PACK_A_BLOCKED:
+    case HMX_PACK_A_BLOCKED_T:
+      return (((i >> 5) * (cp >> 5) + (j >> 5)) * 32 + (i & 31)) * 32 + (j & 31);
+    case HMX_PACK_B_BLOCKED:
+    case HMX_PACK_B_BLOCKED_T:
+      return (((j >> 5) * (rp >> 5) + (i >> 5)) * 32 + (i & 31)) * 32 + (j & 31);
+    case HMX_PACK_B_BLOCKED_VNNI:
+    case HMX_PACK_B_BLOCKED_VNNI_T:
+      return (((((j >> 5) * (rp >> 5) + (i >> 5)) * 16 + ((i & 31) >> 1)) * 32 + (j & 31)) * 2) + (i & 1);
+    case HMX_PACK_B_VNNI_PANELS_T:
+      return (((j / pn) * (rp >> 1) + (i >> 1)) * pn + (j % pn)) * 2 + (i & 1);
+    case HMX_PACK_B_PANELS:
+    case HMX_PACK_A_PANELS:
+      return ((j / pn) * rp + i) * pn + (j % pn);
+    default:  // PAD, TRANSPOSE: [RP][CP]
+      return i * cp + j;
+  }
+}
+
+// Columns per destination run that stay contiguous: the 32-wide blocks, the
+// panel, or the whole padded row.
+__device__ __forceinline__ bool run_contiguous(const PackArgs& a, int64_t j, int len) {
+  switch (a.kind) {
+    case HMX_PACK_B_VNNI_PANELS_T:
+    case HMX_PACK_B_PANELS:
+    case HMX_PACK_A_PANELS:
+      return (j % a.panel) + len <= a.panel;
+    case HMX_PACK_PAD:
+    case HMX_PACK_TRANSPOSE:
+      return true;
+    default:
+      return (j & 31) + len <= 32;
+  }
+}
+
+__device__ __forceinline__ bool vnni_kind(int kind) {
+  return kind == HMX_PACK_B_BLOCKED_VNNI || kind == HMX_PACK_B_BLOCKED_VNNI_T ||
+         kind == HMX_PACK_B_VNNI_PANELS_T;
+}
+
+// Eight consecutive elements of stored row `r` from column `c` (zero outside
+// [rows, cols)): 16-byte loads when `vec` (16-byte aligned base and lines).
+template <typename T>
+__device__ __forceinline__ void load8(const T* __restrict__ src, int64_t ld, int64_t r, int64_t c,
+                                      int64_t rows, int64_t cols, bool vec, T (&v)[8]) {
+  if (vec && r < rows && c + 8 <= cols) {
+    const uint4* p = (const uint4*)(src + r * ld + c);
+#pragma unroll
+    for (int h = 0; h < (int)sizeof(T) * 8 / 16; ++h) {
+      const uint4 u = p[h];
+      __builtin_memcpy(&v[h * (16 / (int)sizeof(T))], &u, 16);
+    }
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (r < rows && c + e < cols) ? src[r * ld + c + e] : T(0);
+}
+
+// Every layout of the pack kinds in one tiled kernel: workgroup (bx, by)
+// loads the 64 x 64 tile of the padded logical matrix L at (64 by, 64 bx)
+// into LDS (16-byte row loads; a transposed source is read along its own
+// rows and stored transposed), then writes it as runs of 8 destination
+// elements with 16-byte stores: 8 consecutive columns of one row, or, for the
+// VNNI layouts, 4 columns of a row pair (K pairs are innermost). Runs that
+// leave the padded extent, a block or a panel, or 16-byte alignment, are
+// written element by element. Zero past the source's extent.
+template <typename T>
+__global__ __launch_bounds__(256) void pack_tiled_kernel(PackArgs a, bool vec_src, bool vec_dst) {
+  constexpr int TL = 64, PITCH = TL + 8;
+  __shared__ T tile[TL * PITCH];
+  const T* src = (const T*)a.src;
+  T* dst = (T*)a.dst;
+  const int64_t i0 = (int64_t)blockIdx.y * TL, j0 = (int64_t)blockIdx.x * TL;
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const int rl = (t >> 3) + 32 * pass, cl = (t & 7) * 8;
+    T v[8];
+    if (!a.transposed) {
+      load8<T>(src, a.ld, i0 + rl, j0 + cl, a.lrows, a.lcols, vec_src, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tile[rl * PITCH + cl + e] = v[e];
+    } else {
+      // Stored row j0 + rl holds L's column j0 + rl; its columns are L's rows.
+      load8<T>(src, a.ld, j0 + rl, i0 + cl, a.lcols, a.lrows, vec_src, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tile[(cl + e) * PITCH + rl] = v[e];
+    }
+  }
+  __syncthreads();
+  constexpr int VE = 16 / (int)sizeof(T);  // elements per 16-byte store
+  if (vnni_kind(a.kind)) {
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      const int pl = (t >> 4) + 16 * pass, jl = (t & 15) * 4;  // row pair, 4 columns
+      const int64_t i = i0 + 2 * pl, j = j0 + jl;
+      if (i >= a.rows_pad) continue;
+      const int64_t d = dst_index(a, i, j);
+      if (vec_dst && i + 1 < a.rows_pad && j + 4 <= a.cols_pad && run_contiguous(a, j, 4) && d % VE == 0) {
+        T v[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          v[2 * q] = tile[(2 * pl) * PITCH + jl + q];
+          v[2 * q + 1] = tile[(2 * pl + 1) * PITCH + jl + q];
+        }
+#pragma unroll
+        for (int h = 0; h < 8 / VE; ++h) {
+          uint4 u;
+          __builtin_memcpy(&u, &v[h * VE], 16);
+          *(uint4*)(dst + d + h * VE) = u;
+        }
+      } else {
+        for (int p = 0; p < 2; ++p)
+          for (int q = 0; q < 4; ++q)
+            if (i + p < a.rows_pad && j + q < a.cols_pad)
+              dst[dst_index(a, i + p, j + q)] = tile[(2 * pl + p) * PITCH + jl + q];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      const int rl = (t >> 3) + 32 * pass, cl = (t & 7) * 8;
+      const int64_t i = i0 + rl, j = j0 + cl;
+      if (i >= a.rows_pad) continue;
+      const int64_t d = dst_index(a, i, j);
+      if (vec_dst && j + 8 <= a.cols_pad && run_contiguous(a, j, 8) && d % VE == 0) {
+#pragma unroll
+        for (int h = 0; h < 8 / VE; ++h) {
+          uint4 u;
+          __builtin_memcpy(&u, &tile[rl * PITCH + cl + h * VE], 16);
+          *(uint4*)(dst + d + h * VE) = u;
+        }
+      } else {
+        for (int e = 0; e < 8; ++e)
+          if (j + e < a.cols_pad) dst[dst_index(a, i, j + e)] = tile[rl * PITCH + cl + e];
+      }
+    }
   }
 }
 
@@ -195,6 +341,8 @@ __global__ __launch_bounds__(256) void transpose16_kernel(const uint16_t* __rest
   }
 }
 
+constexpr int64_t kMaxGridX = 0x7fffffff;
+
 bool is_transposed(int kind) {
   return kind == HMX_PACK_A_BLOCKED_T || kind == HMX_PACK_B_BLOCKED_T ||
          kind == HMX_PACK_B_BLOCKED_VNNI_T || kind == HMX_PACK_B_VNNI_PANELS_T ||
@@ -269,6 +417,16 @@ extern "C" int hmx_pack(int kind, int dtype, const void* src, int64_t rows, int6
       launch(pack_vnni_t_kernel<false>, grid, 256, s, (const uint16_t*)src, (uint32_t*)dst, rows, cols, ld,
              rows_pad / 2, panel);
     return check_launch("pack VNNI panels");
+  }
+  if (ceil_div(rows_pad, 64) <= 65535 && ceil_div(cols_pad, 64) <= kMaxGridX) {
+    const int64_t esz = dtype_bytes(dtype);
+    const bool vec_src = aligned16(src) && ld % (16 / esz) == 0;
+    const dim3 grid((unsigned)ceil_div(cols_pad, 64), (unsigned)ceil_div(rows_pad, 64));
+    if (dtype == HMX_DTYPE_BF16)
+      launch(pack_tiled_kernel<uint16_t>, grid, 256, s, a, vec_src, aligned16(dst));
+    else
+      launch(pack_tiled_kernel<float>, grid, 256, s, a, vec_src, aligned16(dst));
+    return check_launch("pack");
   }
   const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(a.total, 256), 65536);
   if (dtype == HMX_DTYPE_BF16)

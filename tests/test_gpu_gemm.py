@@ -265,7 +265,8 @@ def test_bmm_config5_full_size(gpu_device, dtype) -> None:
 # Packing and prepacked GEMMs
 
 
-@pytest.mark.parametrize(("rows", "cols"), [(128, 96), (70, 45), (1, 1), (33, 64)])
+@pytest.mark.parametrize(("rows", "cols"), [(128, 96), (70, 45), (1, 1), (33, 64), (600, 1040), (1040, 600),
+                                          (259, 77)])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_pack_kernels_match_oracle(gpu_device, rows, cols, dtype) -> None:
     x = tensor(RNG.normal(0, 1, (rows, cols)).astype(np.float32), dtype, gpu_device)
