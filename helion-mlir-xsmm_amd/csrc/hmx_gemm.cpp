@@ -128,11 +128,10 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
   plan.splits = splits;
   const int64_t partial_bytes = splits > 1 ? (int64_t)splits * batch * m * n * 4 : 0;
   plan.bt_bytes = ceil_div(n * k * 2, 256) * 256;
-  // Whole 256 x 256 tiles of row-major A read row-major B in place
-  // (direct-to-LDS kernel); other bf16 shapes with enough rows read it
-  // transposed up front.
-  const bool dma_reads_b = plan.tile.bm == 256 && !trans_a && m % 256 == 0 && n % 256 == 0 &&
-                           k % plan.tile.bk == 0 && plan.k_chunk % plan.tile.bk == 0;
+  // 256 x 256 tiles of row-major A with K chunks of whole 64-element stages
+  // read row-major B in place (direct-to-LDS kernel; ragged M and N too);
+  // other bf16 shapes with enough rows read it transposed up front.
+  const bool dma_reads_b = plan.tile.bm == 256 && !trans_a && k % 64 == 0 && plan.k_chunk % 64 == 0;
   plan.transpose_b = bf16 && b_layout == HMX_B_ROW && !dma_reads_b && batch == 1 &&
                      m >= kTransposeMinRows &&
                      n * k * 2 < INT32_MAX &&
@@ -328,10 +327,16 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
   auto s = (hipStream_t)stream;
   if (ab_dtype == HMX_DTYPE_BF16) {
     const TileChoice t = plan.tile;
-    if (t.bm == 256 && !guard && la == L_KCONTIG &&
+    // The direct-to-LDS kernels: row-major A, 16-byte aligned operands whose
+    // spans fit buffer loads, whole 256 x 256 tiles, or ragged M and N with K
+    // chunks of whole 64-element stages and B K-contiguous or row-major.
+    const bool dma_shape = g.a.vec && g.b.vec && bytes_ok &&
+                           (whole || ((lb_run == L_KCONTIG || lb_run == L_RCONTIG) && k % 64 == 0 &&
+                                      plan.k_chunk % 64 == 0));
+    if (t.bm == 256 && dma_shape && la == L_KCONTIG &&
         (lb_run == L_KCONTIG || lb_run == L_RCONTIG || gemm_bf16_dma_packed_ok(g, lb_run)) &&
         dma_direct_ok(g) && dma_enabled()) {
-      const int64_t n1 = lb_run == L_KCONTIG && plan.splits == 1 && batch == 1 && g.k_chunk % 64 == 0
+      const int64_t n1 = whole && lb_run == L_KCONTIG && plan.splits == 1 && batch == 1 && g.k_chunk % 64 == 0
                              ? whole_round_columns(tiles_m, tiles_n)
                              : 0;
       if (n1 > 0) {

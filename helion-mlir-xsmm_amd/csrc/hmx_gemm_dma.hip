@@ -242,7 +242,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(GemmArgs g) {
 // stage t; the next LOADS slots issue the loads of stage t + 2 into it and the
 // last FM + FN slots read stage t + 1's first fragments. The loads of a stage
 // have ~one step to land.
-template <int LB, int ACT, bool BF16, int NW, int BN>
+template <int LB, int ACT, bool BF16, int NW, int BN, bool RAGGED = false>
 __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
   // B [K, N] row-major, or packed in K-major panels of P columns ([N/P, K, P])
   // or 32 x 32 blocks ([N/32, K/32, 32 k, 32 n]): each lands in LDS as the
@@ -253,6 +253,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
   constexpr int BM = 256, BK = 64;
   static_assert(BN == 256 || (BN == 128 && NW == 4 && LB == L_KCONTIG),
                 "256 x 128 tiles: four waves, K-contiguous B");
+  static_assert(!RAGGED || LB == L_KCONTIG || LB == L_RCONTIG, "ragged tiles: B [N, K] or [K, N]");
   constexpr int ROWB = BK * 2;                     // bytes per K-contiguous tile row
   constexpr int NROWB = BN * 2;                    // bytes per row-major B tile row
   constexpr int A_BYTES = BM * ROWB;               // 32 KiB
@@ -293,6 +294,21 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
   const int32_t voff_a0 = kc_voff(g.a.ld, 0), voff_a1 = kc_voff(g.a.ld, 1);
   const int32_t soff_a = (int32_t)((m0 + wave * (256 / NW)) * g.a.ld * 2);
   const int32_t blk_a = (int32_t)(8 * g.a.ld * 2);
+  // RAGGED (M or N not whole tiles): the scalar offset of a buffer load is
+  // not range-checked, so rows (columns) past the edge are not addressed at
+  // all: each lane's offset holds its whole row (column), clamped to the last
+  // row M - 1 (N - 1, or the last 8-column chunk of row-major B), and the
+  // scalar offset only the K position. The duplicated rows and columns reach
+  // only outputs that are never stored.
+  auto kc_voff_clamped = [&](int64_t ld, int64_t row, int64_t rows, int par) {
+    return (int32_t)((min(row, rows - 1) * ld + (slot ^ ((rr >> 1) | (par << 2))) * 8) * 2);
+  };
+  int32_t va[RAGGED ? LA : 1];
+  if constexpr (RAGGED) {
+#pragma unroll
+    for (int q = 0; q < LA; ++q)
+      va[q] = kc_voff_clamped(g.a.ld, m0 + wave * (256 / NW) + q * 8 + rr, g.m, q & 1);
+  }
   // B: K-contiguous as A; row-major: wave w loads K rows Q w .. Q w + Q - 1
   // (Q = 64 / NW) in pairs Q w + 2 q, Q w + 2 q + 1, lane l filling slot
   // l % 32 of row l / 32 of the pair.
@@ -340,15 +356,28 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
     soff_b = blk_b = 0;
   } else if constexpr (BT) {
     const int r = lane >> 5, c = lane & 31;
-    voff_b0 = (int32_t)((r * g.b.ld + (c ^ swz_n(r)) * 8) * 2);      // even q
-    voff_b1 = (int32_t)((r * g.b.ld + (c ^ swz_n(r + 2)) * 8) * 2);  // odd q
-    soff_b = (int32_t)((wave * (64 / NW) * g.b.ld + n0) * 2);
+    if constexpr (RAGGED) {
+      const int64_t last = ((g.n - 1) >> 3) << 3;  // the last 8-column chunk
+      voff_b0 = (int32_t)((r * g.b.ld + min(n0 + (c ^ swz_n(r)) * 8, last)) * 2);
+      voff_b1 = (int32_t)((r * g.b.ld + min(n0 + (c ^ swz_n(r + 2)) * 8, last)) * 2);
+      soff_b = (int32_t)(wave * (64 / NW) * g.b.ld * 2);
+    } else {
+      voff_b0 = (int32_t)((r * g.b.ld + (c ^ swz_n(r)) * 8) * 2);      // even q
+      voff_b1 = (int32_t)((r * g.b.ld + (c ^ swz_n(r + 2)) * 8) * 2);  // odd q
+      soff_b = (int32_t)((wave * (64 / NW) * g.b.ld + n0) * 2);
+    }
     blk_b = (int32_t)(2 * g.b.ld * 2);
   } else {
     voff_b0 = kc_voff(g.b.ld, 0);
     voff_b1 = kc_voff(g.b.ld, 1);
     soff_b = (int32_t)((n0 + wave * (BN / NW)) * g.b.ld * 2);
     blk_b = (int32_t)(8 * g.b.ld * 2);
+  }
+  int32_t vb[RAGGED && !BT && !VN ? LBN : 1];
+  if constexpr (RAGGED && !BT && !VN) {
+#pragma unroll
+    for (int q = 0; q < LBN; ++q)
+      vb[q] = kc_voff_clamped(g.b.ld, n0 + wave * (BN / NW) + q * 8 + rr, g.n, q & 1);
   }
   const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + wave * LA * 1024;
   const uint32_t lds_wb = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + A_BYTES + wave * LBN * 1024;
@@ -359,7 +388,10 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
     const uint32_t st = lds_w + (uint32_t)((t & 1) * STAGE);
     const uint32_t sb = lds_wb + (uint32_t)((t & 1) * STAGE);
     if (q < LA) {
-      lds_dma16(srd_a, (q & 1) ? voff_a1 : voff_a0, soff_a + q * blk_a + (int32_t)(k0 * 2), st + q * 1024);
+      if constexpr (RAGGED)
+        lds_dma16(srd_a, va[q], (int32_t)(k0 * 2), st + q * 1024);
+      else
+        lds_dma16(srd_a, (q & 1) ? voff_a1 : voff_a0, soff_a + q * blk_a + (int32_t)(k0 * 2), st + q * 1024);
     } else if constexpr (VN) {
       const int qb = q - LA;
       lds_dma16(srd_b, voff_b0, vn_off[qb] + (int32_t)((k0 / 2) * 4 * P), sb + qb * 1024);
@@ -368,6 +400,9 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
       const int64_t kr = k0 + wave * (64 / NW) + 2 * qb;  // even
       const int64_t row = LB == L_PANELS ? kr * P : (kr >> 5) * 1024 + (kr & 31) * 32;
       lds_dma16(srd_b, (qb & 1) ? voff_b1 : voff_b0, (int32_t)(row * 2), sb + qb * 1024);
+    } else if constexpr (RAGGED && !BT) {
+      const int qb = q - LA;
+      lds_dma16(srd_b, vb[qb], (int32_t)(k0 * 2), sb + qb * 1024);
     } else {
       const int qb = q - LA;
       const int32_t kb = BT ? (int32_t)(k0 * g.b.ld * 2) : (int32_t)(k0 * 2);
@@ -467,7 +502,11 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
     __builtin_amdgcn_sched_barrier(0);
   }
   wait_vmem<0>();  // no load into LDS outlives the loop
-  epilogue_direct<FM, FN, WM, WN, false, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
+  // RAGGED: tiles that cross M or N store element by element, guarded.
+  if (!RAGGED || (m0 + BM <= g.m && n0 + BN <= g.n))
+    epilogue_direct<FM, FN, WM, WN, false, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
+  else
+    epilogue_direct<FM, FN, WM, WN, true, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -712,7 +751,30 @@ void launch_gemm_bf16_dma_narrow(const GemmArgs& g, dim3 grid, hipStream_t s) {
     launch_bf16_dma_narrow<false>(g, grid, s);
 }
 
+// Output not a whole number of 256 x 256 tiles (K chunks of whole 64-element
+// stages, B K-contiguous or row-major): the eight-wave kernel with clamped
+// edge rows and columns and the guarded edge epilogue.
+template <int LB, bool BF16>
+void launch_bf16_dma_ragged(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  switch (g.act) {
+    case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 8, 256, true>, grid, 512, s, g); break;
+    case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 8, 256, true>, grid, 512, s, g); break;
+    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 8, 256, true>, grid, 512, s, g); break;
+  }
+}
+
 void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {
+  if (g.m % 256 != 0 || g.n % 256 != 0) {
+    const bool bf16 = g.c_dtype == HMX_DTYPE_BF16;
+    if (lb == L_RCONTIG) {
+      if (bf16) launch_bf16_dma_ragged<L_RCONTIG, true>(g, grid, s);
+      else launch_bf16_dma_ragged<L_RCONTIG, false>(g, grid, s);
+    } else {
+      if (bf16) launch_bf16_dma_ragged<L_KCONTIG, true>(g, grid, s);
+      else launch_bf16_dma_ragged<L_KCONTIG, false>(g, grid, s);
+    }
+    return;
+  }
   if (lb == L_VNNI_PANELS || lb == L_BLOCKED_VNNI) {
     // The blocked VNNI layout [N/32, Kp/32, 16, 32, 2] is VNNI panels of 32.
     GemmArgs v = g;

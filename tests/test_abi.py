@@ -135,9 +135,12 @@ def test_plans_of_the_baseline_configs(lib: ctypes.CDLL) -> None:
     # 4096^3 bf16: 256 tiles of 256 x 256 fill the 256 CUs, no split; whole
     # tiles read the row-major B in place, so no workspace.
     assert _plan(lib, bf16, 4096, 4096, 4096) == (1, 256, 256, 64, 0)
-    # Ragged shapes with enough rows transpose B once into the workspace.
-    assert _plan(lib, bf16, 4000, 4096, 4096) == (1, 256, 256, 64, 4096 * 4096 * 2)
-    assert _plan(lib, bf16, 4000, 4096, 4096, max_ws=0) == (1, 256, 256, 64, 0)
+    # Ragged M or N with K in whole 32-element stages: the direct-to-LDS kernel
+    # reads row-major B in place (no transpose); other ragged shapes with
+    # enough rows transpose B once into the workspace.
+    assert _plan(lib, bf16, 4000, 4096, 4096) == (1, 256, 256, 64, 0)
+    assert _plan(lib, bf16, 4000, 4096, 4100) == (1, 256, 256, 64, 4096 * 4100 * 2)
+    assert _plan(lib, bf16, 4000, 4096, 4100, max_ws=0) == (1, 256, 256, 64, 0)
     # Few output rows do not amortize the transpose.
     assert _plan(lib, bf16, 256, 4000, 4096)[4] == 0
     # Fused linear, 8192 x 11008 x 4096 (B row-major here): 1376 tiles, no split.

@@ -112,6 +112,43 @@ def test_matmul_whole_tiles_direct_to_lds(gpu_device, act, out_dtype, trans_b) -
     _check(to_np(got), ref, k, to_np(a), to_np(b), "bf16")
 
 
+# Ragged M and N with K in whole 32- or 64-element stages: the direct-to-LDS
+# kernels with the guarded edge epilogue (tiles that cross M or N).
+@pytest.mark.parametrize("mnk", [(300, 520, 256), (1000, 700, 320), (100, 1000, 512), (520, 260, 96), (257, 255, 64)])
+@pytest.mark.parametrize("trans_b", [False, True])
+@pytest.mark.parametrize(("act", "out_dtype"), [("identity", torch.bfloat16), ("silu", torch.float32),
+                                                ("relu", torch.bfloat16)])
+def test_matmul_ragged_direct_to_lds(gpu_device, mnk, trans_b, act, out_dtype) -> None:
+    m, n, k = mnk
+    a, b = _operands(m, n, k, False, trans_b, "bf16", gpu_device, 0.3)
+    bias = tensor(RNG.normal(0, 1, n).astype(np.float32), "bf16", gpu_device)
+    got = U.matmul(a, b, trans_b=trans_b, bias=bias, epilogue=ACTS[act], out_dtype=out_dtype)
+    out = "bf16" if out_dtype == torch.bfloat16 else "f32"
+    ref = R.matmul(to_np(a), to_np(b), False, trans_b, to_np(bias), act=act, out=out)
+    _check(to_np(got), ref, k, to_np(a), to_np(b), "bf16")
+
+
+def test_matmul_ragged_row_major_b_view(gpu_device) -> None:
+    # N = 203 of a [128, 208] buffer: row-major B whose last column chunk
+    # straddles N (the clamped chunk reads inside the wider rows).
+    a = tensor(RNG.normal(0, 0.3, (300, 128)).astype(np.float32), "bf16", gpu_device)
+    wide = tensor(RNG.normal(0, 0.3, (128, 208)).astype(np.float32), "bf16", gpu_device)
+    b = wide[:, :203]
+    got = to_np(U.matmul(a, b))
+    ref = R.matmul(to_np(a), to_np(b), out="bf16")
+    _check(got, ref, 128, to_np(a), to_np(b), "bf16")
+
+
+def test_bmm_ragged_split_k_direct_to_lds(gpu_device) -> None:
+    a = tensor(RNG.uniform(-1, 1, (2, 300, 4096)).astype(np.float32), "bf16", gpu_device)
+    b = tensor(RNG.uniform(-1, 1, (2, 4096, 200)).astype(np.float32), "bf16", gpu_device)
+    c = U.bmm(a, b, out_dtype=torch.float32, splits=4)
+    assert torch.equal(c, U.bmm(a, b, out_dtype=torch.float32, splits=4))
+    for s in range(2):
+        an, bn = to_np(a)[s], to_np(b)[s]
+        _check(to_np(c)[s], R.matmul(an, bn), 4096, an, bn, "bf16")
+
+
 def test_bmm_whole_tiles_split_k_direct_to_lds(gpu_device) -> None:
     a = tensor(RNG.uniform(-1, 1, (1, 4096, 1024)).astype(np.float32), "bf16", gpu_device)
     b = tensor(RNG.uniform(-1, 1, (1, 1024, 4096)).astype(np.float32), "bf16", gpu_device)
