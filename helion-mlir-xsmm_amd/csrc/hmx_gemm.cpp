@@ -361,6 +361,9 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
       } else {
         launch_gemm_bf16_dma(g, lb_run, grid, s);
       }
+    } else if (t.bm == 128 && la == L_KCONTIG && lb_run == L_KCONTIG && g.a.vec && g.b.vec && bytes_ok &&
+               k % 64 == 0 && plan.k_chunk % 64 == 0 && dma_direct_ok(g) && dma_enabled()) {
+      launch_gemm_bf16_dma128(g, grid, s);
     } else
       launch_gemm_bf16(g, t.bm, la, lb_run, guard, grid, s);
   } else {

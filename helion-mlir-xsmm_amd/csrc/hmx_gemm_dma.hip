@@ -242,7 +242,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(GemmArgs g) {
 // stage t; the next LOADS slots issue the loads of stage t + 2 into it and the
 // last FM + FN slots read stage t + 1's first fragments. The loads of a stage
 // have ~one step to land.
-template <int LB, int ACT, bool BF16, int NW, int BN, bool RAGGED = false>
+template <int LB, int ACT, bool BF16, int NW, int BN, bool RAGGED = false, int BM = 256>
 __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
   // B [K, N] row-major, or packed in K-major panels of P columns ([N/P, K, P])
   // or 32 x 32 blocks ([N/32, K/32, 32 k, 32 n]): each lands in LDS as the
@@ -250,23 +250,27 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
   constexpr bool BPK = LB == L_PANELS || LB == L_BLOCKED;
   constexpr bool BT = LB == L_RCONTIG || BPK;
   constexpr bool VN = LB == L_VNNI_PANELS;         // B in K-pair (VNNI) panels
-  constexpr int BM = 256, BK = 64;
+  constexpr int BK = 64;
   static_assert(BN == 256 || (BN == 128 && NW == 4 && LB == L_KCONTIG),
-                "256 x 128 tiles: four waves, K-contiguous B");
+                "256 x 128 and 128 x 128 tiles: four waves, K-contiguous B");
+  static_assert(BM == 256 || (BM == 128 && BN == 128), "128-row tiles are 128 x 128");
   static_assert(!RAGGED || LB == L_KCONTIG || LB == L_RCONTIG, "ragged tiles: B [N, K] or [K, N]");
   constexpr int ROWB = BK * 2;                     // bytes per K-contiguous tile row
   constexpr int NROWB = BN * 2;                    // bytes per row-major B tile row
-  constexpr int A_BYTES = BM * ROWB;               // 32 KiB
-  constexpr int STAGE = A_BYTES + BN * BK * 2;     // 64 KiB (48 KiB for 256 x 128 tiles)
-  // NW = 4: one wave per SIMD, 2 x 2 waves of 128 x BN / 2 outputs; NW = 8:
+  constexpr int A_BYTES = BM * ROWB;               // 32 KiB (16 KiB for 128-row tiles)
+  constexpr int STAGE = A_BYTES + BN * BK * 2;     // 64 KiB (48 or 32 KiB for the smaller tiles)
+  // NW = 4: one wave per SIMD, 2 x 2 waves of BM / 2 x BN / 2 outputs; NW = 8:
   // two per SIMD, 2 x 4 waves of 128 x 64.
-  constexpr int WM = 128, WN = BN / (NW / 2), FM = WM / 32, FN = WN / 32;
-  constexpr int LA = 32 / NW, LBN = BN / 8 / NW;   // 1 KiB loads of A / B per wave per stage
+  constexpr int WM = BM / 2, WN = BN / (NW / 2), FM = WM / 32, FN = WN / 32;
+  constexpr int LA = BM / 8 / NW, LBN = BN / 8 / NW;  // 1 KiB loads of A / B per wave per stage
   constexpr int LOADS = LA + LBN;
   constexpr int NS = FM * FN, SLOTS = 4 * NS;      // MFMAs per k-step / per stage
   constexpr int NF = FM + FN;                      // fragment reads per k-step
-  constexpr int BAR = NS == 16 ? 44 : 24;          // slot of the stage's wait + barrier
-  static_assert(BAR >= 2 * NS + NF && BAR < SLOTS, "slot plan");
+  // Slot of the stage's wait + barrier: after the last k-step's fragment
+  // reads (slot 2 NS + NF), at or before the next stage's first reads (slot
+  // SLOTS - NF).
+  constexpr int BAR = NS == 16 ? 44 : NS == 8 ? 24 : 12;
+  static_assert(BAR >= 2 * NS + NF && BAR <= SLOTS - NF && BAR < SLOTS, "slot plan");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
 
   int tm, tn;
@@ -292,7 +296,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
     return (int32_t)((rr * ld + (slot ^ ((rr >> 1) | (par << 2))) * 8) * 2);
   };
   const int32_t voff_a0 = kc_voff(g.a.ld, 0), voff_a1 = kc_voff(g.a.ld, 1);
-  const int32_t soff_a = (int32_t)((m0 + wave * (256 / NW)) * g.a.ld * 2);
+  const int32_t soff_a = (int32_t)((m0 + wave * (BM / NW)) * g.a.ld * 2);
   const int32_t blk_a = (int32_t)(8 * g.a.ld * 2);
   // RAGGED (M or N not whole tiles): the scalar offset of a buffer load is
   // not range-checked, so rows (columns) past the edge are not addressed at
@@ -307,7 +311,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
   if constexpr (RAGGED) {
 #pragma unroll
     for (int q = 0; q < LA; ++q)
-      va[q] = kc_voff_clamped(g.a.ld, m0 + wave * (256 / NW) + q * 8 + rr, g.m, q & 1);
+      va[q] = kc_voff_clamped(g.a.ld, m0 + wave * (BM / NW) + q * 8 + rr, g.m, q & 1);
   }
   // B: K-contiguous as A; row-major: wave w loads K rows Q w .. Q w + Q - 1
   // (Q = 64 / NW) in pairs Q w + 2 q, Q w + 2 q + 1, lane l filling slot
@@ -760,6 +764,28 @@ void launch_bf16_dma_ragged(const GemmArgs& g, dim3 grid, hipStream_t s) {
     case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 8, 256, true>, grid, 512, s, g); break;
     case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 8, 256, true>, grid, 512, s, g); break;
     default: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 8, 256, true>, grid, 512, s, g); break;
+  }
+}
+
+// 128 x 128 tiles (four waves of 64 x 64), B K-contiguous, whole or ragged.
+template <bool BF16, bool RAGGED>
+void launch_bf16_dma128_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  switch (g.act) {
+    case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<L_KCONTIG, ACT_RELU, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
+    case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<L_KCONTIG, ACT_SILU, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
+    default: launch(gemm_bf16_dma64_kernel<L_KCONTIG, ACT_ID, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
+  }
+}
+
+void launch_gemm_bf16_dma128(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  const bool ragged = g.m % 128 != 0 || g.n % 128 != 0;
+  const bool bf16 = g.c_dtype == HMX_DTYPE_BF16;
+  if (ragged) {
+    if (bf16) launch_bf16_dma128_c<true, true>(g, grid, s);
+    else launch_bf16_dma128_c<false, true>(g, grid, s);
+  } else {
+    if (bf16) launch_bf16_dma128_c<true, false>(g, grid, s);
+    else launch_bf16_dma128_c<false, false>(g, grid, s);
   }
 }
 

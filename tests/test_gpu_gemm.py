@@ -114,18 +114,34 @@ def test_matmul_whole_tiles_direct_to_lds(gpu_device, act, out_dtype, trans_b) -
 
 # Ragged M and N with K in whole 32- or 64-element stages: the direct-to-LDS
 # kernels with the guarded edge epilogue (tiles that cross M or N).
-@pytest.mark.parametrize("mnk", [(300, 520, 256), (1000, 700, 320), (100, 1000, 512), (520, 260, 96), (257, 255, 64)])
+@pytest.mark.parametrize("mnk", [(300, 520, 256), (1000, 704, 320), (100, 1000, 512), (520, 260, 96), (257, 255, 64),
+                                 (640, 392, 128)])
 @pytest.mark.parametrize("trans_b", [False, True])
 @pytest.mark.parametrize(("act", "out_dtype"), [("identity", torch.bfloat16), ("silu", torch.float32),
                                                 ("relu", torch.bfloat16)])
-def test_matmul_ragged_direct_to_lds(gpu_device, mnk, trans_b, act, out_dtype) -> None:
+@pytest.mark.parametrize("tiles", [(256, 256, 64), (128, 128, 64)])
+def test_matmul_ragged_direct_to_lds(gpu_device, mnk, trans_b, act, out_dtype, tiles) -> None:
+    # 256 x 256 tiles: B [N, K] or [K, N] read in place; 128 x 128 tiles: B
+    # [N, K] (row-major B of 512 rows or more is transposed up front).
     m, n, k = mnk
     a, b = _operands(m, n, k, False, trans_b, "bf16", gpu_device, 0.3)
     bias = tensor(RNG.normal(0, 1, n).astype(np.float32), "bf16", gpu_device)
-    got = U.matmul(a, b, trans_b=trans_b, bias=bias, epilogue=ACTS[act], out_dtype=out_dtype)
+    got = U.matmul(a, b, trans_b=trans_b, bias=bias, epilogue=ACTS[act], out_dtype=out_dtype, block_sizes=tiles)
     out = "bf16" if out_dtype == torch.bfloat16 else "f32"
     ref = R.matmul(to_np(a), to_np(b), False, trans_b, to_np(bias), act=act, out=out)
     _check(to_np(got), ref, k, to_np(a), to_np(b), "bf16")
+
+
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_matmul_ragged_large(gpu_device, trans_b) -> None:
+    # 16 x 16 tiles of 256 x 256, the last row and column of tiles ragged
+    # (4000 = 15 * 256 + 160), chosen by the planner itself.
+    m, n, k = 4000, 4000, 256
+    a, b = _operands(m, n, k, False, trans_b, "bf16", gpu_device, 0.3)
+    c = U.matmul(a, b, trans_b=trans_b)
+    rows = np.concatenate([np.arange(0, 8), np.arange(3830, 3850), np.arange(3990, 4000)])
+    an, bn = to_np(a)[rows], to_np(b)
+    _check(to_np(c)[rows], R.matmul(an, bn, False, trans_b, out="bf16"), k, an, bn, "bf16")
 
 
 def test_matmul_ragged_row_major_b_view(gpu_device) -> None:
