@@ -131,7 +131,8 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
   // 256 x 256 tiles of row-major A with K chunks of whole 64-element stages
   // read row-major B in place (direct-to-LDS kernel; ragged M and N too);
   // other bf16 shapes with enough rows read it transposed up front.
-  const bool dma_reads_b = plan.tile.bm == 256 && !trans_a && k % 64 == 0 && plan.k_chunk % 64 == 0;
+  const bool dma_reads_b = plan.tile.bm == 256 && k % 64 == 0 && plan.k_chunk % 64 == 0 &&
+                           (!trans_a || (m % 256 == 0 && n % 256 == 0));
   plan.transpose_b = bf16 && b_layout == HMX_B_ROW && !dma_reads_b && batch == 1 &&
                      m >= kTransposeMinRows &&
                      n * k * 2 < INT32_MAX &&
@@ -361,6 +362,9 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
       } else {
         launch_gemm_bf16_dma(g, lb_run, grid, s);
       }
+    } else if (t.bm == 256 && la == L_RCONTIG && whole && g.a.vec && g.b.vec && bytes_ok &&
+               (lb_run == L_KCONTIG || lb_run == L_RCONTIG) && dma_direct_ok(g) && dma_enabled()) {
+      launch_gemm_bf16_dma_ta(g, lb_run, grid, s);
     } else if (t.bm == 128 && la == L_KCONTIG && lb_run == L_KCONTIG && g.a.vec && g.b.vec && bytes_ok &&
                k % 64 == 0 && plan.k_chunk % 64 == 0 && dma_direct_ok(g) && dma_enabled()) {
       launch_gemm_bf16_dma128(g, grid, s);

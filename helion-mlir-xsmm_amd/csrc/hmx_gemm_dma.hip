@@ -242,7 +242,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(GemmArgs g) {
 // stage t; the next LOADS slots issue the loads of stage t + 2 into it and the
 // last FM + FN slots read stage t + 1's first fragments. The loads of a stage
 // have ~one step to land.
-template <int LB, int ACT, bool BF16, int NW, int BN, bool RAGGED = false, int BM = 256>
+template <int LB, int ACT, bool BF16, int NW, int BN, bool RAGGED = false, int BM = 256, bool TA = false>
 __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g) {
   // B [K, N] row-major, or packed in K-major panels of P columns ([N/P, K, P])
   // or 32 x 32 blocks ([N/32, K/32, 32 k, 32 n]): each lands in LDS as the
@@ -254,6 +254,10 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
   static_assert(BN == 256 || (BN == 128 && NW == 4 && LB == L_KCONTIG),
                 "256 x 128 and 128 x 128 tiles: four waves, K-contiguous B");
   static_assert(BM == 256 || (BM == 128 && BN == 128), "128-row tiles are 128 x 128");
+  // TA: A stored [K, M] (op(A) = its transpose): its 64 x 256 stage tiles are
+  // loaded and read exactly as row-major B's (512-byte rows, transposing LDS
+  // reads), M in place of N.
+  static_assert(!TA || (BM == 256 && !RAGGED), "transposed A: whole 256 x 256 tiles");
   static_assert(!RAGGED || LB == L_KCONTIG || LB == L_RCONTIG, "ragged tiles: B [N, K] or [K, N]");
   constexpr int ROWB = BK * 2;                     // bytes per K-contiguous tile row
   constexpr int NROWB = BN * 2;                    // bytes per row-major B tile row
@@ -295,9 +299,19 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
   auto kc_voff = [&](int64_t ld, int par) {
     return (int32_t)((rr * ld + (slot ^ ((rr >> 1) | (par << 2))) * 8) * 2);
   };
-  const int32_t voff_a0 = kc_voff(g.a.ld, 0), voff_a1 = kc_voff(g.a.ld, 1);
-  const int32_t soff_a = (int32_t)((m0 + wave * (BM / NW)) * g.a.ld * 2);
-  const int32_t blk_a = (int32_t)(8 * g.a.ld * 2);
+  int32_t voff_a0, voff_a1, soff_a, blk_a;
+  if constexpr (TA) {
+    const int r = lane >> 5, c = lane & 31;
+    voff_a0 = (int32_t)((r * g.a.ld + (c ^ swz_n(r)) * 8) * 2);      // even q
+    voff_a1 = (int32_t)((r * g.a.ld + (c ^ swz_n(r + 2)) * 8) * 2);  // odd q
+    soff_a = (int32_t)((wave * (64 / NW) * g.a.ld + m0) * 2);
+    blk_a = (int32_t)(2 * g.a.ld * 2);
+  } else {
+    voff_a0 = kc_voff(g.a.ld, 0);
+    voff_a1 = kc_voff(g.a.ld, 1);
+    soff_a = (int32_t)((m0 + wave * (BM / NW)) * g.a.ld * 2);
+    blk_a = (int32_t)(8 * g.a.ld * 2);
+  }
   // RAGGED (M or N not whole tiles): the scalar offset of a buffer load is
   // not range-checked, so rows (columns) past the edge are not addressed at
   // all: each lane's offset holds its whole row (column), clamped to the last
@@ -394,6 +408,9 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
     if (q < LA) {
       if constexpr (RAGGED)
         lds_dma16(srd_a, va[q], (int32_t)(k0 * 2), st + q * 1024);
+      else if constexpr (TA)
+        lds_dma16(srd_a, (q & 1) ? voff_a1 : voff_a0, soff_a + q * blk_a + (int32_t)(k0 * g.a.ld * 2),
+                  st + q * 1024);
       else
         lds_dma16(srd_a, (q & 1) ? voff_a1 : voff_a0, soff_a + q * blk_a + (int32_t)(k0 * 2), st + q * 1024);
     } else if constexpr (VN) {
@@ -428,13 +445,18 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
   const int frow = lane & 31, fk = lane >> 5, fswz = swz64(frow);
   const uint8_t* a_frag = lds + (wm * WM + frow) * ROWB;
   const uint8_t* b_frag = lds + A_BYTES + (wn * WN + frow) * ROWB;
-  int b_tr[FN];
+  int b_tr[FN], a_tr[TA ? FM : 1];
   {
     const int gi = lane >> 4, sl = lane & 15;
     const int v = (2 * (gi & 1) + ((sl & 3) >> 1)) ^ swz_n(sl >> 2);
 #pragma unroll
     for (int j = 0; j < FN; ++j)
       b_tr[j] = A_BYTES + (8 * (gi >> 1) + (sl >> 2)) * NROWB + ((wn * (WN / 8) + 4 * j) ^ v) * 16 + 8 * (sl & 1);
+    if constexpr (TA) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        a_tr[i] = (8 * (gi >> 1) + (sl >> 2)) * (BM * 2) + ((wm * (WM / 8) + 4 * i) ^ v) * 16 + 8 * (sl & 1);
+    }
   }
   // VNNI B: column n = wn * 128 + 32 j + lane % 32 needs K pairs
   // 8 ks + 4 (lane / 32) .. + 3 (4 * PL bytes apart), i.e. K values
@@ -449,7 +471,12 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
     }
   }
   auto a_read = [&](int stage, int ks, int i) -> bf16x8_t {
-    return *(const bf16x8_t*)(a_frag + stage * STAGE + i * 32 * ROWB + ((2 * ks + fk) ^ fswz) * 16);
+    if constexpr (TA) {
+      const uint8_t* p = lds + stage * STAGE + a_tr[i] + 16 * ks * (BM * 2);
+      return __builtin_shufflevector(lds_read_tr(p), lds_read_tr(p + 4 * (BM * 2)), 0, 1, 2, 3, 4, 5, 6, 7);
+    } else {
+      return *(const bf16x8_t*)(a_frag + stage * STAGE + i * 32 * ROWB + ((2 * ks + fk) ^ fswz) * 16);
+    }
   };
   auto b_read = [&](int stage, int ks, int j) -> bf16x8_t {
     if constexpr (VN) {
@@ -786,6 +813,28 @@ void launch_gemm_bf16_dma128(const GemmArgs& g, dim3 grid, hipStream_t s) {
   } else {
     if (bf16) launch_bf16_dma128_c<true, false>(g, grid, s);
     else launch_bf16_dma128_c<false, false>(g, grid, s);
+  }
+}
+
+// A stored [K, M] (trans_a), whole 256 x 256 tiles, K chunks of whole
+// 64-element stages, B K-contiguous or row-major: eight waves.
+template <int LB, bool BF16>
+void launch_bf16_dma_ta_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  switch (g.act) {
+    case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 8, 256, false, 256, true>, grid, 512, s, g); break;
+    case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 8, 256, false, 256, true>, grid, 512, s, g); break;
+    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 8, 256, false, 256, true>, grid, 512, s, g); break;
+  }
+}
+
+void launch_gemm_bf16_dma_ta(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {
+  const bool bf16 = g.c_dtype == HMX_DTYPE_BF16;
+  if (lb == L_RCONTIG) {
+    if (bf16) launch_bf16_dma_ta_c<L_RCONTIG, true>(g, grid, s);
+    else launch_bf16_dma_ta_c<L_RCONTIG, false>(g, grid, s);
+  } else {
+    if (bf16) launch_bf16_dma_ta_c<L_KCONTIG, true>(g, grid, s);
+    else launch_bf16_dma_ta_c<L_KCONTIG, false>(g, grid, s);
   }
 }
 

@@ -165,6 +165,29 @@ def test_bmm_ragged_split_k_direct_to_lds(gpu_device) -> None:
         _check(to_np(c)[s], R.matmul(an, bn), 4096, an, bn, "bf16")
 
 
+@pytest.mark.parametrize("trans_b", [False, True])
+@pytest.mark.parametrize(("act", "out_dtype"), [("identity", torch.bfloat16), ("silu", torch.float32)])
+def test_matmul_trans_a_direct_to_lds(gpu_device, trans_b, act, out_dtype) -> None:
+    # A stored [K, M]: its stage tiles are loaded and read as row-major B's.
+    m, n, k = 512, 768, 320
+    a, b = _operands(m, n, k, True, trans_b, "bf16", gpu_device, 0.3)
+    bias = tensor(RNG.normal(0, 1, n).astype(np.float32), "bf16", gpu_device)
+    got = U.matmul(a, b, trans_a=True, trans_b=trans_b, bias=bias, epilogue=ACTS[act], out_dtype=out_dtype,
+                   block_sizes=(256, 256, 64))
+    out = "bf16" if out_dtype == torch.bfloat16 else "f32"
+    ref = R.matmul(to_np(a), to_np(b), True, trans_b, to_np(bias), act=act, out=out)
+    _check(to_np(got), ref, k, to_np(a).T, to_np(b), "bf16")
+
+
+def test_matmul_trans_a_4096(gpu_device) -> None:
+    cfg = W.config3()
+    at = cfg["a"].t().contiguous().to(gpu_device)  # A stored [K, M]
+    c = U.matmul(at, cfg["b"].to(gpu_device), trans_a=True)
+    rows = np.sort(RNG.choice(4096, 64, replace=False))
+    an, bn = to_np(cfg["a"][torch.from_numpy(rows)]), to_np(cfg["b"])
+    _check(to_np(c)[rows], R.matmul(an, bn, out="bf16"), 4096, an, bn, "bf16")
+
+
 def test_bmm_whole_tiles_split_k_direct_to_lds(gpu_device) -> None:
     a = tensor(RNG.uniform(-1, 1, (1, 4096, 1024)).astype(np.float32), "bf16", gpu_device)
     b = tensor(RNG.uniform(-1, 1, (1, 1024, 4096)).astype(np.float32), "bf16", gpu_device)
