@@ -561,9 +561,9 @@ def main() -> int:
     print(f"bench: {w.name} {result['ms']:.4f} ms/step {result['value']:.1f} {w.unit}, "
           f"{result['launch_ms']:.4f} ms/launch", file=sys.stderr, flush=True)
 
-    # The dominant kernel is the step's only launch, except the split-K bmm,
-    # whose step is the split GEMM plus its fixed-order reduction: both are
-    # inside the measured launch time there.
+    # The launch time spans all of a step's kernels: one launch, or two for the
+    # split-K bmm (split GEMM + fixed-order reduction), the linear's whole-round
+    # split (256 x 256 head + 256 x 128 tail) and column_sum (partials + sum).
     per_launch_ms = result["launch_ms"]
     achieved = w.work / (per_launch_ms * 1e-3) / (1e12 if w.unit == "TFLOP/s" else 1e9)
     roofline = {
