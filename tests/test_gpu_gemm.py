@@ -188,6 +188,32 @@ def test_matmul_trans_a_4096(gpu_device) -> None:
     _check(to_np(c)[rows], R.matmul(an, bn, out="bf16"), 4096, an, bn, "bf16")
 
 
+def _random_cases(count: int, seed: int) -> list[tuple]:
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(count):
+        m = int(rng.choice([int(rng.integers(1, 700)), 256 * int(rng.integers(1, 4))]))
+        n = int(rng.choice([int(rng.integers(1, 700)), 256 * int(rng.integers(1, 4))]))
+        k = 64 * int(rng.integers(1, 9)) if rng.random() < 0.8 else int(rng.integers(1, 300))
+        cases.append((m, n, k, bool(rng.random() < 0.3), bool(rng.random() < 0.5),
+                      [None, (256, 256, 64), (128, 128, 64)][int(rng.integers(0, 3))],
+                      ["identity", "relu", "silu"][int(rng.integers(0, 3))], bool(rng.random() < 0.5)))
+    return cases
+
+
+@pytest.mark.parametrize(("m", "n", "k", "trans_a", "trans_b", "tiles", "act", "f32_out"), _random_cases(40, 11))
+def test_matmul_random_shapes(gpu_device, m, n, k, trans_a, trans_b, tiles, act, f32_out) -> None:
+    # Seeded shapes over every bf16 path: whole, ragged and 128 x 128 tiles,
+    # transposed A and B, K in whole stages or not, fused bias + activation.
+    a, b = _operands(m, n, k, trans_a, trans_b, "bf16", gpu_device, 0.3)
+    bias = tensor(RNG.normal(0, 1, n).astype(np.float32), "bf16", gpu_device)
+    out_dtype = torch.float32 if f32_out else torch.bfloat16
+    got = U.matmul(a, b, trans_a=trans_a, trans_b=trans_b, bias=bias, epilogue=ACTS[act], out_dtype=out_dtype,
+                   block_sizes=tiles)
+    ref = R.matmul(to_np(a), to_np(b), trans_a, trans_b, to_np(bias), act=act, out="f32" if f32_out else "bf16")
+    _check(to_np(got), ref, k, to_np(a), to_np(b), "bf16")
+
+
 def test_bmm_whole_tiles_split_k_direct_to_lds(gpu_device) -> None:
     a = tensor(RNG.uniform(-1, 1, (1, 4096, 1024)).astype(np.float32), "bf16", gpu_device)
     b = tensor(RNG.uniform(-1, 1, (1, 1024, 4096)).astype(np.float32), "bf16", gpu_device)
