@@ -153,6 +153,9 @@ def test_plans_of_the_baseline_configs(lib: ctypes.CDLL) -> None:
     assert _plan(lib, bf16, 256, 256, 65536, batch=16)[:4] == (16, 256, 256, 64)
     # Too few K tiles to fill the GPU by splitting: the small tile.
     assert _plan(lib, f32, 256, 256, 4096, batch=16)[1:3] == (128, 128)
+    # A skinny bf16 product (decode-shaped linear): 86 tiles of 128 x 128, split
+    # four ways (one workgroup per CU at most), f32 partials in the workspace.
+    assert _plan(lib, bf16, 32, 11008, 4096) == (4, 128, 128, 64, 4 * 32 * 11008 * 4)
     # The f32 512^3 plumbing case: 16 tiles of 128 x 128 and too few K tiles to
     # split them, so 64 x 64 tiles (64 workgroups), no split.
     assert _plan(lib, f32, 512, 512, 512)[:3] == (1, 64, 64)
