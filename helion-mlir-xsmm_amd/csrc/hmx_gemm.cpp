@@ -130,11 +130,15 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
   plan.splits = splits;
   const int64_t partial_bytes = splits > 1 ? (int64_t)splits * batch * m * n * 4 : 0;
   plan.bt_bytes = ceil_div(n * k * 2, 256) * 256;
-  // 256 x 256 tiles of row-major A with K chunks of whole 64-element stages
-  // read row-major B in place (direct-to-LDS kernel; ragged M and N too);
-  // other bf16 shapes with enough rows read it transposed up front.
-  const bool dma_reads_b = plan.tile.bm == 256 && k % 64 == 0 && plan.k_chunk % 64 == 0 &&
-                           (!trans_a || (m % 256 == 0 && n % 256 == 0));
+  // The direct-to-LDS kernels read row-major B in place (256 x 256 tiles,
+  // ragged M and N too, or transposed A on whole tiles; 128 x 128 tiles of
+  // row-major A) when K chunks are whole 64-element stages; other bf16 shapes
+  // with enough rows read it transposed up front.
+  // (N % 8 == 0: the rows of a contiguous B keep the 16-byte alignment those
+  // loads need.)
+  const bool dma_reads_b = k % 64 == 0 && plan.k_chunk % 64 == 0 && n % 8 == 0 &&
+                           ((plan.tile.bm == 256 && (!trans_a || (m % 256 == 0 && n % 256 == 0))) ||
+                            (plan.tile.bm == 128 && !trans_a));
   plan.transpose_b = bf16 && b_layout == HMX_B_ROW && !dma_reads_b && batch == 1 &&
                      m >= kTransposeMinRows &&
                      n * k * 2 < INT32_MAX &&
@@ -367,9 +371,9 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
     } else if (t.bm == 256 && la == L_RCONTIG && whole && g.a.vec && g.b.vec && bytes_ok &&
                (lb_run == L_KCONTIG || lb_run == L_RCONTIG) && dma_direct_ok(g) && dma_enabled()) {
       launch_gemm_bf16_dma_ta(g, lb_run, grid, s);
-    } else if (t.bm == 128 && la == L_KCONTIG && lb_run == L_KCONTIG && g.a.vec && g.b.vec && bytes_ok &&
-               k % 64 == 0 && plan.k_chunk % 64 == 0 && dma_direct_ok(g) && dma_enabled()) {
-      launch_gemm_bf16_dma128(g, grid, s);
+    } else if (t.bm == 128 && la == L_KCONTIG && (lb_run == L_KCONTIG || lb_run == L_RCONTIG) && g.a.vec &&
+               g.b.vec && bytes_ok && k % 64 == 0 && plan.k_chunk % 64 == 0 && dma_direct_ok(g) && dma_enabled()) {
+      launch_gemm_bf16_dma128(g, lb_run, grid, s);
     } else
       launch_gemm_bf16(g, t.bm, la, lb_run, guard, grid, s);
   } else {

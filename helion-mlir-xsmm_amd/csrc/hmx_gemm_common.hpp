@@ -320,8 +320,8 @@ void launch_gemm_bf16_dma_narrow(const GemmArgs& g, dim3 grid, hipStream_t s);
 // row-major.
 void launch_gemm_bf16_dma_ta(const GemmArgs& g, int lb, dim3 grid, hipStream_t s);
 // The 64-wide direct-to-LDS kernel on 128 x 128 tiles (four waves of 64 x 64,
-// B [N, K], K chunks of whole 64-element stages), whole or ragged.
-void launch_gemm_bf16_dma128(const GemmArgs& g, dim3 grid, hipStream_t s);
+// B [N, K] or [K, N], K chunks of whole 64-element stages), whole or ragged.
+void launch_gemm_bf16_dma128(const GemmArgs& g, int lb, dim3 grid, hipStream_t s);
 // Whether the 64-wide direct-to-LDS kernel reads this packed B in place
 // (VNNI panels, blocked VNNI, K-major panels, 32 x 32 blocks).
 bool gemm_bf16_dma_packed_ok(const GemmArgs& g, int lb);

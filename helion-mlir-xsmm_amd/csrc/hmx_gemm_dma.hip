@@ -251,8 +251,8 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
   constexpr bool BT = LB == L_RCONTIG || BPK;
   constexpr bool VN = LB == L_VNNI_PANELS;         // B in K-pair (VNNI) panels
   constexpr int BK = 64;
-  static_assert(BN == 256 || (BN == 128 && NW == 4 && LB == L_KCONTIG),
-                "256 x 128 and 128 x 128 tiles: four waves, K-contiguous B");
+  static_assert(BN == 256 || (BN == 128 && NW == 4 && (LB == L_KCONTIG || LB == L_RCONTIG)),
+                "256 x 128 and 128 x 128 tiles: four waves, B [N, K] or [K, N]");
   static_assert(BM == 256 || (BM == 128 && BN == 128), "128-row tiles are 128 x 128");
   // TA: A stored [K, M] (op(A) = its transpose): its 64 x 256 stage tiles are
   // loaded and read exactly as row-major B's (512-byte rows, transposing LDS
@@ -372,6 +372,19 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
     voff_b0 = (int32_t)((col(n0 + (c ^ swz_n(r)) * 8) + r * rs) * 2);
     voff_b1 = (int32_t)((col(n0 + (c ^ swz_n(r + 2)) * 8) + r * rs) * 2);
     soff_b = blk_b = 0;
+  } else if constexpr (BT && BN == 128) {
+    // 256-byte rows: a 1 KiB load is 4 K rows, lane l filling slot l % 16 of
+    // row l / 16; row k % 4 == l / 16 for every load, so one lane offset.
+    const int r = lane >> 4, c = lane & 15;
+    if constexpr (RAGGED) {
+      const int64_t last = ((g.n - 1) >> 3) << 3;  // the last 8-column chunk
+      voff_b0 = voff_b1 = (int32_t)((r * g.b.ld + min(n0 + (c ^ swz_n(r)) * 8, last)) * 2);
+      soff_b = (int32_t)(wave * (64 / NW) * g.b.ld * 2);
+    } else {
+      voff_b0 = voff_b1 = (int32_t)((r * g.b.ld + (c ^ swz_n(r)) * 8) * 2);
+      soff_b = (int32_t)((wave * (64 / NW) * g.b.ld + n0) * 2);
+    }
+    blk_b = (int32_t)(4 * g.b.ld * 2);
   } else if constexpr (BT) {
     const int r = lane >> 5, c = lane & 31;
     if constexpr (RAGGED) {
@@ -794,26 +807,35 @@ void launch_bf16_dma_ragged(const GemmArgs& g, dim3 grid, hipStream_t s) {
   }
 }
 
-// 128 x 128 tiles (four waves of 64 x 64), B K-contiguous, whole or ragged.
-template <bool BF16, bool RAGGED>
+// 128 x 128 tiles (four waves of 64 x 64), B K-contiguous or row-major, whole
+// or ragged.
+template <int LB, bool BF16, bool RAGGED>
 void launch_bf16_dma128_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
   switch (g.act) {
-    case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<L_KCONTIG, ACT_RELU, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
-    case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<L_KCONTIG, ACT_SILU, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
-    default: launch(gemm_bf16_dma64_kernel<L_KCONTIG, ACT_ID, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
+    case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
+    case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
+    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
   }
 }
 
-void launch_gemm_bf16_dma128(const GemmArgs& g, dim3 grid, hipStream_t s) {
+template <int LB>
+void launch_bf16_dma128_b(const GemmArgs& g, dim3 grid, hipStream_t s) {
   const bool ragged = g.m % 128 != 0 || g.n % 128 != 0;
   const bool bf16 = g.c_dtype == HMX_DTYPE_BF16;
   if (ragged) {
-    if (bf16) launch_bf16_dma128_c<true, true>(g, grid, s);
-    else launch_bf16_dma128_c<false, true>(g, grid, s);
+    if (bf16) launch_bf16_dma128_c<LB, true, true>(g, grid, s);
+    else launch_bf16_dma128_c<LB, false, true>(g, grid, s);
   } else {
-    if (bf16) launch_bf16_dma128_c<true, false>(g, grid, s);
-    else launch_bf16_dma128_c<false, false>(g, grid, s);
+    if (bf16) launch_bf16_dma128_c<LB, true, false>(g, grid, s);
+    else launch_bf16_dma128_c<LB, false, false>(g, grid, s);
   }
+}
+
+void launch_gemm_bf16_dma128(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {
+  if (lb == L_RCONTIG)
+    launch_bf16_dma128_b<L_RCONTIG>(g, grid, s);
+  else
+    launch_bf16_dma128_b<L_KCONTIG>(g, grid, s);
 }
 
 // A stored [K, M] (trans_a), whole 256 x 256 tiles, K chunks of whole
