@@ -343,7 +343,8 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
     if (t.bm == 256 && dma_shape && la == L_KCONTIG &&
         (lb_run == L_KCONTIG || lb_run == L_RCONTIG || gemm_bf16_dma_packed_ok(g, lb_run)) &&
         dma_direct_ok(g) && dma_enabled()) {
-      const int64_t n1 = whole && lb_run == L_KCONTIG && plan.splits == 1 && batch == 1 && g.k_chunk % 64 == 0
+      const int64_t n1 = whole && (lb_run == L_KCONTIG || lb_run == L_RCONTIG) && plan.splits == 1 &&
+                                 batch == 1 && g.k_chunk % 64 == 0
                              ? whole_round_columns(tiles_m, tiles_n)
                              : 0;
       if (n1 > 0) {
@@ -356,15 +357,16 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
         GemmArgs rest = g;
         rest.n = n - off;
         rest.tiles_n = (int)(rest.n / 128);
-        rest.b.p = (const uint16_t*)g.b.p + off * g.b.ld;
+        // B [N, K]: rows off..; B [K, N]: columns off.. of every row.
+        rest.b.p = (const uint16_t*)g.b.p + (lb_run == L_RCONTIG ? off : off * g.b.ld);
         rest.b.rows = rest.n;
-        rest.b.bytes = (int32_t)(((rest.n - 1) * g.b.ld + k) * 2);
+        rest.b.bytes = (int32_t)((lb_run == L_RCONTIG ? (k - 1) * g.b.ld + rest.n : (rest.n - 1) * g.b.ld + k) * 2);
         rest.c = (char*)g.c + off * dtype_bytes(g.c_dtype);
         const int64_t vb = off * dtype_bytes(vec_dtype);
         if (g.bias) rest.bias = (const char*)g.bias + vb;
         if (g.scale) rest.scale = (const char*)g.scale + vb;
         if (g.shift) rest.shift = (const char*)g.shift + vb;
-        launch_gemm_bf16_dma_narrow(rest, dim3((unsigned)(tiles_m * rest.tiles_n), 1, 1), s);
+        launch_gemm_bf16_dma_narrow(rest, lb_run, dim3((unsigned)(tiles_m * rest.tiles_n), 1, 1), s);
       } else {
         launch_gemm_bf16_dma(g, lb_run, grid, s);
       }

@@ -313,8 +313,8 @@ void launch_gemm_bf16(const GemmArgs& g, int tile_bm, int la, int lb, bool guard
 // ReLU / SiLU epilogue.
 void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s);
 // The 64-wide direct-to-LDS kernel on 256 x 128 tiles (four waves, B
-// [N, K]): the columns past the last whole round of 256 x 256 tiles.
-void launch_gemm_bf16_dma_narrow(const GemmArgs& g, dim3 grid, hipStream_t s);
+// [N, K] or [K, N]): the columns past the last whole round of 256 x 256 tiles.
+void launch_gemm_bf16_dma_narrow(const GemmArgs& g, int lb, dim3 grid, hipStream_t s);
 // The 64-wide direct-to-LDS kernel with A stored [K, M] (trans_a): whole
 // 256 x 256 tiles, K chunks of whole 64-element stages, B K-contiguous or
 // row-major.

@@ -779,20 +779,24 @@ bool gemm_bf16_dma_packed_ok(const GemmArgs& g, int lb) {
   return g.b.kpad % 2 == 0 && p % 32 == 0 && (256 % p == 0 || p % 256 == 0);
 }
 
-template <bool BF16>
+template <int LB, bool BF16>
 void launch_bf16_dma_narrow(const GemmArgs& g, dim3 grid, hipStream_t s) {
   switch (g.act) {
-    case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<L_KCONTIG, ACT_RELU, BF16, 4, 128>, grid, 256, s, g); break;
-    case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<L_KCONTIG, ACT_SILU, BF16, 4, 128>, grid, 256, s, g); break;
-    default: launch(gemm_bf16_dma64_kernel<L_KCONTIG, ACT_ID, BF16, 4, 128>, grid, 256, s, g); break;
+    case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 4, 128>, grid, 256, s, g); break;
+    case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 4, 128>, grid, 256, s, g); break;
+    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 4, 128>, grid, 256, s, g); break;
   }
 }
 
-void launch_gemm_bf16_dma_narrow(const GemmArgs& g, dim3 grid, hipStream_t s) {
-  if (g.c_dtype == HMX_DTYPE_BF16)
-    launch_bf16_dma_narrow<true>(g, grid, s);
-  else
-    launch_bf16_dma_narrow<false>(g, grid, s);
+void launch_gemm_bf16_dma_narrow(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {
+  const bool bf16 = g.c_dtype == HMX_DTYPE_BF16;
+  if (lb == L_RCONTIG) {
+    if (bf16) launch_bf16_dma_narrow<L_RCONTIG, true>(g, grid, s);
+    else launch_bf16_dma_narrow<L_RCONTIG, false>(g, grid, s);
+  } else {
+    if (bf16) launch_bf16_dma_narrow<L_KCONTIG, true>(g, grid, s);
+    else launch_bf16_dma_narrow<L_KCONTIG, false>(g, grid, s);
+  }
 }
 
 // Output not a whole number of 256 x 256 tiles (K chunks of whole 64-element

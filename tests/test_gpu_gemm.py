@@ -248,17 +248,19 @@ def test_matmul_config3_bf16_4096(gpu_device, out_dtype) -> None:
 
 
 @pytest.mark.parametrize("out", ["bf16", "f32"])
-def test_matmul_whole_rounds_split(gpu_device, out) -> None:
+@pytest.mark.parametrize("trans_b", [True, False])
+def test_matmul_whole_rounds_split(gpu_device, out, trans_b) -> None:
     # 16 x 17 = 272 tiles of 256 x 256 on 256 CUs: the first 16 tile columns (one
     # whole round) run as 256 x 256 tiles, the last 256 columns as 256 x 128
-    # tiles (B rows, C columns and bias from column 4096 on). Checked in full.
+    # tiles (B rows or columns, C columns and bias from column 4096 on).
+    # Checked in full.
     m, n, k = 4096, 4352, 320
     a = tensor(RNG.normal(0, 1, (m, k)).astype(np.float32), "bf16", gpu_device)
-    w = tensor(RNG.normal(0, 1, (n, k)).astype(np.float32), "bf16", gpu_device)
+    w = tensor(RNG.normal(0, 1, (n, k) if trans_b else (k, n)).astype(np.float32), "bf16", gpu_device)
     bias = tensor(RNG.normal(0, 1, n).astype(np.float32), "bf16", gpu_device)
     odt = torch.float32 if out == "f32" else None
-    got = to_np(U.matmul(a, w, trans_b=True, bias=bias, epilogue=F.silu, out_dtype=odt))
-    ref = R.matmul(to_np(a), to_np(w), False, True, to_np(bias), act="silu", out=out)
+    got = to_np(U.matmul(a, w, trans_b=trans_b, bias=bias, epilogue=F.silu, out_dtype=odt))
+    ref = R.matmul(to_np(a), to_np(w), False, trans_b, to_np(bias), act="silu", out=out)
     _check(got, ref, k, to_np(a), to_np(w), "bf16")
 
 
