@@ -191,6 +191,35 @@ class Linear(Workload):
                 "sample": f"oracle.restate.matmul on the first {rows} of 8192 rows, {reps} reps, {_cpu_model()}"}
 
 
+class LinearDecode(Linear):
+    """Config 4's layer at decode shape: the first 32 rows of X, so the step
+    streams W once (HBM-bound; the skinny kernel)."""
+
+    ROWS = 32
+
+    def __init__(self, device) -> None:
+        super().__init__(device)
+        r = self.ROWS
+        self.x = self.x[:r].contiguous()
+        self.name = "linear_decode"
+        self.description = f"fused linear SiLU(X @ W^T + b), {r} x 11008 x 4096 (config 4's layer, {r} rows)"
+        self.unit, self.bound, self.peak = "GB/s", "hbm", PEAK_HBM_GBS
+        # W, X and b read once, Y written once.
+        self.work = 2.0 * (11008 * 4096 + r * 4096 + 11008 + r * 11008)
+        self.kernel = "gemm_bf16_skinny_kernel"
+        self.config = {"workload": self.description, "m": r, "n": 11008, "k": 4096, "seed": 3}
+
+    def cpu_baseline(self) -> dict:
+        from oracle import restate as R
+
+        x = self.cpu["x"][: self.ROWS].float().numpy()
+        w = self.cpu["w"].float().numpy()
+        b = self.cpu["b"].float().numpy()
+        rate, reps = _time_cpu(lambda: R.matmul(x, w, False, True, b, act="silu", out="bf16"), self.work)
+        return {"value": rate / 1e9, "unit": "GB/s", "cores": _blas_threads(), "kind": "port",
+                "sample": f"oracle.restate.matmul on the whole {self.ROWS}-row problem, {reps} reps, {_cpu_model()}"}
+
+
 class RowOp(Workload):
     def __init__(self, device, op: str, dtype_name: str) -> None:
         import torch
@@ -438,6 +467,7 @@ def make(name: str, device) -> Workload:
         "gemm_f32c": lambda: Gemm(device, "f32"),
         "gemm_prepacked": lambda: Gemm(device, prepacked=True),
         "linear": lambda: Linear(device),
+        "linear_decode": lambda: LinearDecode(device),
         "softmax": lambda: RowOp(device, "softmax", "bf16"),
         "softmax_f32": lambda: RowOp(device, "softmax", "f32"),
         "rmsnorm": lambda: RowOp(device, "rmsnorm", "bf16"),

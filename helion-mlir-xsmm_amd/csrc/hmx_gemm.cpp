@@ -44,6 +44,9 @@ struct Plan {
   // kernel path then reads it without register transposes.
   bool transpose_b;
   int64_t bt_bytes;
+  // M <= 32 against B [N, K]: the skinny kernel (tile 32 x 32 x 64, no
+  // split, no workspace).
+  bool skinny;
 };
 
 // Output rows from which a row-major bf16 B is transposed once up front.
@@ -71,10 +74,35 @@ int auto_splits(TileChoice tile, int64_t tiles, int64_t m, int64_t n, int64_t k,
   return splits;
 }
 
+// Skinny products (at most 32 rows of row-major A against B [N, K], batch 1,
+// K in whole 64-element stages) take the skinny kernel unless the caller
+// asks for K splits or names a tile, or the environment sets HMX_GEMM_SKINNY=0 (for
+// comparison). It reads B once with every CU streaming: 32 x 11008 x 4096
+// took 26 us as four splits of 128 x 128 tiles plus the reduction.
+bool skinny_shape(int ab_dtype, int64_t m, int64_t k, int64_t batch, int trans_a, int b_layout,
+                  int splits, int tile_m, int tile_n, int tile_k) {
+  static const bool on = [] {
+    const char* e = getenv("HMX_GEMM_SKINNY");
+    return !(e && e[0] == '0');
+  }();
+  return on && ab_dtype == HMX_DTYPE_BF16 && m >= 1 && m <= 32 && k >= 64 && k % 64 == 0 && batch == 1 &&
+         !trans_a && b_layout == HMX_B_TRANS && splits <= 1 && tile_m <= 0 && tile_n <= 0 && tile_k <= 0;
+}
+
 int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int trans_a,
               int b_layout, int splits, int64_t max_ws, int tile_m, int tile_n, int tile_k,
               Plan& plan) {
   const bool bf16 = ab_dtype == HMX_DTYPE_BF16;
+  plan.skinny = skinny_shape(ab_dtype, m, k, batch, trans_a, b_layout, splits, tile_m, tile_n, tile_k);
+  if (plan.skinny) {
+    plan.tile = TileChoice{32, 32, 64};
+    plan.splits = 1;
+    plan.k_chunk = k;
+    plan.transpose_b = false;
+    plan.bt_bytes = 0;
+    plan.workspace_bytes = 0;
+    return HMX_OK;
+  }
   const TileChoice* table = bf16 ? kBf16Tiles : kF32Tiles;
   const int count = bf16 ? (int)(sizeof(kBf16Tiles) / sizeof(TileChoice))
                          : (int)(sizeof(kF32Tiles) / sizeof(TileChoice));
@@ -332,7 +360,18 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
   const bool guard = !(whole && g.a.vec && g.b.vec && bytes_ok);
   const dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)plan.splits, (unsigned)batch);
   auto s = (hipStream_t)stream;
-  if (ab_dtype == HMX_DTYPE_BF16) {
+  if (plan.skinny) {
+    // The skinny kernel's loads need the aligned, 2^31-bounded operands of
+    // the direct-to-LDS kernels; otherwise the register-staged kernel runs
+    // the same product on one 128 x 128 tile row.
+    if (g.a.vec && g.b.vec && bytes_ok && dma_enabled()) {
+      launch_gemm_bf16_skinny(g, s);
+    } else {
+      g.tiles_m = 1;
+      g.tiles_n = (int)ceil_div(n, 128);
+      launch_gemm_bf16(g, 128, la, lb_run, true, dim3((unsigned)g.tiles_n, 1, 1), s);
+    }
+  } else if (ab_dtype == HMX_DTYPE_BF16) {
     const TileChoice t = plan.tile;
     // The direct-to-LDS kernels: row-major A, 16-byte aligned operands whose
     // spans fit buffer loads, whole 256 x 256 tiles, or ragged M and N with K

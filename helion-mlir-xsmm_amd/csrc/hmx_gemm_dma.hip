@@ -718,6 +718,151 @@ __global__ __launch_bounds__(256, 1) void gemm_f32_dma_kernel(GemmArgs g) {
   epilogue_direct<FM, FN, WM, WN, false, ACT_ID, false>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
 }
 
+// Skinny products: at most 32 rows of row-major A against B [N, K] (a
+// decode-shaped linear layer, batch 1), bound by reading B once. A workgroup
+// owns 32 rows of B (32 columns of C); its NW waves split K into NW ranges
+// of whole 64-element stages and each streams its own range with no
+// workgroup barrier: D stages in flight, D + 1 ring slots of LDS per wave
+// (D = 1 or 2: deeper queues measured slower).
+// A slot holds the B tile [32 n][64 k] (4 KiB) and A rows [8 XL][64 k]: the
+// rows of A the product has (XL = 1, 2 or 4 loads of 8 rows; rows past M
+// repeat row M - 1, fragment rows past 8 XL repeat the first 8 XL), in the
+// same 128-byte swizzled rows as the GEMM tiles (chunk c of row r in slot
+// c ^ swz64(r)), so every load fetches whole 128-byte pieces of 8 rows.
+//
+// Each stage is four v_mfma_f32_32x32x16_bf16 with B's rows as the first
+// operand, giving C transposed: element e of lane l is column
+// n0 + 8 (e / 4) + 4 (l / 32) + e % 4 of C row l % 32. After the loop the
+// waves' accumulators meet in LDS and are summed in wave order (the K ranges
+// in increasing order, so results do not depend on timing); wave w finishes
+// groups e / 4 = w (4 / NW) .. of every lane: bias, scale, shift, the
+// activation, one rounding, four adjacent columns per store.
+template <int NW, int XL, int D>
+__global__ __launch_bounds__(NW * 64) void gemm_bf16_skinny_kernel(GemmArgs g) {
+  static_assert((NW == 2 || NW == 4) && (XL == 1 || XL == 2 || XL == 4), "skinny shape");
+  constexpr int L = 4 + XL;              // loads per stage per wave
+  constexpr int SB = 4096 + 1024 * XL;   // bytes per ring slot
+  constexpr int RING = (D + 1) * SB;     // bytes per wave
+  static_assert(L * D < 64 && NW * RING <= 160 * 1024 && NW * 64 * 64 <= NW * RING, "skinny LDS plan");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NW * RING];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t n0 = (int64_t)blockIdx.x * 32;
+  const int stages = (int)(g.k / 64);
+  const int t0 = wave * stages / NW, count = (wave + 1) * stages / NW - t0;
+
+  const i32x4_t srd_a = make_srd(g.a.p, g.a.bytes);
+  const i32x4_t srd_b = make_srd(g.b.p, g.b.bytes);
+  // Load q of a stage fills 8 rows: lane l slot l % 8 of row 8 q + l / 8,
+  // clamped to the operand's last row. The lane offset holds the row; the
+  // scalar offset (not range-checked) only the stage's K position.
+  const int rr = lane >> 3, slot = lane & 7;
+  int32_t voff_b[4], voff_a[XL];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = 8 * q + rr;
+    voff_b[q] = (int32_t)((min(n0 + r, g.n - 1) * g.b.ld + (slot ^ swz64(r)) * 8) * 2);
+  }
+#pragma unroll
+  for (int q = 0; q < XL; ++q) {
+    const int r = 8 * q + rr;
+    voff_a[q] = (int32_t)((min((int64_t)r, g.m - 1) * g.a.ld + (slot ^ swz64(r)) * 8) * 2);
+  }
+  const uint32_t ring = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + wave * RING;
+  // Workgroup b walks its waves' ranges from stage b mod count on, wrapping
+  // around: the workgroups in flight then read different K positions of
+  // their rows instead of one 128-byte column of B at a time.
+  const int rot = (int)(blockIdx.x % (unsigned)max(count, 1));
+  auto issue = [&](int u) {
+    int uu = u + rot;
+    if (uu >= count) uu -= count;
+    const int32_t kb = (t0 + uu) * 128;
+    const uint32_t st = ring + (uint32_t)((u % (D + 1)) * SB);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) lds_dma16(srd_b, voff_b[q], kb, st + q * 1024);
+#pragma unroll
+    for (int q = 0; q < XL; ++q) lds_dma16(srd_a, voff_a[q], kb, st + 4096 + q * 1024);
+  };
+
+  // Fragment reads of MFMA s: row l % 32, chunk 2 s + l / 32 (K 16 s + 8 (l / 32) ..).
+  const int fr = lane & 31, fh = lane >> 5;
+  const int ar = fr & (8 * XL - 1);
+  const int b_off = fr * 128, a_off = 4096 + ar * 128;
+  const int b_swz = swz64(fr), a_swz = swz64(ar);
+  f32x16_t acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  if (count > 0) {
+#pragma unroll
+    for (int u = 0; u < D; ++u)
+      if (u < count) issue(u);
+    for (int u = 0; u < count; ++u) {
+      if (u + D < count) {
+        issue(u + D);  // into the slot read in step u - 1
+        wait_vmem<L * D>();
+      } else {
+        wait_vmem<0>();
+      }
+      const uint8_t* st = lds + wave * RING + (u % (D + 1)) * SB;
+      bf16x8_t fb[4], fa[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        fb[s] = *(const bf16x8_t*)(st + b_off + (((2 * s + fh) ^ b_swz) << 4));
+        fa[s] = *(const bf16x8_t*)(st + a_off + (((2 * s + fh) ^ a_swz) << 4));
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[s], fa[s], acc, 0, 0, 0);
+    }
+  }
+
+  // Every wave's loads have landed (wait_vmem<0> ends its loop) and its ring
+  // reads have been consumed; the ring becomes the reduction buffer.
+  __syncthreads();
+  float* red = (float*)lds;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) red[(wave * 16 + e) * 64 + lane] = acc[e];
+  __syncthreads();
+  constexpr int GPW = 4 / NW;  // groups of four accumulators finished per wave
+  const int64_t row = fr;
+  if (row >= g.m) return;
+#pragma unroll
+  for (int gi = 0; gi < GPW; ++gi) {
+    const int grp = wave * GPW + gi;
+    const int64_t col0 = n0 + 8 * grp + 4 * fh;
+    float v[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int e = 4 * grp + c;
+      float sum = red[e * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) sum += red[(w * 16 + e) * 64 + lane];
+      float bias, scale, shift;
+      column_vectors(g, col0 + c, col0 + c < g.n, bias, scale, shift);
+      v[c] = apply_activation(g.act, (sum + bias) * scale + shift, g.act_arg);
+    }
+    if (g.c_dtype == HMX_DTYPE_BF16) {
+      uint16_t* p = (uint16_t*)g.c + row * g.ldc + col0;
+      if (col0 + 3 < g.n && (((uintptr_t)p) & 7) == 0) {
+        *(uint2*)p = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (col0 + c < g.n) p[c] = (uint16_t)f32_to_bf16_bits(v[c]);
+      }
+    } else {
+      float* p = (float*)g.c + row * g.ldc + col0;
+      if (col0 + 3 < g.n && (((uintptr_t)p) & 15) == 0) {
+        *(float4*)p = float4{v[0], v[1], v[2], v[3]};
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (col0 + c < g.n) p[c] = v[c];
+      }
+    }
+  }
+}
+
 template <int LB, bool BF16, bool K64, int NW = 4>
 void launch_bf16_dma_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
   if constexpr (K64) {
@@ -899,6 +1044,30 @@ void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {
     if (k64) launch_bf16_dma_b<L_KCONTIG, true>(g, grid, s);
     else launch_bf16_dma_b<L_KCONTIG, false>(g, grid, s);
   }
+}
+
+template <int NW, int D>
+void launch_bf16_skinny(const GemmArgs& g, hipStream_t s) {
+  const dim3 grid((unsigned)ceil_div(g.n, 32));
+  if (g.m <= 8)
+    launch(gemm_bf16_skinny_kernel<NW, 1, D>, grid, NW * 64, s, g);
+  else if (g.m <= 16)
+    launch(gemm_bf16_skinny_kernel<NW, 2, D>, grid, NW * 64, s, g);
+  else
+    launch(gemm_bf16_skinny_kernel<NW, 4, D>, grid, NW * 64, s, g);
+}
+
+// Up to 256 groups of 32 B rows (at most one workgroup per CU): four waves,
+// two stages in flight each; more: two waves, one stage in flight. Measured
+// with graph replay on one box, M x N x K: 8 x 4096 x 4096 7.8 us (one stage
+// in flight: 8.6 us), 32 x 4096 x 11008 20.1 us (20.0 us); two waves with one
+// stage: 32 x 11008 x 4096 16.6 us and 32 x 28672 x 8192 92.7 us (two stages:
+// 19.2 and 102 us; four waves with three: 20.1 and 103 us).
+void launch_gemm_bf16_skinny(const GemmArgs& g, hipStream_t s) {
+  if (ceil_div(g.n, 32) <= 256)
+    launch_bf16_skinny<4, 2>(g, s);
+  else
+    launch_bf16_skinny<2, 1>(g, s);
 }
 
 void launch_gemm_f32_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {

@@ -167,12 +167,15 @@ def _plan(ab: int, m: int, n: int, k: int, batch: int, trans_a: bool, layout: in
 
 
 def gemm_plan(a_dtype: torch.dtype, m: int, n: int, k: int, batch: int = 1,
-              splits: int = 0, block_sizes: Sequence[int] | None = None) -> dict[str, int]:
+              splits: int = 0, block_sizes: Sequence[int] | None = None,
+              trans_b: bool = False) -> dict[str, int]:
     """The launch the gpu GEMM makes for this problem: K splits, workgroup tile
     and workspace bytes (host-only; the GPU tile table that replaces the
-    reference's CPU heuristics, matmul.py:368-446, 1257-1287)."""
+    reference's CPU heuristics, matmul.py:368-446, 1257-1287). ``trans_b``
+    plans for B stored [N, K] (``nn.Linear`` weights); tile (32, 32, 64) is
+    the skinny kernel (at most 32 rows of A against such a B)."""
     s, tm, tn, tk, ws = _plan(native.dtype_code(a_dtype), m, n, k, batch, False,
-                              native.B_ROW, splits, block_sizes)
+                              native.B_TRANS if trans_b else native.B_ROW, splits, block_sizes)
     return {"splits": s, "tile_m": tm, "tile_n": tn, "tile_k": tk, "workspace_bytes": ws}
 
 

@@ -122,10 +122,11 @@ def test_gemm_refuses_bad_arguments(lib: ctypes.CDLL, kw: dict, message: str) ->
 
 
 def _plan(lib: ctypes.CDLL, ab: int, m: int, n: int, k: int, batch: int = 1, splits: int = 0,
-          max_ws: int = -1, tiles: tuple[int, int, int] = (0, 0, 0)) -> tuple[int, int, int, int, int]:
+          max_ws: int = -1, tiles: tuple[int, int, int] = (0, 0, 0),
+          b_layout: int = native.B_ROW) -> tuple[int, int, int, int, int]:
     outs = [ctypes.c_int() for _ in range(4)]
     ws = ctypes.c_int64()
-    assert lib.hmx_gemm_plan(ab, m, n, k, batch, 0, 0, splits, max_ws, *tiles,
+    assert lib.hmx_gemm_plan(ab, m, n, k, batch, 0, b_layout, splits, max_ws, *tiles,
                              *[ctypes.byref(o) for o in outs], ctypes.byref(ws)) == 0
     return (*[o.value for o in outs], ws.value)
 
@@ -153,8 +154,23 @@ def test_plans_of_the_baseline_configs(lib: ctypes.CDLL) -> None:
     assert _plan(lib, bf16, 256, 256, 65536, batch=16)[:4] == (16, 256, 256, 64)
     # Too few K tiles to fill the GPU by splitting: the small tile.
     assert _plan(lib, f32, 256, 256, 4096, batch=16)[1:3] == (128, 128)
-    # A skinny bf16 product (decode-shaped linear): 86 tiles of 128 x 128, split
-    # four ways (one workgroup per CU at most), f32 partials in the workspace.
+    # A skinny bf16 product against B [N, K] (a decode-shaped linear): the
+    # skinny kernel, one workgroup per 32 columns of C, no split or workspace.
+    trans = native.B_TRANS
+    assert _plan(lib, bf16, 32, 11008, 4096, b_layout=trans) == (1, 32, 32, 64, 0)
+    assert _plan(lib, bf16, 1, 4096, 64, b_layout=trans) == (1, 32, 32, 64, 0)
+    # One split (what a prepared call passes back) is no split: still skinny.
+    assert _plan(lib, bf16, 32, 11008, 4096, splits=1, b_layout=trans) == (1, 32, 32, 64, 0)
+    # Not skinny: 33 rows, K not in whole 64-element stages, batches, or a
+    # caller's splits or tile.
+    assert _plan(lib, bf16, 33, 11008, 4096, b_layout=trans)[1] == 128
+    assert _plan(lib, bf16, 32, 11008, 4000, b_layout=trans)[1] == 128
+    assert _plan(lib, bf16, 32, 11008, 4096, batch=2, b_layout=trans)[1] == 128
+    assert _plan(lib, bf16, 32, 11008, 4096, splits=2, b_layout=trans)[:2] == (2, 128)
+    assert _plan(lib, bf16, 32, 11008, 4096, tiles=(128, 128, 64), b_layout=trans)[1] == 128
+    assert _plan(lib, f32, 32, 11008, 4096, b_layout=trans)[1] != 32
+    # The same product with row-major B: 86 tiles of 128 x 128, split four
+    # ways (one workgroup per CU at most), f32 partials in the workspace.
     assert _plan(lib, bf16, 32, 11008, 4096) == (4, 128, 128, 64, 4 * 32 * 11008 * 4)
     # The f32 512^3 plumbing case: 16 tiles of 128 x 128 and too few K tiles to
     # split them, so 64 x 64 tiles (64 workgroups), no split.

@@ -146,6 +146,9 @@ def test_gemm_plan_of_the_baseline_configs() -> None:
     assert U.gemm_plan(torch.bfloat16, 4096, 4096, 4096) == {
         "splits": 1, "tile_m": 256, "tile_n": 256, "tile_k": 64, "workspace_bytes": 0}
     assert U.gemm_plan(torch.float32, 256, 256, 65536, batch=16)["splits"] >= 16
+    # A decode-shaped linear (B [N, K]): the skinny kernel, no split.
+    assert U.gemm_plan(torch.bfloat16, 32, 11008, 4096, trans_b=True) == {
+        "splits": 1, "tile_m": 32, "tile_n": 32, "tile_k": 64, "workspace_bytes": 0}
     assert U.tall_output_tiles(8192, 11008, 4096) == (256, 256, 64)
     assert U.vnni_panel(128, 4096) == 256
 

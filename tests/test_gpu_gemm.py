@@ -214,6 +214,36 @@ def test_matmul_random_shapes(gpu_device, m, n, k, trans_a, trans_b, tiles, act,
     _check(to_np(got), ref, k, to_np(a), to_np(b), "bf16")
 
 
+@pytest.mark.parametrize(("m", "n", "k", "lda"), [
+    (1, 11008, 4096, 0), (32, 11008, 4096, 0), (12, 9000, 512, 0), (31, 17000, 256, 0),  # 2 waves
+    (8, 4096, 4096, 0), (16, 203, 192, 0), (17, 1000, 64, 0), (32, 300, 128, 0), (5, 33, 640, 0),  # 4 waves
+    (32, 4096, 1024, 1088),  # A a strided view
+    (20, 500, 256, 257),  # A rows misaligned: the register-staged kernel
+])
+@pytest.mark.parametrize(("act", "f32_out"), [("identity", False), ("silu", True), ("gelu", False)])
+def test_matmul_skinny(gpu_device, m, n, k, lda, act, f32_out) -> None:
+    # Decode-shaped products (M <= 32, B [N, K]): one workgroup per 32 columns
+    # of C, K split over its waves (ranges empty when K has fewer 64-element
+    # stages than waves), ragged N, 8 / 16 / 32 rows of A loaded, fused bias,
+    # scale, shift and activation; two calls give equal bits.
+    a_full = tensor(RNG.normal(0, 0.3, (m, lda or k)).astype(np.float32), "bf16", gpu_device)
+    a = a_full[:, :k]
+    b = tensor(RNG.normal(0, 0.3, (n, k)).astype(np.float32), "bf16", gpu_device)
+    bias, scale, shift = (tensor(RNG.normal(1, 0.5, n).astype(np.float32), "bf16", gpu_device) for _ in range(3))
+    out_dtype = torch.float32 if f32_out else torch.bfloat16
+
+    def run() -> torch.Tensor:
+        return U.matmul(a, b, trans_b=True, bias=bias, scale=scale, shift=shift, epilogue=ACTS[act],
+                        out_dtype=out_dtype)
+
+    assert U.gemm_plan(torch.bfloat16, m, n, k, trans_b=True)["tile_m"] == 32
+    got = run()
+    assert torch.equal(run(), got)
+    ref = R.matmul(to_np(a), to_np(b), False, True, to_np(bias), to_np(scale), to_np(shift), act,
+                   out="f32" if f32_out else "bf16")
+    _check(to_np(got), ref, k, to_np(a), to_np(b), "bf16")
+
+
 def test_bmm_whole_tiles_split_k_direct_to_lds(gpu_device) -> None:
     a = tensor(RNG.uniform(-1, 1, (1, 4096, 1024)).astype(np.float32), "bf16", gpu_device)
     b = tensor(RNG.uniform(-1, 1, (1, 1024, 4096)).astype(np.float32), "bf16", gpu_device)
