@@ -44,7 +44,7 @@ struct Plan {
   // kernel path then reads it without register transposes.
   bool transpose_b;
   int64_t bt_bytes;
-  // M <= 32 against B [N, K]: the skinny kernel (tile 32 x 32 x 64, no
+  // M <= 64 against B [N, K]: the skinny kernel (tile 32 x 32 x 64, no
   // split, no workspace).
   bool skinny;
 };
@@ -74,7 +74,7 @@ int auto_splits(TileChoice tile, int64_t tiles, int64_t m, int64_t n, int64_t k,
   return splits;
 }
 
-// Skinny products (at most 32 rows of row-major A against B [N, K], batch 1,
+// Skinny products (at most 64 rows of row-major A against B [N, K], batch 1,
 // K in whole 64-element stages) take the skinny kernel unless the caller
 // asks for K splits or names a tile, or the environment sets HMX_GEMM_SKINNY=0 (for
 // comparison). It reads B once with every CU streaming: 32 x 11008 x 4096
@@ -85,7 +85,7 @@ bool skinny_shape(int ab_dtype, int64_t m, int64_t k, int64_t batch, int trans_a
     const char* e = getenv("HMX_GEMM_SKINNY");
     return !(e && e[0] == '0');
   }();
-  return on && ab_dtype == HMX_DTYPE_BF16 && m >= 1 && m <= 32 && k >= 64 && k % 64 == 0 && batch == 1 &&
+  return on && ab_dtype == HMX_DTYPE_BF16 && m >= 1 && m <= 64 && k >= 64 && k % 64 == 0 && batch == 1 &&
          !trans_a && b_layout == HMX_B_TRANS && splits <= 1 && tile_m <= 0 && tile_n <= 0 && tile_k <= 0;
 }
 

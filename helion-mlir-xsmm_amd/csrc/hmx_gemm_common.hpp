@@ -322,7 +322,7 @@ void launch_gemm_bf16_dma_ta(const GemmArgs& g, int lb, dim3 grid, hipStream_t s
 // The 64-wide direct-to-LDS kernel on 128 x 128 tiles (four waves of 64 x 64,
 // B [N, K] or [K, N], K chunks of whole 64-element stages), whole or ragged.
 void launch_gemm_bf16_dma128(const GemmArgs& g, int lb, dim3 grid, hipStream_t s);
-// Skinny products: M <= 32, row-major A, B [N, K], batch 1, K a multiple of
+// Skinny products: M <= 64, row-major A, B [N, K], batch 1, K a multiple of
 // 64, operand spans below 2^31 bytes, 16-byte aligned rows; one workgroup per
 // 32 columns of C, K split over its waves, any epilogue, C bf16 or f32.
 void launch_gemm_bf16_skinny(const GemmArgs& g, hipStream_t s);

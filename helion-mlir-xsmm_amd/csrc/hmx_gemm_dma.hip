@@ -718,37 +718,42 @@ __global__ __launch_bounds__(256, 1) void gemm_f32_dma_kernel(GemmArgs g) {
   epilogue_direct<FM, FN, WM, WN, false, ACT_ID, false>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
 }
 
-// Skinny products: at most 32 rows of row-major A against B [N, K] (a
+// Skinny products: at most 64 rows of row-major A against B [N, K] (a
 // decode-shaped linear layer, batch 1), bound by reading B once. A workgroup
-// owns 32 rows of B (32 columns of C); its NW waves split K into NW ranges
+// owns 32 RB rows of B (32 RB columns of C); its NW waves split K into NW ranges
 // of whole 64-element stages and each streams its own range with no
 // workgroup barrier: D stages in flight, D + 1 ring slots of LDS per wave
 // (D = 1 or 2: deeper queues measured slower).
-// A slot holds the B tile [32 n][64 k] (4 KiB) and A rows [8 XL][64 k]: the
-// rows of A the product has (XL = 1, 2 or 4 loads of 8 rows; rows past M
+// A slot holds the B tile [32 RB n][64 k] (4 RB KiB) and A rows [8 XL][64 k]: the
+// rows of A the product has (XL = 1, 2, 4 or 8 loads of 8 rows; rows past M
 // repeat row M - 1, fragment rows past 8 XL repeat the first 8 XL), in the
 // same 128-byte swizzled rows as the GEMM tiles (chunk c of row r in slot
 // c ^ swz64(r)), so every load fetches whole 128-byte pieces of 8 rows.
 //
-// Each stage is four v_mfma_f32_32x32x16_bf16 with B's rows as the first
-// operand, giving C transposed: element e of lane l is column
-// n0 + 8 (e / 4) + 4 (l / 32) + e % 4 of C row l % 32. After the loop the
-// waves' accumulators meet in LDS and are summed in wave order (the K ranges
-// in increasing order, so results do not depend on timing); wave w finishes
-// groups e / 4 = w (4 / NW) .. of every lane: bias, scale, shift, the
-// activation, one rounding, four adjacent columns per store.
-template <int NW, int XL, int D>
+// Each stage is four v_mfma_f32_32x32x16_bf16 per pair of 32-row blocks of B
+// (rb) and A (mb; two blocks past 32 rows) with B's rows as the first
+// operand, giving C transposed: element e of lane l of tile (rb, mb) is
+// column n0 + 32 rb + 8 (e / 4) + 4 (l / 32) + e % 4 of C row 32 mb + l % 32.
+// After the loop the waves' accumulators meet in LDS and are summed in wave
+// order (so results do not depend on timing); the groups of four elements
+// e / 4 of every tile are dealt to the waves in turn, each finishing its
+// groups (bias, scale, shift, the activation, one rounding) and storing four
+// adjacent columns at a time.
+template <int NW, int XL, int D, int RB>
 __global__ __launch_bounds__(NW * 64) void gemm_bf16_skinny_kernel(GemmArgs g) {
-  static_assert((NW == 2 || NW == 4) && (XL == 1 || XL == 2 || XL == 4), "skinny shape");
-  constexpr int L = 4 + XL;              // loads per stage per wave
-  constexpr int SB = 4096 + 1024 * XL;   // bytes per ring slot
-  constexpr int RING = (D + 1) * SB;     // bytes per wave
-  static_assert(L * D < 64 && NW * RING <= 160 * 1024 && NW * 64 * 64 <= NW * RING, "skinny LDS plan");
+  static_assert((NW == 2 || NW == 4) && (XL == 1 || XL == 2 || XL == 4 || XL == 8) && (RB == 1 || RB == 2),
+                "skinny shape");
+  constexpr int MB = XL == 8 ? 2 : 1;          // 32-row blocks of A (columns of the MFMA)
+  constexpr int BB = 4096 * RB;                // bytes of B per stage: [32 RB n][64 k]
+  constexpr int L = 4 * RB + XL;               // loads per stage per wave
+  constexpr int SB = BB + 1024 * XL;           // bytes per ring slot
+  constexpr int RING = (D + 1) * SB;           // bytes per wave
+  static_assert(L * D < 64 && NW * RING <= 160 * 1024 && RB * MB * 64 * 64 <= RING, "skinny LDS plan");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NW * RING];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t n0 = (int64_t)blockIdx.x * 32;
+  const int64_t n0 = (int64_t)blockIdx.x * (32 * RB);
   const int stages = (int)(g.k / 64);
   const int t0 = wave * stages / NW, count = (wave + 1) * stages / NW - t0;
 
@@ -758,9 +763,9 @@ __global__ __launch_bounds__(NW * 64) void gemm_bf16_skinny_kernel(GemmArgs g) {
   // clamped to the operand's last row. The lane offset holds the row; the
   // scalar offset (not range-checked) only the stage's K position.
   const int rr = lane >> 3, slot = lane & 7;
-  int32_t voff_b[4], voff_a[XL];
+  int32_t voff_b[4 * RB], voff_a[XL];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int q = 0; q < 4 * RB; ++q) {
     const int r = 8 * q + rr;
     voff_b[q] = (int32_t)((min(n0 + r, g.n - 1) * g.b.ld + (slot ^ swz64(r)) * 8) * 2);
   }
@@ -780,19 +785,27 @@ __global__ __launch_bounds__(NW * 64) void gemm_bf16_skinny_kernel(GemmArgs g) {
     const int32_t kb = (t0 + uu) * 128;
     const uint32_t st = ring + (uint32_t)((u % (D + 1)) * SB);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) lds_dma16(srd_b, voff_b[q], kb, st + q * 1024);
+    for (int q = 0; q < 4 * RB; ++q) lds_dma16(srd_b, voff_b[q], kb, st + q * 1024);
 #pragma unroll
-    for (int q = 0; q < XL; ++q) lds_dma16(srd_a, voff_a[q], kb, st + 4096 + q * 1024);
+    for (int q = 0; q < XL; ++q) lds_dma16(srd_a, voff_a[q], kb, st + BB + q * 1024);
   };
 
   // Fragment reads of MFMA s: row l % 32, chunk 2 s + l / 32 (K 16 s + 8 (l / 32) ..).
+  // (Rows 32 rb + l % 32 of B share the swizzle of row l % 32.)
   const int fr = lane & 31, fh = lane >> 5;
-  const int ar = fr & (8 * XL - 1);
-  const int b_off = fr * 128, a_off = 4096 + ar * 128;
-  const int b_swz = swz64(fr), a_swz = swz64(ar);
-  f32x16_t acc;
+  const int b_off = fr * 128, b_swz = swz64(fr);
+  int a_off[MB], a_swz[MB];
+  f32x16_t acc[RB][MB];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  for (int mb = 0; mb < MB; ++mb) {
+    const int ar = MB == 2 ? 32 * mb + fr : fr & (8 * XL - 1);
+    a_off[mb] = BB + ar * 128;
+    a_swz[mb] = swz64(ar);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[rb][mb][e] = 0.f;
+  }
   if (count > 0) {
 #pragma unroll
     for (int u = 0; u < D; ++u)
@@ -805,38 +818,54 @@ __global__ __launch_bounds__(NW * 64) void gemm_bf16_skinny_kernel(GemmArgs g) {
         wait_vmem<0>();
       }
       const uint8_t* st = lds + wave * RING + (u % (D + 1)) * SB;
-      bf16x8_t fb[4], fa[4];
+      bf16x8_t fb[RB][4], fa[MB][4];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        fb[s] = *(const bf16x8_t*)(st + b_off + (((2 * s + fh) ^ b_swz) << 4));
-        fa[s] = *(const bf16x8_t*)(st + a_off + (((2 * s + fh) ^ a_swz) << 4));
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          fb[rb][s] = *(const bf16x8_t*)(st + rb * 4096 + b_off + (((2 * s + fh) ^ b_swz) << 4));
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          fa[mb][s] = *(const bf16x8_t*)(st + a_off[mb] + (((2 * s + fh) ^ a_swz[mb]) << 4));
       }
 #pragma unroll
-      for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[s], fa[s], acc, 0, 0, 0);
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+            acc[rb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[rb][s], fa[mb][s], acc[rb][mb], 0, 0, 0);
     }
   }
 
   // Every wave's loads have landed (wait_vmem<0> ends its loop) and its ring
   // reads have been consumed; the ring becomes the reduction buffer.
   __syncthreads();
+  // Tile t = RB * MB + ... of wave w at red[((w * RB * MB + t) * 16 + e) * 64 + lane].
+  constexpr int TILES = RB * MB;
   float* red = (float*)lds;
 #pragma unroll
-  for (int e = 0; e < 16; ++e) red[(wave * 16 + e) * 64 + lane] = acc[e];
-  __syncthreads();
-  constexpr int GPW = 4 / NW;  // groups of four accumulators finished per wave
-  const int64_t row = fr;
-  if (row >= g.m) return;
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-  for (int gi = 0; gi < GPW; ++gi) {
-    const int grp = wave * GPW + gi;
-    const int64_t col0 = n0 + 8 * grp + 4 * fh;
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) red[((wave * TILES + rb * MB + mb) * 16 + e) * 64 + lane] = acc[rb][mb][e];
+  __syncthreads();
+  // Unit u (< 4 TILES: group u % 4 of tile u / 4) goes to wave u % NW.
+#pragma unroll
+  for (int j = 0; j < 4 * TILES / NW; ++j) {
+    const int u = wave + NW * j, t = u >> 2, grp = u & 3;
+    const int rb = t / MB, mb = t % MB;
+    const int64_t row = 32 * mb + fr;
+    if (row >= g.m) continue;
+    const int64_t col0 = n0 + 32 * rb + 8 * grp + 4 * fh;
     float v[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int e = 4 * grp + c;
-      float sum = red[e * 64 + lane];
+      float sum = red[(t * 16 + e) * 64 + lane];
 #pragma unroll
-      for (int w = 1; w < NW; ++w) sum += red[(w * 16 + e) * 64 + lane];
+      for (int w = 1; w < NW; ++w) sum += red[((w * TILES + t) * 16 + e) * 64 + lane];
       float bias, scale, shift;
       column_vectors(g, col0 + c, col0 + c < g.n, bias, scale, shift);
       v[c] = apply_activation(g.act, (sum + bias) * scale + shift, g.act_arg);
@@ -1046,28 +1075,34 @@ void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {
   }
 }
 
-template <int NW, int D>
+template <int NW, int D, int RB>
 void launch_bf16_skinny(const GemmArgs& g, hipStream_t s) {
-  const dim3 grid((unsigned)ceil_div(g.n, 32));
+  const dim3 grid((unsigned)ceil_div(g.n, 32 * RB));
   if (g.m <= 8)
-    launch(gemm_bf16_skinny_kernel<NW, 1, D>, grid, NW * 64, s, g);
+    launch(gemm_bf16_skinny_kernel<NW, 1, D, RB>, grid, NW * 64, s, g);
   else if (g.m <= 16)
-    launch(gemm_bf16_skinny_kernel<NW, 2, D>, grid, NW * 64, s, g);
+    launch(gemm_bf16_skinny_kernel<NW, 2, D, RB>, grid, NW * 64, s, g);
+  else if (g.m <= 32)
+    launch(gemm_bf16_skinny_kernel<NW, 4, D, RB>, grid, NW * 64, s, g);
   else
-    launch(gemm_bf16_skinny_kernel<NW, 4, D>, grid, NW * 64, s, g);
+    launch(gemm_bf16_skinny_kernel<NW, 8, D, RB>, grid, NW * 64, s, g);
 }
 
-// Up to 256 groups of 32 B rows (at most one workgroup per CU): four waves,
-// two stages in flight each; more: two waves, one stage in flight. Measured
-// with graph replay on one box, M x N x K: 8 x 4096 x 4096 7.8 us (one stage
-// in flight: 8.6 us), 32 x 4096 x 11008 20.1 us (20.0 us); two waves with one
-// stage: 32 x 11008 x 4096 16.6 us and 32 x 28672 x 8192 92.7 us (two stages:
-// 19.2 and 102 us; four waves with three: 20.1 and 103 us).
+// Up to 256 groups of 32 B rows (at most one workgroup per CU): four waves
+// of 32 rows, two stages in flight each; more: four waves of 64 rows (two
+// 32-row blocks share each A fragment, halving A's share of the loads), one
+// stage in flight. Measured with graph replay on one box, M x N x K (torch /
+// hipBLASLt in brackets): 32 x 4096 x 4096 8.6 us (9.6), 64 x 4096 x 4096
+// 12.0 us (11.9); 32 x 11008 x 4096 16.7 us (17.8), 64 x 11008 x 4096 19.9 us
+// (19.4), 32 x 28672 x 8192 85.0 us (131.6), 64 x 28672 x 8192 99.4 us
+// (99.1). Alternatives on the large shapes: two waves of 32 rows with one
+// stage 16.9 / 22.4 / 92.2 / 126.3 us, four waves of 32 rows 18.0 / 24.2 /
+// 95.9 / 119.9 us; two stages in flight or more measured slower there.
 void launch_gemm_bf16_skinny(const GemmArgs& g, hipStream_t s) {
   if (ceil_div(g.n, 32) <= 256)
-    launch_bf16_skinny<4, 2>(g, s);
+    launch_bf16_skinny<4, 2, 1>(g, s);
   else
-    launch_bf16_skinny<2, 1>(g, s);
+    launch_bf16_skinny<4, 1, 2>(g, s);
 }
 
 void launch_gemm_f32_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {

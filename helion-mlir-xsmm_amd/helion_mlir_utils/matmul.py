@@ -173,7 +173,7 @@ def gemm_plan(a_dtype: torch.dtype, m: int, n: int, k: int, batch: int = 1,
     and workspace bytes (host-only; the GPU tile table that replaces the
     reference's CPU heuristics, matmul.py:368-446, 1257-1287). ``trans_b``
     plans for B stored [N, K] (``nn.Linear`` weights); tile (32, 32, 64) is
-    the skinny kernel (at most 32 rows of A against such a B)."""
+    the skinny kernel (at most 64 rows of A against such a B)."""
     s, tm, tn, tk, ws = _plan(native.dtype_code(a_dtype), m, n, k, batch, False,
                               native.B_TRANS if trans_b else native.B_ROW, splits, block_sizes)
     return {"splits": s, "tile_m": tm, "tile_n": tn, "tile_k": tk, "workspace_bytes": ws}

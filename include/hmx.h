@@ -128,7 +128,7 @@ int hmx_time_launches(void* start_event, void* stop_event);
  * second kernel: results do not depend on timing. splits = 0 lets the
  * library choose (see hmx_gemm_plan). tile_m/tile_n/tile_k request a
  * workgroup tile (0 = default): the largest instantiated tile within the
- * request is used. At most 32 rows of row-major bf16 A against B [N, K]
+ * request is used. At most 64 rows of row-major bf16 A against B [N, K]
  * (batch 1, K a multiple of 64; a decode-shaped linear layer) with splits
  * 0 or 1 and no tile requested take a skinny kernel: one workgroup per 32
  * columns of C, K split over its waves and summed in a fixed order, no

@@ -161,9 +161,10 @@ def test_plans_of_the_baseline_configs(lib: ctypes.CDLL) -> None:
     assert _plan(lib, bf16, 1, 4096, 64, b_layout=trans) == (1, 32, 32, 64, 0)
     # One split (what a prepared call passes back) is no split: still skinny.
     assert _plan(lib, bf16, 32, 11008, 4096, splits=1, b_layout=trans) == (1, 32, 32, 64, 0)
-    # Not skinny: 33 rows, K not in whole 64-element stages, batches, or a
+    assert _plan(lib, bf16, 64, 11008, 4096, b_layout=trans) == (1, 32, 32, 64, 0)
+    # Not skinny: 65 rows, K not in whole 64-element stages, batches, or a
     # caller's splits or tile.
-    assert _plan(lib, bf16, 33, 11008, 4096, b_layout=trans)[1] == 128
+    assert _plan(lib, bf16, 65, 11008, 4096, b_layout=trans)[1] == 128
     assert _plan(lib, bf16, 32, 11008, 4000, b_layout=trans)[1] == 128
     assert _plan(lib, bf16, 32, 11008, 4096, batch=2, b_layout=trans)[1] == 128
     assert _plan(lib, bf16, 32, 11008, 4096, splits=2, b_layout=trans)[:2] == (2, 128)

@@ -217,14 +217,15 @@ def test_matmul_random_shapes(gpu_device, m, n, k, trans_a, trans_b, tiles, act,
 @pytest.mark.parametrize(("m", "n", "k", "lda"), [
     (1, 11008, 4096, 0), (32, 11008, 4096, 0), (12, 9000, 512, 0), (31, 17000, 256, 0),  # 2 waves
     (8, 4096, 4096, 0), (16, 203, 192, 0), (17, 1000, 64, 0), (32, 300, 128, 0), (5, 33, 640, 0),  # 4 waves
+    (64, 11008, 4096, 0), (64, 9000, 64, 0), (33, 4096, 1024, 0), (48, 203, 192, 0),  # two 32-row blocks of A
     (32, 4096, 1024, 1088),  # A a strided view
     (20, 500, 256, 257),  # A rows misaligned: the register-staged kernel
 ])
 @pytest.mark.parametrize(("act", "f32_out"), [("identity", False), ("silu", True), ("gelu", False)])
 def test_matmul_skinny(gpu_device, m, n, k, lda, act, f32_out) -> None:
-    # Decode-shaped products (M <= 32, B [N, K]): one workgroup per 32 columns
+    # Decode-shaped products (M <= 64, B [N, K]): one workgroup per 32 columns
     # of C, K split over its waves (ranges empty when K has fewer 64-element
-    # stages than waves), ragged N, 8 / 16 / 32 rows of A loaded, fused bias,
+    # stages than waves), ragged N, 8 / 16 / 32 / 64 rows of A loaded, fused bias,
     # scale, shift and activation; two calls give equal bits.
     a_full = tensor(RNG.normal(0, 0.3, (m, lda or k)).astype(np.float32), "bf16", gpu_device)
     a = a_full[:, :k]
