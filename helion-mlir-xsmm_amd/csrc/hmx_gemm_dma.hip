@@ -561,6 +561,9 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
 // 256 registers, and the compiler sinks the loads to where they are stored;
 // here the loads go straight to LDS, so four waves (one per SIMD, 128 x 128
 // outputs each, 256 accumulators in AGPRs) keep two fragment sets in VGPRs.
+// With NW = 8 the eight waves (two per SIMD) own 128 x 64 outputs each (128
+// accumulators): one wave's MFMAs run while the other of its SIMD waits at
+// the stage barrier or on an LDS read.
 //
 // Stages are 32 K deep (one 128-byte line of each A row), two of 64 KiB:
 // K-contiguous tiles [256 rows][32 k] with 16-byte chunk c of row r in slot
@@ -568,23 +571,30 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
 // chunk c of row k in slot c ^ (8 ((k >> 2) & 1)), so the two half-waves of a
 // fragment read (rows k and k + 4, same columns) meet different banks.
 //
-// A step is K = 8 (four MFMAs of K = 2 for each of the 16 fragment pairs, 64
-// slots); a stage is four steps. Slots 0-7 of each step read the next step's
-// fragments (two register sets alternate). Before step 3 the wave waits for
-// its loads of stage t + 1 and its reads of stage t, and the barrier both
-// publishes t + 1 and frees t; step 3 then reads t + 1's first fragments
-// (slots 0-7) and issues the 16 loads of stage t + 2 into t's buffer (slots
-// 8-23), three steps ahead of their use.
-template <int LB>
-__global__ __launch_bounds__(256, 1) void gemm_f32_dma_kernel(GemmArgs g) {
+// A step is K = 8 (four MFMAs of K = 2 for each of the FM x FN fragment
+// pairs: 64 slots with four waves, 32 with eight); a stage is four steps. The
+// first FM + FN slots of each step read the next step's fragments (two
+// register sets alternate). Before step 3 the wave waits for its loads of
+// stage t + 1 and its reads of stage t, and the barrier both publishes t + 1
+// and frees t; step 3 then reads t + 1's first fragments and issues the
+// wave's 16 (8) loads of stage t + 2 into t's buffer from slot 8 on, three
+// steps ahead of their use.
+template <int LB, int NW = 4>
+__global__ __launch_bounds__(NW * 64, 1) void gemm_f32_dma_kernel(GemmArgs g) {
+  static_assert(NW == 4 || NW == 8, "f32 waves");
   constexpr bool BT = LB == L_RCONTIG;             // B row-major [K, N]
   constexpr int BM = 256, BN = 256, BK = 32;
   constexpr int ROWB = BK * 4;                     // bytes per K-contiguous tile row
   constexpr int NROWB = BN * 4;                    // bytes per row-major B tile row
   constexpr int A_BYTES = BM * ROWB;               // 32 KiB
   constexpr int STAGE = A_BYTES + BN * BK * 4;     // 64 KiB
-  constexpr int FM = 4, FN = 4, WM = 128, WN = 128;
-  constexpr int LOADS = 16;                        // DMA instructions per wave per stage
+  // Four waves of 128 x 128 (2 x 2), or eight of 128 x 64 (2 x 4).
+  constexpr int FM = 4, FN = NW == 8 ? 2 : 4, WM = 128, WN = 32 * FN;
+  constexpr int LOADS = 64 / NW;                   // DMA instructions per wave per stage
+  constexpr int LA = LOADS / 2;                    // of which A
+  constexpr int KCR = 256 / NW;                    // K-contiguous tile rows per wave
+  constexpr int BTR = 32 / NW;                     // row-major B rows per wave
+  constexpr int SLOTS = FM * FN * 4;               // MFMAs per step
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
 
   int tm, tn;
@@ -597,12 +607,12 @@ __global__ __launch_bounds__(256, 1) void gemm_f32_dma_kernel(GemmArgs g) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / (NW / 2), wn = wave % (NW / 2);
 
   const i32x4_t srd_a = make_srd((const float*)g.a.p + batch * g.stride_a, g.a.bytes);
   const i32x4_t srd_b = make_srd((const float*)g.b.p + batch * g.stride_b, g.b.bytes);
-  // K-contiguous operands: wave w loads tile rows 64 w .. 64 w + 63, 8 rows
-  // of 128 bytes per load (lane l: slot l % 8 of row 64 w + 8 q + l / 8,
+  // K-contiguous operands: wave w loads tile rows KCR w .. KCR w + KCR - 1,
+  // 8 rows of 128 bytes per load (lane l: slot l % 8 of row KCR w + 8 q + l / 8,
   // swizzle (l / 16) | 4 (q & 1)). Byte offsets below 2^31: the operands'
   // byte ranges are.
   const int rr = lane >> 3, slot = lane & 7;
@@ -610,34 +620,36 @@ __global__ __launch_bounds__(256, 1) void gemm_f32_dma_kernel(GemmArgs g) {
     return (int32_t)((rr * ld + (slot ^ ((rr >> 1) | (par << 2))) * 4) * 4);
   };
   const int32_t voff_a0 = kc_voff(g.a.ld, 0), voff_a1 = kc_voff(g.a.ld, 1);
-  const int32_t soff_a = (int32_t)((m0 + wave * 64) * g.a.ld * 4);
+  const int32_t soff_a = (int32_t)((m0 + wave * KCR) * g.a.ld * 4);
   const int32_t blk_a = (int32_t)(8 * g.a.ld * 4);
-  // B: K-contiguous as A; row-major: wave w loads K rows 8 w .. 8 w + 7, one
-  // 1 KiB row per load (lane l: slot l), swizzled by bit 2 of the row.
+  // B: K-contiguous as A; row-major: wave w loads K rows BTR w .. BTR w +
+  // BTR - 1, one 1 KiB row per load (lane l: slot l), swizzled by bit 2 of
+  // the row.
   int32_t voff_b0, voff_b1, soff_b, blk_b;
   if constexpr (BT) {
-    voff_b0 = (int32_t)((n0 + lane * 4) * 4);          // loads 0-3: rows 8 w + 0..3
-    voff_b1 = (int32_t)((n0 + (lane ^ 8) * 4) * 4);    // loads 4-7: rows 8 w + 4..7
-    soff_b = (int32_t)(wave * 8 * g.b.ld * 4);
+    voff_b0 = (int32_t)((n0 + lane * 4) * 4);          // rows with bit 2 clear
+    voff_b1 = (int32_t)((n0 + (lane ^ 8) * 4) * 4);    // rows with bit 2 set
+    soff_b = (int32_t)(wave * BTR * g.b.ld * 4);
     blk_b = (int32_t)(g.b.ld * 4);
   } else {
     voff_b0 = kc_voff(g.b.ld, 0);
     voff_b1 = kc_voff(g.b.ld, 1);
-    soff_b = (int32_t)((n0 + wave * 64) * g.b.ld * 4);
+    soff_b = (int32_t)((n0 + wave * KCR) * g.b.ld * 4);
     blk_b = (int32_t)(8 * g.b.ld * 4);
   }
-  const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + wave * 8 * 1024;
+  const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + wave * (32 * 1024 / NW);
 
-  // DMA q (< 16) of stage t: A for q < 8, then B.
+  // DMA q (< LOADS) of stage t: A for q < LA, then B.
   auto dma = [&](int t, int q) {
     const int64_t k0 = k_begin + (int64_t)min(t, ktiles - 1) * BK;
     const uint32_t st = lds_w + (uint32_t)((t & 1) * STAGE);
-    if (q < 8) {
+    if (q < LA) {
       lds_dma16(srd_a, (q & 1) ? voff_a1 : voff_a0, soff_a + q * blk_a + (int32_t)(k0 * 4), st + q * 1024);
     } else {
-      const int qb = q - 8;
+      const int qb = q - LA;
       const int32_t kb = BT ? (int32_t)(k0 * g.b.ld * 4) : (int32_t)(k0 * 4);
-      const int32_t voff = BT ? (qb < 4 ? voff_b0 : voff_b1) : ((qb & 1) ? voff_b1 : voff_b0);
+      const int32_t voff = BT ? ((((BTR * wave + qb) >> 2) & 1) ? voff_b1 : voff_b0)
+                              : ((qb & 1) ? voff_b1 : voff_b0);
       lds_dma16(srd_b, voff, soff_b + qb * blk_b + kb, st + A_BYTES + qb * 1024);
     }
   };
@@ -698,17 +710,17 @@ __global__ __launch_bounds__(256, 1) void gemm_f32_dma_kernel(GemmArgs g) {
       const int set = step & 1;
       if (step == 3) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
-      for (int x = 0; x < 64; ++x) {
+      for (int x = 0; x < SLOTS; ++x) {
         __builtin_amdgcn_sched_barrier(0);
-        if (x < 8) {
+        if (x < FM + FN) {
           // The next step's fragments: this stage's, or t + 1's first.
           const int stg = step < 3 ? cur : nxt, k8 = step < 3 ? 8 * (step + 1) : 0;
-          if (x < 4) fa[set ^ 1][x] = a_read(stg, k8, x);
-          else fb[set ^ 1][x - 4] = b_read(stg, k8, x - 4);
-        } else if (step == 3 && x < 8 + LOADS) {
+          if (x < FM) fa[set ^ 1][x] = a_read(stg, k8, x);
+          else fb[set ^ 1][x - FM] = b_read(stg, k8, x - FM);
+        } else if (step == 3 && x >= 8 && x < 8 + LOADS) {
           dma(t + 2, x - 8);
         }
-        const int s = x >> 4, idx = x & 15, i = idx >> 2, j = idx & 3;
+        const int s = x / (FM * FN), idx = x % (FM * FN), i = idx / FN, j = idx % FN;
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[set][i][s], fb[set][j][s], acc[i][j], 0, 0, 0);
       }
     }
@@ -1106,6 +1118,19 @@ void launch_gemm_bf16_skinny(const GemmArgs& g, hipStream_t s) {
 }
 
 void launch_gemm_f32_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {
+  // Eight waves (two per SIMD) unless the environment sets HMX_F32_WAVES=4:
+  // config 5 (bmm [16, 256, 65536] x [16, 65536, 256]) 0.987 -> 0.970 ms.
+  static const int waves = [] {
+    const char* e = getenv("HMX_F32_WAVES");
+    return e && e[0] == '4' ? 4 : 8;
+  }();
+  if (waves == 8) {
+    if (lb == L_RCONTIG)
+      launch(gemm_f32_dma_kernel<L_RCONTIG, 8>, grid, 512, s, g);
+    else
+      launch(gemm_f32_dma_kernel<L_KCONTIG, 8>, grid, 512, s, g);
+    return;
+  }
   if (lb == L_RCONTIG)
     launch(gemm_f32_dma_kernel<L_RCONTIG>, grid, 256, s, g);
   else
