@@ -340,6 +340,18 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
   g.act = epilogue;
   g.act_arg = epilogue_arg;
   if (plan.splits > 1) {
+    // Split-K grids of one tile per batch slice share no operand data between
+    // workgroups: each walks its K chunk from a stage of its own, so the
+    // workgroups in flight read different K positions of their rows (bf16 bmm
+    // [16, 256, 65536] x [16, 65536, 256]: 238 -> 208 us; the f32 one, MFMA-
+    // bound, unchanged). Grids of several tiles keep the common walk, whose
+    // shared A and B panels meet in L2. HMX_GEMM_STAGGER=0 turns it off (for
+    // comparison).
+    static const bool stagger = [] {
+      const char* e = getenv("HMX_GEMM_STAGGER");
+      return !(e && e[0] == '0');
+    }();
+    g.k_stagger = stagger && tiles_m * tiles_n == 1;
     g.c = partials;
     g.c_dtype = HMX_DTYPE_F32;
     g.ldc = n;

@@ -92,6 +92,9 @@ struct GemmArgs {
   int act;
   float act_arg;
   int tiles_m, tiles_n;
+  // Nonzero: each workgroup walks its K chunk from a stage of its own
+  // (wrapping), for split-K grids whose workgroups share no operand data.
+  int k_stagger;
 };
 
 // blockIdx.x -> (tile_m, tile_n). Consecutive workgroups are dealt to the 8

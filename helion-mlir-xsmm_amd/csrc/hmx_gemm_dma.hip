@@ -413,9 +413,13 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
   const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + wave * LA * 1024;
   const uint32_t lds_wb = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + A_BYTES + wave * LBN * 1024;
 
+  // Stage t of the walk is K stage (t + rot) mod ktiles of the chunk.
+  const int rot = g.k_stagger ? (int)((blockIdx.z * gridDim.y + blockIdx.y) % (unsigned)ktiles) : 0;
   // DMA q (< LOADS) of stage t: A for q < LA, then B.
   auto dma = [&](int t, int q) {
-    const int64_t k0 = k_begin + (int64_t)min(t, ktiles - 1) * BK;
+    int tr = min(t, ktiles - 1) + rot;
+    if (tr >= ktiles) tr -= ktiles;
+    const int64_t k0 = k_begin + (int64_t)tr * BK;
     const uint32_t st = lds_w + (uint32_t)((t & 1) * STAGE);
     const uint32_t sb = lds_wb + (uint32_t)((t & 1) * STAGE);
     if (q < LA) {
@@ -639,9 +643,13 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_f32_dma_kernel(GemmArgs g) {
   }
   const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + wave * (32 * 1024 / NW);
 
+  // Stage t of the walk is K stage (t + rot) mod ktiles of the chunk.
+  const int rot = g.k_stagger ? (int)((blockIdx.z * gridDim.y + blockIdx.y) % (unsigned)ktiles) : 0;
   // DMA q (< LOADS) of stage t: A for q < LA, then B.
   auto dma = [&](int t, int q) {
-    const int64_t k0 = k_begin + (int64_t)min(t, ktiles - 1) * BK;
+    int tr = min(t, ktiles - 1) + rot;
+    if (tr >= ktiles) tr -= ktiles;
+    const int64_t k0 = k_begin + (int64_t)tr * BK;
     const uint32_t st = lds_w + (uint32_t)((t & 1) * STAGE);
     if (q < LA) {
       lds_dma16(srd_a, (q & 1) ? voff_a1 : voff_a0, soff_a + q * blk_a + (int32_t)(k0 * 4), st + q * 1024);
