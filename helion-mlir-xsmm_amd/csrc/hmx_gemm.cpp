@@ -345,8 +345,9 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
     // workgroups in flight read different K positions of their rows (bf16 bmm
     // [16, 256, 65536] x [16, 65536, 256]: 238 -> 208 us; the f32 one, MFMA-
     // bound, unchanged). Grids of several tiles keep the common walk, whose
-    // shared A and B panels meet in L2. HMX_GEMM_STAGGER=0 turns it off (for
-    // comparison).
+    // shared A and B panels meet in L2 (a single tile row, whose workgroups
+    // share only A, measured the same either way). HMX_GEMM_STAGGER=0 turns
+    // it off (for comparison).
     static const bool stagger = [] {
       const char* e = getenv("HMX_GEMM_STAGGER");
       return !(e && e[0] == '0');

@@ -414,7 +414,8 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
   const uint32_t lds_wb = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + A_BYTES + wave * LBN * 1024;
 
   // Stage t of the walk is K stage (t + rot) mod ktiles of the chunk.
-  const int rot = g.k_stagger ? (int)((blockIdx.z * gridDim.y + blockIdx.y) % (unsigned)ktiles) : 0;
+  const int rot =
+      g.k_stagger ? (int)(((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) % (unsigned)ktiles) : 0;
   // DMA q (< LOADS) of stage t: A for q < LA, then B.
   auto dma = [&](int t, int q) {
     int tr = min(t, ktiles - 1) + rot;
@@ -644,7 +645,8 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_f32_dma_kernel(GemmArgs g) {
   const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + wave * (32 * 1024 / NW);
 
   // Stage t of the walk is K stage (t + rot) mod ktiles of the chunk.
-  const int rot = g.k_stagger ? (int)((blockIdx.z * gridDim.y + blockIdx.y) % (unsigned)ktiles) : 0;
+  const int rot =
+      g.k_stagger ? (int)(((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) % (unsigned)ktiles) : 0;
   // DMA q (< LOADS) of stage t: A for q < LA, then B.
   auto dma = [&](int t, int q) {
     int tr = min(t, ktiles - 1) + rot;
