@@ -417,7 +417,7 @@ class MatmulF32(Workload):
         self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_F32_TFLOPS
         self.work = 2.0 * 512**3
         self.dtype = "f32"
-        self.kernel = "gemm_f32_kernel"
+        self.kernel = "gemm_f32_kernel + splitk_reduce_kernel"
         self.config = {"workload": self.description, "m": 512, "n": 512, "k": 512, "seed": 0,
                        "block_sizes": [64, 64, 64]}
 

@@ -49,6 +49,22 @@ struct Plan {
   bool skinny;
 };
 
+// f32 products whose tiles fill at most a quarter of the CUs are bound by
+// latency, not operand traffic: split K until the grid holds one workgroup
+// per CU, each chunk keeping at least 4 K tiles, at most 16 splits (the
+// partials are a few MiB at most), or as auto_splits says if that is more. HIP-graph replay on one box, 64 x 64
+// tiles: 512^3 15.8 -> 12.3 us (4 splits, 1 before), 384 x 384 x 2048
+// 53 -> 22 us (4, 1), 256 x 256 x 1024 27.6 -> 13.3 us (8, 1), 256 x 256 x
+// 4096 32 -> 21 us (16, 4); 64 splits of 128 x 128 x 8192 took 37 us
+// against 26 us for 16 (the reduction sums each output's partials in order).
+int small_f32_splits(int64_t tiles, int64_t kt, int64_t outputs, int64_t max_ws) {
+  int splits = 1;
+  while (splits < 16 && tiles * splits * 2 <= kCus && kt / (splits * 2) >= 4 &&
+         (max_ws < 0 || (int64_t)splits * 2 * outputs * 4 <= max_ws))
+    splits *= 2;
+  return splits;
+}
+
 // Output rows from which a row-major bf16 B is transposed once up front.
 constexpr int64_t kTransposeMinRows = 512;
 
@@ -146,7 +162,11 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
   plan.tile = pick == -2 ? kF32Big : table[pick];
   const int64_t tiles = ceil_div(m, plan.tile.bm) * ceil_div(n, plan.tile.bn) * batch;
   const int64_t kt = ceil_div(k, plan.tile.bk);
-  if (splits == 0) splits = auto_splits(plan.tile, tiles, m, n, k, batch, bf16 ? 2 : 4, max_ws);
+  if (splits == 0) {
+    splits = auto_splits(plan.tile, tiles, m, n, k, batch, bf16 ? 2 : 4, max_ws);
+    if (!bf16 && plan.tile.bm < 256 && tiles * 4 <= kCus)
+      splits = std::max(splits, small_f32_splits(tiles, kt, batch * m * n, max_ws));
+  }
   if (splits < 1) splits = 1;
   if (splits > 1) {
     // Whole K tiles per chunk; no empty chunks.

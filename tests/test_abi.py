@@ -174,8 +174,15 @@ def test_plans_of_the_baseline_configs(lib: ctypes.CDLL) -> None:
     # ways (one workgroup per CU at most), f32 partials in the workspace.
     assert _plan(lib, bf16, 32, 11008, 4096) == (4, 128, 128, 64, 4 * 32 * 11008 * 4)
     # The f32 512^3 plumbing case: 16 tiles of 128 x 128 and too few K tiles to
-    # split them, so 64 x 64 tiles (64 workgroups), no split.
-    assert _plan(lib, f32, 512, 512, 512)[:3] == (1, 64, 64)
+    # split them, so 64 x 64 tiles (64 workgroups), split four ways (one
+    # workgroup per CU, four K tiles each).
+    assert _plan(lib, f32, 512, 512, 512)[:3] == (4, 64, 64)
+    # Small f32 products split at most 16 ways, each chunk at least 4 K tiles.
+    assert _plan(lib, f32, 128, 128, 8192)[:3] == (16, 64, 64)
+    assert _plan(lib, f32, 512, 512, 128)[:3] == (1, 64, 64)
+    assert _plan(lib, f32, 256, 256, 1024)[:3] == (8, 64, 64)
+    # Long K on one tile keeps the traffic rule's larger split.
+    assert _plan(lib, f32, 64, 64, 65536)[:3] == (256, 128, 128)
     # Split-K fills the CUs with 128 x 128 tiles: they stay.
     assert _plan(lib, f32, 256, 256, 4096, batch=16)[:3] == (4, 128, 128)
     # A request below every f32 tile gets the smallest.
