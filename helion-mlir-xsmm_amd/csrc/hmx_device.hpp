@@ -104,14 +104,13 @@ __device__ __forceinline__ float wave_max(float v) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// exp through the hardware base-2 exponential.
-__device__ __forceinline__ float fast_exp(float x) {
-  return __builtin_amdgcn_exp2f(x * kLog2e);
-}
-
-// exp(x - m) given ml = m * log2(e): one FMA and one v_exp_f32.
-__device__ __forceinline__ float exp_shifted(float x, float ml) {
-  return __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2e, -ml));
+// exp(x - m): the difference first, as exp(x - row_max) is written, then one
+// v_exp_f32 of its base-2 scaling. Folding m into an FMA, exp2(x * log2e -
+// m * log2e), would carry the rounding error of m * log2e (half an ulp of
+// |m| * 1.44, over 128 once |m| passes ~3e9) into every exponent of the row:
+// finite rows such as [1e10, 0] would overflow to inf / NaN.
+__device__ __forceinline__ float exp_sub(float x, float m) {
+  return __builtin_amdgcn_exp2f((x - m) * kLog2e);
 }
 
 // The activations a fused epilogue may apply to an f32 value, codes as in

@@ -221,11 +221,10 @@ __global__ __launch_bounds__(kMaxBlock) void softmax_cached(const T* x, T* y, in
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) mx = fmaxf(mx, v[i]);
   mx = row_max_all(mx, red_max, tpr);
-  const float ml = mx * kLog2e;
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL * EPV; ++i) {
-    v[i] = exp_shifted(v[i], ml);
+    v[i] = exp_sub(v[i], mx);
     if (WHOLE || col_of<EPV>(i / EPV, p.li, p.tpr, i % EPV) < n) sum += v[i];
   }
   sum = row_sum_all(sum, red_sum, tpr);
@@ -253,19 +252,18 @@ __global__ __launch_bounds__(kBlock) void softmax_stream(const T* x,
     for (int e = 0; e < EPV; ++e) mx = fmaxf(mx, v[e]);
   }
   mx = wave_max(mx);
-  const float ml = mx * kLog2e;
   float sum = 0.f;
   for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
     load_chunk<T, EPV>(xr, n, col, v, -INFINITY);
 #pragma unroll
     for (int e = 0; e < EPV; ++e)
-      if (col + e < n) sum += exp_shifted(v[e], ml);
+      if (col + e < n) sum += exp_sub(v[e], mx);
   }
   const float inv = 1.f / wave_sum(sum);
   for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
     load_chunk<T, EPV>(xr, n, col, v, 0.f);
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) v[e] = exp_shifted(v[e], ml) * inv;
+    for (int e = 0; e < EPV; ++e) v[e] = exp_sub(v[e], mx) * inv;
     store_chunk<T, EPV>(yr, n, col, v);
   }
 }

@@ -114,12 +114,13 @@ def matmul(
     1332-1368 (f32 fused) and 156-228, 862-904 (blocked, bias, affine)."""
     acc = _op(a, trans_a) @ _op(b, trans_b)  # f32 x f32 -> f32 accumulation
     acc = acc.astype(F32)
-    if bias is not None:
-        acc = acc + np.asarray(bias, dtype=F32)
-    if scale is not None:
-        acc = acc * np.asarray(scale, dtype=F32)
-    if shift is not None:
-        acc = acc + np.asarray(shift, dtype=F32)
+    with np.errstate(over="ignore", invalid="ignore"):  # IEEE overflow / NaN are results here
+        if bias is not None:
+            acc = acc + np.asarray(bias, dtype=F32)
+        if scale is not None:
+            acc = acc * np.asarray(scale, dtype=F32)
+        if shift is not None:
+            acc = acc + np.asarray(shift, dtype=F32)
     return round_to(activation(act, acc, act_arg), out)
 
 
@@ -322,4 +323,5 @@ def leaky_relu(x: np.ndarray, slope: float = 0.01, out: str = "f32") -> np.ndarr
 
 def scalar_mul(x: np.ndarray, s: float, out: str = "f32") -> np.ndarray:
     """elementwise.py:34-39."""
-    return round_to(np.asarray(x, dtype=F32) * F32(s), out)
+    with np.errstate(over="ignore", invalid="ignore"):
+        return round_to(np.asarray(x, dtype=F32) * F32(s), out)

@@ -55,3 +55,69 @@ def bf16_gemm_atol(k: int, a: np.ndarray, b: np.ndarray) -> float:
     ra = float(np.sqrt(np.mean(np.square(a, dtype=np.float64)))) if a.size else 1.0
     rb = float(np.sqrt(np.mean(np.square(b, dtype=np.float64)))) if b.size else 1.0
     return float(np.sqrt(max(k, 1)) * 2.0**-8 * ra * rb * 0.01) + 1e-6
+
+
+# ---------------------------------------------------------------------------
+# Adversarial inputs: the values where an op's answer changes (signed zeros,
+# infinities, NaN, the smallest normal and the largest finite value of the
+# dtype, and the dtype's neighbours of given constants), laid out so that
+# neighbouring rows, neighbouring columns and columns 16 or 64 apart hold
+# different values: a kernel that reads the wrong row or lane cannot pass.
+# The reference's tests use values of this kind (tests/inputs.py:22-76).
+
+
+def special_values(dtype: str, constants: tuple[float, ...] = (), finite: bool = False,
+                   largest: bool = True) -> list[float]:
+    """±0, ±inf, NaN, ±tiny, ±max of ``dtype`` ('f32'/'bf16') and, for each
+    constant, its value in ``dtype`` and the two neighbouring values, both
+    signs; ``finite`` drops inf and NaN, ``largest=False`` drops ±max (for
+    sums, whose overflow would depend on the order of the terms)."""
+    tdt = DTYPES[dtype]
+    info = torch.finfo(tdt)
+    values = [0.0, -0.0, float(info.tiny), -float(info.tiny)]
+    if largest:
+        values += [float(info.max), -float(info.max)]
+    if not finite:
+        values += [float("inf"), float("-inf"), float("nan")]
+    for c in constants:
+        at = torch.tensor(c, dtype=torch.float64).to(tdt)
+        for v in (at, torch.nextafter(at, torch.tensor(float("-inf"), dtype=tdt)),
+                  torch.nextafter(at, torch.tensor(float("inf"), dtype=tdt))):
+            values += [float(v), -float(v)]
+    out, seen = [], set()
+    for v in values:
+        key = np.float64(v).tobytes()
+        if key not in seen:
+            seen.add(key)
+            out.append(v)
+    return out
+
+
+def spread(values: list[float], rows: int, cols: int, extra: float = 3.0) -> np.ndarray:
+    """``values`` over [rows, cols] as float32: element (r, c) is value
+    (r + c) mod count. The count is made odd (one more value, ``extra``), so
+    it divides neither 16 nor 64: columns 16 or 64 apart, and neighbouring
+    rows and columns, differ."""
+    vals = list(values)
+    if len(vals) % 2 == 0:
+        vals.append(extra)
+    idx = (np.arange(rows)[:, None] + np.arange(cols)[None, :]) % len(vals)
+    return np.asarray(vals, dtype=np.float64)[idx].astype(np.float32)
+
+
+def assert_specials_close(got: np.ndarray, ref: np.ndarray, rtol: float, atol: "float | np.ndarray") -> None:
+    """The same NaNs and the same infinities (by sign) as ``ref``; every
+    finite element within ``atol + rtol * |ref|`` (``atol`` a scalar or an
+    array broadcast to ``ref``'s shape)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    atol = np.broadcast_to(np.asarray(atol, np.float64), ref.shape)
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    for what, fn in (("NaN", np.isnan), ("+inf", np.isposinf), ("-inf", np.isneginf)):
+        bad = fn(got) != fn(ref)
+        if bad.any():
+            at = np.argwhere(bad)[:5]
+            detail = [(tuple(i), got[tuple(i)], ref[tuple(i)]) for i in at]
+            raise AssertionError(f"{int(bad.sum())} {what} elements differ: {detail}")
+    fin = np.isfinite(ref)
+    assert_close(got[fin], ref[fin], rtol, atol[fin])

@@ -106,6 +106,30 @@ def test_softmax_one_column_and_nonfinite_rows(dtype: str) -> None:
     np.testing.assert_allclose(got[3], [0.5, 0.0, 0.5])
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_softmax_large_finite_rows_match_torch(dtype: str) -> None:
+    # exp(x - row_max) (normalization.py:61-72) stays finite however large the
+    # row's values: a formulation that folds the maximum into the exponent's
+    # scaling (exp2(x * log2e - max * log2e)) carries max * log2e's rounding
+    # error into every exponent and fails these rows.
+    x = R.round_to(np.array([[1e10, 0.0], [-1e10, -1e10 + 2048.0], [3e38, -3e38], [5e9, 5e9],
+                             [-5e9, 1e-30]], np.float32), dtype)
+    got = R.softmax(x, dtype)
+    np.testing.assert_array_equal(got, torch.softmax(_f64(x), -1).numpy().astype(np.float32))
+    col = R.round_to(np.array([[5e9], [3e38], [-3e38], [1e-30]], np.float32), dtype)
+    np.testing.assert_array_equal(R.softmax(col, dtype), np.ones_like(col))
+    # The folded formulation with one FMA, exp2(fma(x, log2e, -RN(max *
+    # log2e))), modelled in float64 (exact product, one rounding), is wrong on
+    # the first row: the oracle would catch a kernel that used it.
+    log2e = np.float32(1.4426950408889634)
+    ml = np.float32(x[0].max() * log2e)
+    t = (x[0].astype(np.float64) * np.float64(log2e) - np.float64(ml)).astype(np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        e = np.exp2(t)
+        folded = e / e.sum(dtype=np.float32)
+    assert not np.array_equal(folded, [1.0, 0.0])
+
+
 # ---------------------------------------------------------------------------
 # RMSNorm / GroupNorm / LayerNorm
 
