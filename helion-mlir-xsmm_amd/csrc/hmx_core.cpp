@@ -2,6 +2,7 @@
 // per-thread timing events of hmx_time_launches.
 #include <string.h>
 
+#include <atomic>
 #include <string>
 
 #include "hmx_internal.hpp"
@@ -11,9 +12,37 @@ namespace hmx {
 namespace {
 thread_local char g_error[1024] = {0};
 thread_local LaunchEvents g_events = {nullptr, nullptr};
+
+// Device shapes read so far, by device index: (cus << 16) | xcds, 0 = not yet
+// read. Written once per device with the same value from any thread.
+constexpr int kMaxDevices = 64;
+std::atomic<uint32_t> g_shapes[kMaxDevices];
+
+DeviceShape query_shape(int device) {
+  int cus = 0, xcds = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
+    return kMi355x;
+  if (hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, device) != hipSuccess || xcds <= 0)
+    xcds = 1;
+  return DeviceShape{cus, xcds};
 }
+}  // namespace
 
 LaunchEvents& launch_events() { return g_events; }
+
+DeviceShape current_device_shape() {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) {
+    (void)hipGetLastError();  // no device: not an error of the caller's next call
+    return kMi355x;
+  }
+  if (device < 0 || device >= kMaxDevices) return query_shape(device);
+  const uint32_t known = g_shapes[device].load(std::memory_order_relaxed);
+  if (known != 0) return DeviceShape{(int)(known >> 16), (int)(known & 0xffff)};
+  const DeviceShape d = query_shape(device);
+  g_shapes[device].store(((uint32_t)d.cus << 16) | (uint32_t)(d.xcds & 0xffff), std::memory_order_relaxed);
+  return d;
+}
 
 int set_error(int status, const char* fmt, ...) {
   va_list args;

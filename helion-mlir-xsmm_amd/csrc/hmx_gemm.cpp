@@ -20,7 +20,8 @@ constexpr TileChoice kF32Tiles[] = {{128, 128, 32}, {64, 64, 32}};
 // The f32 tile long-K split-K products of whole 256 x 256 tiles take (see
 // make_plan): one workgroup per CU reading each operand once.
 constexpr TileChoice kF32Big = {256, 256, 32};
-constexpr int kCus = 256;  // MI355X compute units
+// The skinny kernel's plan (see skinny_shape).
+constexpr TileChoice kSkinny = {32, 32, 64};
 
 int layout_code(int b_layout) {
   switch (b_layout) {
@@ -57,9 +58,9 @@ struct Plan {
 // 53 -> 22 us (4, 1), 256 x 256 x 1024 27.6 -> 13.3 us (8, 1), 256 x 256 x
 // 4096 32 -> 21 us (16, 4); 64 splits of 128 x 128 x 8192 took 37 us
 // against 26 us for 16 (the reduction sums each output's partials in order).
-int small_f32_splits(int64_t tiles, int64_t kt, int64_t outputs, int64_t max_ws) {
+int small_f32_splits(int64_t tiles, int64_t kt, int64_t outputs, int64_t max_ws, int cus) {
   int splits = 1;
-  while (splits < 16 && tiles * splits * 2 <= kCus && kt / (splits * 2) >= 4 &&
+  while (splits < 16 && tiles * splits * 2 <= cus && kt / (splits * 2) >= 4 &&
          (max_ws < 0 || (int64_t)splits * 2 * outputs * 4 <= max_ws))
     splits *= 2;
   return splits;
@@ -75,10 +76,10 @@ constexpr int64_t kTransposeMinRows = 512;
 // tiles count one per CU: on a skinny 32 x 11008 x 4096 product four splits
 // (344 workgroups) measure 26 us, eight 36 us.
 int auto_splits(TileChoice tile, int64_t tiles, int64_t m, int64_t n, int64_t k, int64_t batch,
-                int64_t esz, int64_t max_ws) {
+                int64_t esz, int64_t max_ws, int cus) {
   const int64_t kt = ceil_div(k, tile.bk);
   const int64_t operand_bytes = batch * (m + n) * k * esz;
-  const int64_t resident = (tile.bm == 256 || esz == 2 ? 1 : 4) * kCus;
+  const int64_t resident = (tile.bm == 256 || esz == 2 ? 1 : 4) * (int64_t)cus;
   int splits = 1;
   for (;;) {
     const int s2 = splits * 2;
@@ -92,26 +93,34 @@ int auto_splits(TileChoice tile, int64_t tiles, int64_t m, int64_t n, int64_t k,
 
 // Skinny products (at most 64 rows of row-major A against B [N, K], batch 1,
 // K in whole 64-element stages) take the skinny kernel unless the caller
-// asks for K splits or names a tile, or the environment sets HMX_GEMM_SKINNY=0 (for
-// comparison). It reads B once with every CU streaming: 32 x 11008 x 4096
-// took 26 us as four splits of 128 x 128 tiles plus the reduction.
+// asks for K splits or names another tile, or the environment sets
+// HMX_GEMM_SKINNY=0 (for comparison). It reads B once with every CU
+// streaming: 32 x 11008 x 4096 took 26 us as four splits of 128 x 128 tiles
+// plus the reduction.
 bool skinny_shape(int ab_dtype, int64_t m, int64_t k, int64_t batch, int trans_a, int b_layout,
                   int splits, int tile_m, int tile_n, int tile_k) {
   static const bool on = [] {
     const char* e = getenv("HMX_GEMM_SKINNY");
     return !(e && e[0] == '0');
   }();
+  const bool no_tile = tile_m <= 0 && tile_n <= 0 && tile_k <= 0;
+  const bool skinny_tile = tile_m == kSkinny.bm && tile_n == kSkinny.bn && tile_k == kSkinny.bk;
   return on && ab_dtype == HMX_DTYPE_BF16 && m >= 1 && m <= 64 && k >= 64 && k % 64 == 0 && batch == 1 &&
-         !trans_a && b_layout == HMX_B_TRANS && splits <= 1 && tile_m <= 0 && tile_n <= 0 && tile_k <= 0;
+         !trans_a && b_layout == HMX_B_TRANS && splits <= 1 && (no_tile || skinny_tile);
 }
 
+// A plan is a pure function of the problem, the request (splits, tile) and
+// the device's CU count. Passing a plan's own splits, tile and workspace
+// back reproduces it exactly: a tile request that names an instantiated tile
+// (or the skinny kernel's, or with two or more splits the f32 split-K tile)
+// takes that tile, and the split count is rounded the same way both times.
 int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int trans_a,
               int b_layout, int splits, int64_t max_ws, int tile_m, int tile_n, int tile_k,
-              Plan& plan) {
+              int cus, Plan& plan) {
   const bool bf16 = ab_dtype == HMX_DTYPE_BF16;
   plan.skinny = skinny_shape(ab_dtype, m, k, batch, trans_a, b_layout, splits, tile_m, tile_n, tile_k);
   if (plan.skinny) {
-    plan.tile = TileChoice{32, 32, 64};
+    plan.tile = kSkinny;
     plan.splits = 1;
     plan.k_chunk = k;
     plan.transpose_b = false;
@@ -125,7 +134,13 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
   // Packed B layouts are instantiated for the first tile only.
   const bool packed = b_layout != HMX_B_ROW && b_layout != HMX_B_TRANS;
   int pick = -1;
-  if (tile_m > 0 || tile_n > 0 || tile_k > 0) {
+  // Whole 256 x 256 tiles of row-major A and an unpacked B: what the big f32
+  // split-K tile serves.
+  const bool big_shape = !packed && !trans_a && m % 256 == 0 && n % 256 == 0 && m > 0 && n > 0;
+  if (!bf16 && splits >= 2 && tile_m == kF32Big.bm && tile_n == kF32Big.bn && tile_k == kF32Big.bk &&
+      big_shape && k % kF32Big.bk == 0) {
+    pick = -2;
+  } else if (tile_m > 0 || tile_n > 0 || tile_k > 0) {
     for (int i = 0; i < count && pick < 0; ++i) {
       if ((tile_m <= 0 || table[i].bm <= tile_m) && (tile_n <= 0 || table[i].bn <= tile_n) &&
           (tile_k <= 0 || table[i].bk <= tile_k))
@@ -137,25 +152,24 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
     pick = count - 1;
     for (int i = 0; i < count; ++i) {
       const int64_t tiles = ceil_div(m, table[i].bm) * ceil_div(n, table[i].bn) * batch;
-      if (tiles >= kCus) { pick = i; break; }
+      if (tiles >= cus) { pick = i; break; }
     }
     // f32: 128 x 128 tiles also when split-K fills the CUs with them (half the
     // operand traffic of 64 x 64 tiles); 64 x 64 tiles for products too small
     // for either (512^3: 16 workgroups of 128 x 128, too few K tiles to split).
     if (!bf16 && pick > 0) {
       const int64_t t128 = ceil_div(m, 128) * ceil_div(n, 128) * batch;
-      if (t128 * auto_splits(table[0], t128, m, n, k, batch, 4, max_ws) >= kCus) pick = 0;
+      if (t128 * auto_splits(table[0], t128, m, n, k, batch, 4, max_ws, cus) >= cus) pick = 0;
     }
     // Long-K bf16 products of whole 256 x 256 tiles that split-K can spread
     // over every CU take the big tile: it reads each operand once (half the
     // operand traffic of 128 x 128 tiles), and that traffic bounds them.
     const int64_t big_tiles = (m / 256) * (n / 256) * batch;
     const TileChoice big = bf16 ? table[0] : kF32Big;
-    if (!packed && !trans_a && m % 256 == 0 && n % 256 == 0 && k % big.bk == 0 && big_tiles > 0 &&
-        big_tiles < kCus &&
+    if (big_shape && k % big.bk == 0 && big_tiles < cus &&
         big_tiles * (splits > 0 ? splits
-                                : auto_splits(big, big_tiles, m, n, k, batch, bf16 ? 2 : 4, max_ws)) >=
-            kCus)
+                                : auto_splits(big, big_tiles, m, n, k, batch, bf16 ? 2 : 4, max_ws, cus)) >=
+            cus)
       pick = bf16 ? 0 : -2;
   }
   if (packed && bf16) pick = 0;
@@ -163,9 +177,9 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
   const int64_t tiles = ceil_div(m, plan.tile.bm) * ceil_div(n, plan.tile.bn) * batch;
   const int64_t kt = ceil_div(k, plan.tile.bk);
   if (splits == 0) {
-    splits = auto_splits(plan.tile, tiles, m, n, k, batch, bf16 ? 2 : 4, max_ws);
-    if (!bf16 && plan.tile.bm < 256 && tiles * 4 <= kCus)
-      splits = std::max(splits, small_f32_splits(tiles, kt, batch * m * n, max_ws));
+    splits = auto_splits(plan.tile, tiles, m, n, k, batch, bf16 ? 2 : 4, max_ws, cus);
+    if (!bf16 && plan.tile.bm < 256 && tiles * 4 <= cus)
+      splits = std::max(splits, small_f32_splits(tiles, kt, batch * m * n, max_ws, cus));
   }
   if (splits < 1) splits = 1;
   if (splits > 1) {
@@ -213,13 +227,13 @@ bool dma_enabled() {
 // tiles, one round of half-size tiles, instead of a last round of full tiles
 // on few CUs. Returns n1, or 0 when the split does not apply. The environment
 // variable HMX_GEMM_ROUNDS=0 turns it off (for comparison).
-int64_t whole_round_columns(int64_t tiles_m, int64_t tiles_n) {
+int64_t whole_round_columns(int64_t tiles_m, int64_t tiles_n, int cus) {
   static const bool on = [] {
     const char* e = getenv("HMX_GEMM_ROUNDS");
     return !(e && e[0] == '0');
   }();
-  const int64_t tiles = tiles_m * tiles_n, tail = tiles % kCus;
-  if (!on || tiles <= kCus || tail == 0 || tail > kCus / 2) return 0;
+  const int64_t tiles = tiles_m * tiles_n, tail = tiles % cus;
+  if (!on || tiles <= cus || tail == 0 || tail > cus / 2) return 0;
   if ((tiles - tail) % tiles_m != 0) return 0;
   return (tiles - tail) / tiles_m;
 }
@@ -234,40 +248,14 @@ bool dma_direct_ok(const GemmArgs& g) {
   return act_ok && pair_ok && g.k_chunk % 32 == 0 && g.k > 0;
 }
 
-}  // namespace
-}  // namespace hmx
-
-using namespace hmx;
-
-extern "C" {
-
-int hmx_gemm_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int trans_a,
-                  int b_layout, int splits, int64_t max_workspace_bytes, int tile_m,
-                  int tile_n, int tile_k, int* out_splits, int* out_tile_m, int* out_tile_n,
-                  int* out_tile_k, int64_t* out_workspace_bytes) {
-  HMX_REQUIRE(valid_dtype(ab_dtype), "gemm_plan: unknown dtype %d", ab_dtype);
-  HMX_REQUIRE(layout_code(b_layout) >= 0, "gemm_plan: unknown B layout %d", b_layout);
-  HMX_REQUIRE(m >= 0 && n >= 0 && k >= 0 && batch >= 1, "gemm_plan: invalid shape");
-  HMX_REQUIRE(splits >= 0, "gemm_plan: negative splits");
-  Plan plan;
-  int st = make_plan(ab_dtype, m, n, k, batch, trans_a, b_layout, splits, max_workspace_bytes, tile_m,
-                     tile_n, tile_k, plan);
-  if (st != HMX_OK) return st;
-  if (out_splits) *out_splits = plan.splits;
-  if (out_tile_m) *out_tile_m = plan.tile.bm;
-  if (out_tile_n) *out_tile_n = plan.tile.bn;
-  if (out_tile_k) *out_tile_k = plan.tile.bk;
-  if (out_workspace_bytes) *out_workspace_bytes = plan.workspace_bytes;
-  return HMX_OK;
-}
-
-int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
-             const void* b, int64_t ldb, int b_layout, int64_t b_panel, int64_t b_kpad,
-             void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int64_t batch,
-             int64_t stride_a, int64_t stride_b, int64_t stride_c, const void* bias,
-             const void* scale, const void* shift, int vec_dtype, int epilogue,
-             float epilogue_arg, int splits, void* workspace, int64_t workspace_bytes,
-             int tile_m, int tile_n, int tile_k, void* stream) {
+// hmx_gemm: checks, plan, launches.
+int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
+              const void* b, int64_t ldb, int b_layout, int64_t b_panel, int64_t b_kpad,
+              void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int64_t batch,
+              int64_t stride_a, int64_t stride_b, int64_t stride_c, const void* bias,
+              const void* scale, const void* shift, int vec_dtype, int epilogue,
+              float epilogue_arg, int splits, void* workspace, int64_t workspace_bytes,
+              int tile_m, int tile_n, int tile_k, void* stream) {
   HMX_REQUIRE(valid_dtype(ab_dtype) && valid_dtype(c_dtype), "gemm: unknown dtype");
   HMX_REQUIRE((bias == nullptr && scale == nullptr && shift == nullptr) || valid_dtype(vec_dtype),
               "gemm: unknown vector dtype %d", vec_dtype);
@@ -299,9 +287,10 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
   HMX_REQUIRE(ldc >= n && ldc >= 1, "gemm: ldc %lld too small", (long long)ldc);
   if (m == 0 || n == 0) return HMX_OK;
 
+  const DeviceShape dev = current_device_shape();
   Plan plan;
-  make_plan(ab_dtype, m, n, k, batch, trans_a, b_layout, splits, workspace ? workspace_bytes : 0,
-            tile_m, tile_n, tile_k, plan);
+  make_plan(ab_dtype, m, n, k, batch, trans_a, b_layout, splits, workspace ? workspace_bytes : 0, tile_m,
+            tile_n, tile_k, dev.cus, plan);
   if (plan.splits > 1) {
     HMX_REQUIRE(workspace != nullptr && workspace_bytes >= plan.workspace_bytes,
                 "gemm: split-K needs %lld workspace bytes, got %lld",
@@ -351,6 +340,8 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
   g.n = n;
   g.k = k;
   g.k_chunk = plan.k_chunk;
+  g.cus = dev.cus;
+  g.xcds = dev.xcds;
   g.tiles_m = (int)tiles_m;
   g.tiles_n = (int)tiles_n;
   g.bias = bias;
@@ -417,7 +408,7 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
         dma_direct_ok(g) && dma_enabled()) {
       const int64_t n1 = whole && (lb_run == L_KCONTIG || lb_run == L_RCONTIG) && plan.splits == 1 &&
                                  batch == 1 && g.k_chunk % 64 == 0
-                             ? whole_round_columns(tiles_m, tiles_n)
+                             ? whole_round_columns(tiles_m, tiles_n, dev.cus)
                              : 0;
       if (n1 > 0) {
         GemmArgs head = g;
@@ -479,6 +470,47 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
                     ((uintptr_t)partials % 16) == 0;
   launch_splitk_reduce((const float*)partials, plan.splits, batch, r, vec4, s);
   return check_launch("gemm split-K reduce");
+}
+
+}  // namespace
+}  // namespace hmx
+
+using namespace hmx;
+
+extern "C" {
+
+int hmx_gemm_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int trans_a,
+                  int b_layout, int splits, int64_t max_workspace_bytes, int tile_m,
+                  int tile_n, int tile_k, int compute_units, int* out_splits, int* out_tile_m,
+                  int* out_tile_n, int* out_tile_k, int64_t* out_workspace_bytes) {
+  HMX_REQUIRE(valid_dtype(ab_dtype), "gemm_plan: unknown dtype %d", ab_dtype);
+  HMX_REQUIRE(layout_code(b_layout) >= 0, "gemm_plan: unknown B layout %d", b_layout);
+  HMX_REQUIRE(m >= 0 && n >= 0 && k >= 0 && batch >= 1, "gemm_plan: invalid shape");
+  HMX_REQUIRE(splits >= 0, "gemm_plan: negative splits");
+  HMX_REQUIRE(compute_units >= 0 && compute_units < 65536, "gemm_plan: invalid CU count %d", compute_units);
+  const int cus = compute_units > 0 ? compute_units : current_device_shape().cus;
+  Plan plan;
+  int st = make_plan(ab_dtype, m, n, k, batch, trans_a, b_layout, splits, max_workspace_bytes, tile_m,
+                     tile_n, tile_k, cus, plan);
+  if (st != HMX_OK) return st;
+  if (out_splits) *out_splits = plan.splits;
+  if (out_tile_m) *out_tile_m = plan.tile.bm;
+  if (out_tile_n) *out_tile_n = plan.tile.bn;
+  if (out_tile_k) *out_tile_k = plan.tile.bk;
+  if (out_workspace_bytes) *out_workspace_bytes = plan.workspace_bytes;
+  return HMX_OK;
+}
+
+int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
+             const void* b, int64_t ldb, int b_layout, int64_t b_panel, int64_t b_kpad,
+             void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int64_t batch,
+             int64_t stride_a, int64_t stride_b, int64_t stride_c, const void* bias,
+             const void* scale, const void* shift, int vec_dtype, int epilogue,
+             float epilogue_arg, int splits, void* workspace, int64_t workspace_bytes,
+             int tile_m, int tile_n, int tile_k, void* stream) {
+  return gemm_impl(ab_dtype, c_dtype, a, lda, trans_a, b, ldb, b_layout, b_panel, b_kpad, c, ldc, m, n, k,
+                   batch, stride_a, stride_b, stride_c, bias, scale, shift, vec_dtype, epilogue,
+                   epilogue_arg, splits, workspace, workspace_bytes, tile_m, tile_n, tile_k, stream);
 }
 
 }  // extern "C"

@@ -235,7 +235,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm_bf16_kernel(GemmArgs g) {
   constexpr int STAGE = (BM + BN) * PITCH;
 
   int tm, tn;
-  tile_coords(g.tiles_m, g.tiles_n, tm, tn);
+  tile_coords(g.tiles_m, g.tiles_n, g.xcds, tm, tn);
   const int split = blockIdx.y, batch = blockIdx.z;
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int64_t k_begin = (int64_t)split * g.k_chunk;

@@ -95,17 +95,21 @@ struct GemmArgs {
   // Nonzero: each workgroup walks its K chunk from a stage of its own
   // (wrapping), for split-K grids whose workgroups share no operand data.
   int k_stagger;
+  // The device's compute units and XCDs (workgroups are dealt to the XCDs
+  // in turn; each XCD has its own L2).
+  int cus, xcds;
 };
 
-// blockIdx.x -> (tile_m, tile_n). Consecutive workgroups are dealt to the 8
-// XCDs in turn; renumbering them so that each XCD gets one contiguous range,
-// then walking that range in groups of kGroupM tile rows, makes the tiles
-// that share A rows and B columns run on the same XCD and its L2.
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
-  constexpr int kXcds = 8, kGroupM = 4;
+// blockIdx.x -> (tile_m, tile_n). Consecutive workgroups are dealt to the
+// device's XCDs in turn; renumbering them so that each XCD gets one
+// contiguous range, then walking that range in groups of kGroupM tile rows,
+// makes the tiles that share A rows and B columns run on the same XCD and its
+// L2.
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int xcds, int& tm, int& tn) {
+  constexpr int kGroupM = 4;
   const int nb = tiles_m * tiles_n;
   int bid = blockIdx.x;
-  if (nb % kXcds == 0) bid = (bid % kXcds) * (nb / kXcds) + bid / kXcds;
+  if (xcds > 1 && nb % xcds == 0) bid = (bid % xcds) * (nb / xcds) + bid / xcds;
   const int per_group = kGroupM * tiles_n;
   const int group = bid / per_group;
   const int first_m = group * kGroupM;

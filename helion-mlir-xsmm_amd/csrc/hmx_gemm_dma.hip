@@ -87,7 +87,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE];
 
   int tm, tn;
-  tile_coords(g.tiles_m, g.tiles_n, tm, tn);
+  tile_coords(g.tiles_m, g.tiles_n, g.xcds, tm, tn);
   const int split = blockIdx.y, batch = blockIdx.z;
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int64_t k_begin = (int64_t)split * g.k_chunk;
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
 
   int tm, tn;
-  tile_coords(g.tiles_m, g.tiles_n, tm, tn);
+  tile_coords(g.tiles_m, g.tiles_n, g.xcds, tm, tn);
   const int split = blockIdx.y, batch = blockIdx.z;
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int64_t k_begin = (int64_t)split * g.k_chunk;
@@ -603,7 +603,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_f32_dma_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
 
   int tm, tn;
-  tile_coords(g.tiles_m, g.tiles_n, tm, tn);
+  tile_coords(g.tiles_m, g.tiles_n, g.xcds, tm, tn);
   const int split = blockIdx.y, batch = blockIdx.z;
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int64_t k_begin = (int64_t)split * g.k_chunk;
@@ -1110,7 +1110,7 @@ void launch_bf16_skinny(const GemmArgs& g, hipStream_t s) {
     launch(gemm_bf16_skinny_kernel<NW, 8, D, RB>, grid, NW * 64, s, g);
 }
 
-// Up to 256 groups of 32 B rows (at most one workgroup per CU): four waves
+// Up to one group of 32 B rows per CU (256 on MI355X): four waves
 // of 32 rows, two stages in flight each; more: four waves of 64 rows (two
 // 32-row blocks share each A fragment, halving A's share of the loads), one
 // stage in flight. Measured with graph replay on one box, M x N x K (torch /
@@ -1121,7 +1121,7 @@ void launch_bf16_skinny(const GemmArgs& g, hipStream_t s) {
 // stage 16.9 / 22.4 / 92.2 / 126.3 us, four waves of 32 rows 18.0 / 24.2 /
 // 95.9 / 119.9 us; two stages in flight or more measured slower there.
 void launch_gemm_bf16_skinny(const GemmArgs& g, hipStream_t s) {
-  if (ceil_div(g.n, 32) <= 256)
+  if (ceil_div(g.n, 32) <= g.cus)
     launch_bf16_skinny<4, 2, 1>(g, s);
   else
     launch_bf16_skinny<4, 1, 2>(g, s);

@@ -46,6 +46,20 @@ inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t 
                                   static_cast<KArgs>(args)...);
 }
 
+// The shape of a device that launches are planned for: its compute units and
+// XCDs (the chiplets workgroups are dealt to in turn, each with its own L2).
+struct DeviceShape {
+  int cus;
+  int xcds;
+};
+// MI355X: 256 CUs in 8 XCDs. Plans made without a device use it.
+constexpr DeviceShape kMi355x = {256, 8};
+
+// The current device's shape, read from the runtime once per device and
+// kept (a device's properties do not change while the process runs). With no
+// device visible: kMi355x.
+DeviceShape current_device_shape();
+
 // Enqueues dst[c, r] = src[r, c] for 16-bit elements, src [rows, cols] with
 // row stride ld, dst [cols, rows] contiguous (hmx_pack.hip).
 void launch_transpose16(const void* src, void* dst, int64_t rows, int64_t cols, int64_t ld,

@@ -25,7 +25,7 @@ import torch
 from ..support.errors import UnsupportedTargetError
 
 LIBRARY_ENV = "HMX_LIBRARY"
-ABI_VERSION = 2  # HMX_ABI_VERSION of include/hmx.h
+ABI_VERSION = 3  # HMX_ABI_VERSION of include/hmx.h
 NATIVE_CALL_ENV = "HELION_MLIR_NATIVE_CALL"
 _DEFAULT = Path(__file__).resolve().parents[3] / "csrc" / "libhmx.so"
 
@@ -77,7 +77,7 @@ SIGNATURES: dict[str, list[object]] = {
         _P,  # stream
     ],
     "hmx_gemm_plan": [
-        _I, _L, _L, _L, _L, _I, _I, _I, _L, _I, _I, _I,
+        _I, _L, _L, _L, _L, _I, _I, _I, _L, _I, _I, _I, _I,
         _IP, _IP, _IP, _IP, _LP,
     ],
     "hmx_softmax_rows": [_I, _P, _P, _L, _L, _P],
@@ -95,7 +95,7 @@ _RESTYPES = {"hmx_last_error": ctypes.c_char_p}
 
 _lock = threading.Lock()
 _lib: list[ctypes.CDLL] = []
-_checked_devices: set[int] = set()
+_device_units: dict[int, int] = {}  # compute units of each checked device
 _calls = [0]
 
 
@@ -183,12 +183,23 @@ def native_calls() -> int:
 def ensure_device(device: torch.device) -> None:
     """Check once per device that it is a gfx950 the library was built for."""
     index = device.index if device.index is not None else torch.cuda.current_device()
-    if index in _checked_devices:
+    if index in _device_units:
         return
     with torch.cuda.device(index):
         units = ctypes.c_int(0)
         check(lib().hmx_device_check(ctypes.byref(units)), "hmx_device_check")
-    _checked_devices.add(index)
+    _device_units[index] = int(units.value)
+
+
+def device_units(device: torch.device | None) -> int:
+    """Compute units of ``device`` (checked as ``ensure_device`` does); 0 --
+    the library's default, MI355X's 256 -- for ``None`` or a non-ROCm device,
+    where plans are made without a GPU."""
+    if device is None or device.type != "cuda" or not torch.cuda.is_available():
+        return 0
+    ensure_device(device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return _device_units[index]
 
 
 # torch's raw current-stream query skips building a Stream object (~0.1 us

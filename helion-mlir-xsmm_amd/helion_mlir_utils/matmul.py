@@ -144,10 +144,11 @@ _PLANS_MAX = 1024
 
 
 def _plan(ab: int, m: int, n: int, k: int, batch: int, trans_a: bool, layout: int,
-          splits: int, tiles: Sequence[int] | None) -> tuple[int, int, int, int, int]:
-    """hmx_gemm_plan: (splits, tile_m, tile_n, tile_k, workspace bytes)."""
+          splits: int, tiles: Sequence[int] | None, units: int = 0) -> tuple[int, int, int, int, int]:
+    """hmx_gemm_plan for a device of ``units`` compute units (0: the
+    library's default): (splits, tile_m, tile_n, tile_k, workspace bytes)."""
     tm, tn, tk = (list(tiles) + [0, 0, 0])[:3] if tiles else (0, 0, 0)
-    key = (ab, m, n, k, batch, bool(trans_a), layout, splits, int(tm), int(tn), int(tk))
+    key = (ab, m, n, k, batch, bool(trans_a), layout, splits, int(tm), int(tn), int(tk), units)
     hit = _PLANS.get(key)
     if hit is not None:
         return hit
@@ -155,7 +156,7 @@ def _plan(ab: int, m: int, n: int, k: int, batch: int, trans_a: bool, layout: in
     ws = ctypes.c_int64()
     native.check(
         native.lib().hmx_gemm_plan(ab, m, n, k, batch, int(trans_a), layout, splits, -1,
-                                   int(tm), int(tn), int(tk), *[ctypes.byref(o) for o in out],
+                                   int(tm), int(tn), int(tk), units, *[ctypes.byref(o) for o in out],
                                    ctypes.byref(ws)),
         "hmx_gemm_plan",
     )
@@ -168,14 +169,19 @@ def _plan(ab: int, m: int, n: int, k: int, batch: int, trans_a: bool, layout: in
 
 def gemm_plan(a_dtype: torch.dtype, m: int, n: int, k: int, batch: int = 1,
               splits: int = 0, block_sizes: Sequence[int] | None = None,
-              trans_b: bool = False) -> dict[str, int]:
+              trans_b: bool = False, compute_units: int | None = None) -> dict[str, int]:
     """The launch the gpu GEMM makes for this problem: K splits, workgroup tile
     and workspace bytes (host-only; the GPU tile table that replaces the
     reference's CPU heuristics, matmul.py:368-446, 1257-1287). ``trans_b``
     plans for B stored [N, K] (``nn.Linear`` weights); tile (32, 32, 64) is
-    the skinny kernel (at most 64 rows of A against such a B)."""
+    the skinny kernel (at most 64 rows of A against such a B). The plan is
+    for a device of ``compute_units`` CUs: by default the current ROCm
+    device's, or MI355X's 256 where none is visible."""
+    if compute_units is None:
+        compute_units = native.device_units(torch.device("cuda") if torch.cuda.is_available() else None)
     s, tm, tn, tk, ws = _plan(native.dtype_code(a_dtype), m, n, k, batch, False,
-                              native.B_TRANS if trans_b else native.B_ROW, splits, block_sizes)
+                              native.B_TRANS if trans_b else native.B_ROW, splits, block_sizes,
+                              int(compute_units))
     return {"splits": s, "tile_m": tm, "tile_n": tn, "tile_k": tk, "workspace_bytes": ws}
 
 
@@ -199,8 +205,10 @@ class GemmLaunch:
         epilogue: tuple[int, float] = (native.EPI_IDENTITY, 0.0), splits: int = 0,
         tiles: Sequence[int] | None = None,
     ) -> None:
-        tm, tn, tk = (list(tiles) + [0, 0, 0])[:3] if tiles else (0, 0, 0)
-        s, _, _, _, ws_bytes = _plan(ab, m, n, k, batch, trans_a, layout, splits, tiles)
+        # The launch passes the plan's own splits and tile back with a
+        # workspace of the planned size, which reproduces the plan exactly.
+        s, tm, tn, tk, ws_bytes = _plan(ab, m, n, k, batch, trans_a, layout, splits, tiles,
+                                        native.device_units(device))
         self._fn = native.lib().hmx_gemm
         self._vectors = (bias, scale, shift)
         # The arguments of hmx_gemm in order (include/hmx.h); slots 2 (A),

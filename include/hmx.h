@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 2
+#define HMX_ABI_VERSION 3
 
 /* Status codes. */
 #define HMX_OK 0
@@ -126,11 +126,12 @@ int hmx_time_launches(void* start_event, void* stop_event);
  * elements. `splits` > 1 divides K into that many chunks whose f32 partials
  * ([splits, batch, M, N] in `workspace`) are summed in a fixed order by a
  * second kernel: results do not depend on timing. splits = 0 lets the
- * library choose (see hmx_gemm_plan). tile_m/tile_n/tile_k request a
- * workgroup tile (0 = default): the largest instantiated tile within the
- * request is used. At most 64 rows of row-major bf16 A against B [N, K]
- * (batch 1, K a multiple of 64; a decode-shaped linear layer) with splits
- * 0 or 1 and no tile requested take a skinny kernel: one workgroup per 32
+ * library choose (see hmx_gemm_plan), for the current device's CU count.
+ * tile_m/tile_n/tile_k request a workgroup tile (0 = default): the largest
+ * instantiated tile within the request is used. At most 64 rows of row-major
+ * bf16 A against B [N, K] (batch 1, K a multiple of 64; a decode-shaped
+ * linear layer) with splits 0 or 1 and no tile requested (or the skinny
+ * kernel's own 32 x 32 x 64) take a skinny kernel: one workgroup per 32
  * columns of C, K split over its waves and summed in a fixed order, no
  * workspace (hmx_gemm_plan reports tile 32 x 32 x 64).
  * Stands in for matmul (helion_mlir_utils/matmul.py:1446-1570), its
@@ -150,14 +151,17 @@ int hmx_gemm(int ab_dtype, int c_dtype,
              int tile_m, int tile_n, int tile_k,
              void* stream);
 
-/* The launch hmx_gemm would make for these arguments, without launching:
- * the K splits (after `splits` = 0 is resolved; `max_workspace_bytes` < 0
- * means unlimited), the workgroup tile and the workspace bytes needed.
- * Host-only; needs no device. Stands in for the tile heuristics
+/* The launch hmx_gemm would make for these arguments on a device of
+ * `compute_units` CUs (0 = the current device's; MI355X's 256 when no device
+ * is visible), without launching: the K splits (after `splits` = 0 is
+ * resolved; `max_workspace_bytes` < 0 means unlimited), the workgroup tile
+ * and the workspace bytes needed. Host-only. Passing the result back to
+ * hmx_gemm -- its splits, its tile as tile_m/n/k and a workspace of its size --
+ * makes exactly the planned launch. Stands in for the tile heuristics
  * _fused_pack_tiles / _split_k (helion_mlir_utils/matmul.py:368-446, 1257-1287). */
 int hmx_gemm_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch,
                   int trans_a, int b_layout, int splits, int64_t max_workspace_bytes,
-                  int tile_m, int tile_n, int tile_k,
+                  int tile_m, int tile_n, int tile_k, int compute_units,
                   int* out_splits, int* out_tile_m, int* out_tile_n, int* out_tile_k,
                   int64_t* out_workspace_bytes);
 

@@ -60,7 +60,7 @@ def test_binding_covers_the_header() -> None:
 
 
 def test_abi_version(lib: ctypes.CDLL) -> None:
-    assert lib.hmx_abi_version() == native.ABI_VERSION == 2
+    assert lib.hmx_abi_version() == native.ABI_VERSION == 3
 
 
 @pytest.mark.parametrize(
@@ -123,10 +123,10 @@ def test_gemm_refuses_bad_arguments(lib: ctypes.CDLL, kw: dict, message: str) ->
 
 def _plan(lib: ctypes.CDLL, ab: int, m: int, n: int, k: int, batch: int = 1, splits: int = 0,
           max_ws: int = -1, tiles: tuple[int, int, int] = (0, 0, 0),
-          b_layout: int = native.B_ROW) -> tuple[int, int, int, int, int]:
+          b_layout: int = native.B_ROW, cus: int = 256, trans_a: int = 0) -> tuple[int, int, int, int, int]:
     outs = [ctypes.c_int() for _ in range(4)]
     ws = ctypes.c_int64()
-    assert lib.hmx_gemm_plan(ab, m, n, k, batch, 0, b_layout, splits, max_ws, *tiles,
+    assert lib.hmx_gemm_plan(ab, m, n, k, batch, trans_a, b_layout, splits, max_ws, *tiles, cus,
                              *[ctypes.byref(o) for o in outs], ctypes.byref(ws)) == 0
     return (*[o.value for o in outs], ws.value)
 
@@ -220,6 +220,62 @@ def test_plan_honours_requests_and_limits(lib: ctypes.CDLL) -> None:
     assert _plan(lib, bf16, 256, 256, 100, splits=8)[0] == 2  # 2 K tiles: 2 chunks
     # The workspace limit stops the split.
     assert _plan(lib, native.DTYPE_F32, 256, 256, 65536, batch=16, max_ws=0)[0] == 1
+
+
+# Shapes across every planner branch: whole and ragged tiles, skinny and
+# split-K products, long K, batches, transposed A and packed layouts.
+_PLAN_SHAPES = [
+    (m, n, k, batch)
+    for m, n, k, batch in [
+        (4096, 4096, 4096, 1), (4000, 4096, 4100, 1), (8192, 11008, 4096, 1), (256, 256, 65536, 16),
+        (256, 256, 4096, 16), (512, 512, 512, 1), (128, 128, 8192, 1), (64, 64, 65536, 1),
+        (32, 11008, 4096, 1), (64, 4128, 64, 16), (16, 64, 4128, 16), (64, 64, 4128, 16),
+        (1000, 4096, 4096, 1), (384, 384, 2048, 1), (256, 256, 1024, 1), (100, 100, 130, 1),
+        (1, 1, 1, 1), (37, 45, 19, 3), (600, 333, 129, 1), (2048, 2048, 2048, 1), (96, 96, 100000, 2),
+    ]
+]
+_PLAN_LAYOUTS = [(native.B_ROW, 0), (native.B_TRANS, 0), (native.B_ROW, 1), (native.B_VNNI_PANELS, 0),
+                 (native.B_BLOCKED, 0), (native.B_PANELS, 0)]
+
+
+@pytest.mark.parametrize("cus", [256, 304, 80, 32])
+@pytest.mark.parametrize("ab", [native.DTYPE_BF16, native.DTYPE_F32])
+def test_a_plan_passed_back_is_the_same_plan(lib: ctypes.CDLL, cus: int, ab: int) -> None:
+    # What a prepared launch does: plan with splits = 0 and no workspace
+    # limit, then call hmx_gemm with the plan's splits, tile and workspace.
+    # hmx_gemm plans again from those; the two plans must agree, or the kernel
+    # that runs is not the one gemm_plan() reports.
+    for m, n, k, batch in _PLAN_SHAPES:
+        for layout, trans_a in _PLAN_LAYOUTS:
+            if ab == native.DTYPE_F32 and layout == native.B_VNNI_PANELS:
+                continue
+            first = _plan(lib, ab, m, n, k, batch, b_layout=layout, cus=cus, trans_a=trans_a)
+            s, tm, tn, tk, ws = first
+            again = _plan(lib, ab, m, n, k, batch, splits=s, max_ws=ws, tiles=(tm, tn, tk), b_layout=layout,
+                          cus=cus, trans_a=trans_a)
+            assert again == first, ((m, n, k, batch, layout, trans_a, cus), first, again)
+
+
+def test_plans_follow_the_device_cu_count(lib: ctypes.CDLL) -> None:
+    bf16, f32 = native.DTYPE_BF16, native.DTYPE_F32
+    # 256 CUs: the baseline plans (test_plans_of_the_baseline_configs).
+    assert _plan(lib, f32, 256, 256, 65536, batch=16, cus=256)[:4] == (16, 256, 256, 32)
+    # 80 CUs: 16 slices x 8 splits already give every CU a workgroup.
+    assert _plan(lib, f32, 256, 256, 65536, batch=16, cus=80)[:4] == (8, 256, 256, 32)
+    # 304 CUs: one split more than 256 CUs need would overshoot the grid; the
+    # 16 x 16 grid underfills, so 32 splits.
+    assert _plan(lib, f32, 256, 256, 65536, batch=16, cus=304)[:4] == (32, 256, 256, 32)
+    # 4096^3 bf16: 256 whole tiles are enough for 32 or 256 CUs; 304 CUs
+    # would leave 48 idle, so 128 x 128 tiles (1024 of them).
+    assert _plan(lib, bf16, 4096, 4096, 4096, cus=32)[:3] == (1, 256, 256)
+    assert _plan(lib, bf16, 4096, 4096, 4096, cus=256)[:3] == (1, 256, 256)
+    assert _plan(lib, bf16, 4096, 4096, 4096, cus=304)[:3] == (1, 128, 128)
+    # The f32 512^3 case: 64 tiles of 64 x 64 split until the grid holds one
+    # workgroup per CU when they fill at most a quarter of the CUs; on 128
+    # CUs they fill half, and the partials would cost more than a quarter of
+    # the operand traffic, so no split.
+    assert _plan(lib, f32, 512, 512, 512, cus=256)[:3] == (4, 64, 64)
+    assert _plan(lib, f32, 512, 512, 512, cus=128)[:3] == (1, 64, 64)
 
 
 @no_device
