@@ -4,11 +4,48 @@
 // hmx_gemm_dma.hip and hmx_gemm_f32.hip.
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 
 #include "hmx_gemm_common.hpp"
 
+// The workspace of hmx_gemm_noalloc: split-K partials and the transposed B
+// of a launch, in device memory the library owns instead of memory a caller
+// allocates. One copy per device, held until the process ends. Host code
+// never uses this name as an address (on the host it names a stand-in, not
+// device memory): it takes each device's address once, from
+// hipGetSymbolAddress, and passes that.
+static __device__ __align__(256) uint8_t scratch[HMX_GEMM_SCRATCH_BYTES];
+
 namespace hmx {
 namespace {
+
+constexpr int64_t kScratchBytes = HMX_GEMM_SCRATCH_BYTES;
+
+// The address of `scratch` on the current device, looked up once per device
+// (with that device current) and kept.
+int scratch_of_current_device(void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex lock;
+  static void* addresses[kMaxDevices] = {};
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess)
+    return set_error(HMX_ERR_HIP, "gemm_noalloc: hipGetDevice: %s", hipGetErrorString(err));
+  if (device < 0 || device >= kMaxDevices)
+    return set_error(HMX_ERR_INVALID, "gemm_noalloc: device %d is past the %d devices the scratch serves",
+                     device, kMaxDevices);
+  std::lock_guard<std::mutex> guard(lock);
+  if (addresses[device] == nullptr) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr)
+      return set_error(HMX_ERR_HIP, "gemm_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", device,
+                       hipGetErrorString(err));
+    addresses[device] = p;
+  }
+  *out = addresses[device];
+  return HMX_OK;
+}
 
 struct TileChoice {
   int bm, bn, bk;
@@ -248,14 +285,19 @@ bool dma_direct_ok(const GemmArgs& g) {
   return act_ok && pair_ok && g.k_chunk % 32 == 0 && g.k > 0;
 }
 
-// hmx_gemm: checks, plan, launches.
+// hmx_gemm and hmx_gemm_noalloc: checks, plan, launches. The workspace is
+// `workspace` (workspace_bytes long) or, with `use_scratch`, the library's
+// own per-device scratch array, looked up only when the plan needs workspace.
+// Every workspace byte a launch reads it has written first (the B transpose
+// and each split's whole partial tile), so nothing needs clearing between
+// calls.
 int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
               const void* b, int64_t ldb, int b_layout, int64_t b_panel, int64_t b_kpad,
               void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int64_t batch,
               int64_t stride_a, int64_t stride_b, int64_t stride_c, const void* bias,
               const void* scale, const void* shift, int vec_dtype, int epilogue,
               float epilogue_arg, int splits, void* workspace, int64_t workspace_bytes,
-              int tile_m, int tile_n, int tile_k, void* stream) {
+              bool use_scratch, int tile_m, int tile_n, int tile_k, void* stream) {
   HMX_REQUIRE(valid_dtype(ab_dtype) && valid_dtype(c_dtype), "gemm: unknown dtype");
   HMX_REQUIRE((bias == nullptr && scale == nullptr && shift == nullptr) || valid_dtype(vec_dtype),
               "gemm: unknown vector dtype %d", vec_dtype);
@@ -289,8 +331,20 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
 
   const DeviceShape dev = current_device_shape();
   Plan plan;
-  make_plan(ab_dtype, m, n, k, batch, trans_a, b_layout, splits, workspace ? workspace_bytes : 0, tile_m,
-            tile_n, tile_k, dev.cus, plan);
+  make_plan(ab_dtype, m, n, k, batch, trans_a, b_layout, splits,
+            use_scratch ? kScratchBytes : (workspace ? workspace_bytes : 0), tile_m, tile_n, tile_k, dev.cus,
+            plan);
+  if (use_scratch) {
+    HMX_REQUIRE(plan.workspace_bytes <= kScratchBytes,
+                "gemm_noalloc: the launch needs %lld bytes of workspace and the library's scratch holds "
+                "%lld: ask for fewer splits (splits = 0 plans within the scratch)",
+                (long long)plan.workspace_bytes, (long long)kScratchBytes);
+    if (plan.workspace_bytes > 0) {
+      const int st = scratch_of_current_device(&workspace);
+      if (st != HMX_OK) return st;
+      workspace_bytes = kScratchBytes;
+    }
+  }
   if (plan.splits > 1) {
     HMX_REQUIRE(workspace != nullptr && workspace_bytes >= plan.workspace_bytes,
                 "gemm: split-K needs %lld workspace bytes, got %lld",
@@ -510,7 +564,19 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
              int tile_m, int tile_n, int tile_k, void* stream) {
   return gemm_impl(ab_dtype, c_dtype, a, lda, trans_a, b, ldb, b_layout, b_panel, b_kpad, c, ldc, m, n, k,
                    batch, stride_a, stride_b, stride_c, bias, scale, shift, vec_dtype, epilogue,
-                   epilogue_arg, splits, workspace, workspace_bytes, tile_m, tile_n, tile_k, stream);
+                   epilogue_arg, splits, workspace, workspace_bytes, false, tile_m, tile_n, tile_k, stream);
+}
+
+int hmx_gemm_noalloc(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
+                     const void* b, int64_t ldb, int b_layout, int64_t b_panel, int64_t b_kpad,
+                     void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int64_t batch,
+                     int64_t stride_a, int64_t stride_b, int64_t stride_c, const void* bias,
+                     const void* scale, const void* shift, int vec_dtype, int epilogue,
+                     float epilogue_arg, int splits, int tile_m, int tile_n, int tile_k,
+                     void* stream) {
+  return gemm_impl(ab_dtype, c_dtype, a, lda, trans_a, b, ldb, b_layout, b_panel, b_kpad, c, ldc, m, n, k,
+                   batch, stride_a, stride_b, stride_c, bias, scale, shift, vec_dtype, epilogue,
+                   epilogue_arg, splits, nullptr, 0, true, tile_m, tile_n, tile_k, stream);
 }
 
 }  // extern "C"

@@ -35,6 +35,7 @@ DTYPE_F32, DTYPE_BF16 = 0, 1
 EPI_IDENTITY, EPI_RELU, EPI_SILU, EPI_SIGMOID = 0, 1, 2, 3
 EPI_GELU, EPI_GELU_TANH, EPI_TANH, EPI_LEAKY_RELU = 4, 5, 6, 7
 B_ROW, B_TRANS, B_VNNI_PANELS, B_BLOCKED_VNNI, B_PANELS, B_BLOCKED = range(6)
+GEMM_SCRATCH_BYTES = 64 << 20  # HMX_GEMM_SCRATCH_BYTES
 EXTRA_NONE, EXTRA_ADD, EXTRA_MUL = 0, 1, 2
 ELT_RELU, ELT_LEAKY_RELU, ELT_SCALE = 0, 1, 2
 (
@@ -73,6 +74,19 @@ SIGNATURES: dict[str, list[object]] = {
         _P, _P, _P, _I,  # bias, scale, shift, vec_dtype
         _I, _F,  # epilogue, epilogue_arg
         _I, _P, _L,  # splits, workspace, workspace_bytes
+        _I, _I, _I,  # tile_m, tile_n, tile_k
+        _P,  # stream
+    ],
+    "hmx_gemm_noalloc": [
+        _I, _I,  # ab_dtype, c_dtype
+        _P, _L, _I,  # a, lda, trans_a
+        _P, _L, _I, _L, _L,  # b, ldb, b_layout, b_panel, b_kpad
+        _P, _L,  # c, ldc
+        _L, _L, _L,  # m, n, k
+        _L, _L, _L, _L,  # batch, stride_a, stride_b, stride_c
+        _P, _P, _P, _I,  # bias, scale, shift, vec_dtype
+        _I, _F,  # epilogue, epilogue_arg
+        _I,  # splits
         _I, _I, _I,  # tile_m, tile_n, tile_k
         _P,  # stream
     ],

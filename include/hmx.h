@@ -7,7 +7,8 @@
  *     hmx_last_error() holds a message for the calling thread.
  *   - Pointers are device pointers owned by the caller (torch tensors on the
  *     Python side). Nothing is allocated inside: split-K partials go to the
- *     caller's `workspace`.
+ *     caller's `workspace` (hmx_gemm_noalloc: to the library's static
+ *     per-device scratch).
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream)
  *     and runs asynchronously. Functions keep no mutable global state (only
  *     per-thread error messages and timing events), so they may be called
@@ -150,6 +151,33 @@ int hmx_gemm(int ab_dtype, int c_dtype,
              int splits, void* workspace, int64_t workspace_bytes,
              int tile_m, int tile_n, int tile_k,
              void* stream);
+
+/* Bytes of device memory hmx_gemm_noalloc keeps per device for its
+ * workspace (64 MiB: config 5's 16 split-K partials of [16, 256, 256] f32). */
+#define HMX_GEMM_SCRATCH_BYTES (64ll << 20)
+
+/* hmx_gemm without a caller workspace and without allocating anything: the
+ * split-K partials and a transposed B go to a workspace the library holds per
+ * device (a static device array of HMX_GEMM_SCRATCH_BYTES, taken on each
+ * device's first call and kept until the process ends). No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The arguments are hmx_gemm's. splits = 0 plans within the scratch; a
+ * launch that needs more workspace than it holds (explicit splits) is
+ * refused with HMX_ERR_INVALID. Calls on one device share its scratch, so
+ * calls that overlap on one device (other streams, other threads) race:
+ * order them on one stream. Results equal hmx_gemm's for the same plan. */
+int hmx_gemm_noalloc(int ab_dtype, int c_dtype,
+                     const void* a, int64_t lda, int trans_a,
+                     const void* b, int64_t ldb, int b_layout, int64_t b_panel, int64_t b_kpad,
+                     void* c, int64_t ldc,
+                     int64_t m, int64_t n, int64_t k,
+                     int64_t batch, int64_t stride_a, int64_t stride_b, int64_t stride_c,
+                     const void* bias, const void* scale, const void* shift, int vec_dtype,
+                     int epilogue, float epilogue_arg,
+                     int splits,
+                     int tile_m, int tile_n, int tile_k,
+                     void* stream);
 
 /* The launch hmx_gemm would make for these arguments on a device of
  * `compute_units` CUs (0 = the current device's; MI355X's 256 when no device

@@ -279,6 +279,17 @@ def test_plans_follow_the_device_cu_count(lib: ctypes.CDLL) -> None:
 
 
 @no_device
+def test_noalloc_refuses_a_plan_beyond_its_scratch(lib: ctypes.CDLL) -> None:
+    # 64 explicit splits of [16, 256, 256] f32 partials need 256 MiB; the
+    # scratch holds 64 MiB: refused on the host, before any device call.
+    args = (native.DTYPE_F32, native.DTYPE_F32, 256, 8192, 0, 512, 256, native.B_ROW, 0, 0, 1024, 256,
+            256, 256, 8192, 16, 256 * 8192, 8192 * 256, 256 * 256, None, None, None, native.DTYPE_F32,
+            native.EPI_IDENTITY, 0.0, 64, 0, 0, 0, None)
+    assert lib.hmx_gemm_noalloc(*args) == native.ERR_INVALID
+    assert "scratch" in native.last_error() and str(native.GEMM_SCRATCH_BYTES) in native.last_error()
+
+
+@no_device
 def test_error_message_is_per_thread(lib: ctypes.CDLL) -> None:
     import threading
 
