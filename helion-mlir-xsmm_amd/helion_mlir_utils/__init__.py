@@ -4,12 +4,15 @@ The entry points and signatures are those of the reference's
 ``helion_mlir_utils`` (``helion_mlir_utils/__init__.py:5-69``); tensors on a
 ROCm device run hand-written gfx950 kernels through ``libhmx.so``. New here:
 ``rms_norm``, ``layer_norm``, ``Activation`` epilogues, ``out_dtype`` of
-``matmul``/``bmm``, and the bench panel packers.
+``matmul``/``bmm``, and the benchmarks' panel packers and panel-major
+product (:mod:`.block_pack`).
 """
 
 from __future__ import annotations
 
+from . import block_pack
 from ._gpu import Activation, register_epilogue
+from .block_pack import matmul_packed_b_f32, pack_b_panels_f32, unpack_panel_major
 from .elementwise import leaky_relu, relu, scalar_mul
 from .heuristics import tall_output_tiles, vnni_panel, whole_row_tiles
 from .kernels import per_config
@@ -63,6 +66,7 @@ __all__ = [
     "matmul",
     "matmul_prepacked_b",
     "matmul_prepacked_b_affine",
+    "matmul_packed_b_f32",
     "matvec",
     "pack_a_blocked",
     "pack_a_blocked_t",
@@ -72,6 +76,7 @@ __all__ = [
     "pack_b_blocked_vnni",
     "pack_b_blocked_vnni_t",
     "pack_b_panels",
+    "pack_b_panels_f32",
     "pack_b_vnni_t",
     "pad_2d",
     "per_config",
@@ -86,6 +91,7 @@ __all__ = [
     "supports",
     "supports_matvec",
     "tall_output_tiles",
+    "unpack_panel_major",
     "vnni_panel",
     "whole_row_tiles",
 ]

@@ -468,18 +468,32 @@ def pack_b_vnni_t(b_t: Tensor, panel: int = _VNNI_PANEL) -> Tensor:
                  (n_pad // panel, k_pad // 2, panel, 2), panel)
 
 
-def pack_b_panels(b: Tensor, block_n: int) -> Tensor:
+def pack_b_panels(b: Tensor, block_n: int | None = None) -> Tensor:
     """``[K, N]`` into panel-major ``[N/block_n, K, block_n]``
-    (``benchmarks/helion_block_pack.py:66-71``)."""
+    (``benchmarks/helion_block_pack.py:66-71``). Also takes the benchmark's
+    own form, a ``[K, N/BN, BN]`` view with no ``block_n``
+    (``helion_block_pack.py:40-51``)."""
+    if b.dim() == 3 and block_n is None:
+        k, panels, block_n = map(int, b.shape)
+        b = b.reshape(k, panels * block_n)
+    if block_n is None:
+        raise ValueError("pack_b_panels() of a 2-D [K, N] tensor needs block_n")
     k, n = map(int, b.shape)
     if block_n <= 0 or n % block_n:
         raise ValueError(f"N={n} is not a multiple of block_n={block_n}")
     return _pack(native.PACK_B_PANELS, b, k, n, (n // block_n, k, block_n), block_n)
 
 
-def pack_a_panels(a: Tensor, block_k: int) -> Tensor:
+def pack_a_panels(a: Tensor, block_k: int | None = None) -> Tensor:
     """``[M, K]`` into ``[K/block_k, M, block_k]``
-    (``benchmarks/helion_block_pack.py:74-79``)."""
+    (``benchmarks/helion_block_pack.py:74-79``). Also takes the benchmark's
+    own form, a ``[M, K/BK, BK]`` view with no ``block_k``
+    (``helion_block_pack.py:54-62``)."""
+    if a.dim() == 3 and block_k is None:
+        m, panels, block_k = map(int, a.shape)
+        a = a.reshape(m, panels * block_k)
+    if block_k is None:
+        raise ValueError("pack_a_panels() of a 2-D [M, K] tensor needs block_k")
     m, k = map(int, a.shape)
     if block_k <= 0 or k % block_k:
         raise ValueError(f"K={k} is not a multiple of block_k={block_k}")
@@ -538,11 +552,10 @@ def _packed_layout(a: Tensor, b4: Tensor, n: int) -> tuple[int, int, int, int]:
                 f"a.shape={(m, k)} {a.dtype} and n={n}"
             )
         return native.B_BLOCKED_VNNI, 32, blocks_k * BLOCK_K, blocks_n * BLOCK_N
-    if b4.dim() == 3:  # bench panels: [N/P, K, P]
+    if b4.dim() == 3:  # bench panels: [N/P, K, P] (bf16 or f32)
         panels, kk, panel = shape
         if (
-            a.dtype != torch.bfloat16
-            or kk != k
+            kk != k
             or panel % 8
             or _round_up(n, panel) != panels * panel
         ):
