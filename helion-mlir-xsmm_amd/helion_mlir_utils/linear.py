@@ -1,32 +1,43 @@
-"""``nn.Linear`` on the gpu target, with the weight prepared once and cached.
+"""``nn.Linear`` on the gpu target: the weight is prepared once and its launch
+kept for reuse.
 
-Reference: ``helion_mlir_utils/linear.py`` (``linear`` 97-180, ``linear_affine``
-183-261). The cache is keyed, as there, by the parameters' data pointers,
-``_version``, shapes, dtypes and devices plus the input's dtype, device and
-rows: in-place updates and ``load_state_dict`` are seen, a change through
-``.data`` is not.
+Interface of the reference's ``helion_mlir_utils/linear.py`` (``linear``
+97-180, ``linear_affine`` 183-261): the same functions, arguments, cache
+types and environment switch, so callers hold and pass caches unchanged.
 
-On gfx950 the GEMM kernel's preferred B layout is ``[N, K]`` row-major (each
-MFMA operand fragment is 8 consecutive K values), which is what
-``nn.Linear.weight`` already is: "prepacking" keeps the weight contiguous in
-the input's dtype. ``panel`` asks for the reference's VNNI panels
-(:func:`~.matmul.pack_b_vnni_t`) instead, which the kernel reads in place too.
-The cached call is a :class:`~helion_mlir_backend.PreparedCall`: per call, a
-shape check and one launch.
+How it works here. A call is one GEMM launch with the bias, the optional
+per-column affine post-op and the activation fused. What can be prepared
+ahead is:
+
+* the weight in the layout the kernel reads -- ``[N, K]`` row-major, which is
+  what ``nn.Linear.weight`` already is (the MFMA B fragment is 8 consecutive
+  K values), kept contiguous in the input's dtype; or, when the caller names
+  ``panel``, the reference's VNNI panels (``pack_b_vnni_t``), read in place;
+* the biases, summed once into one vector;
+* the launch itself (plan, workspace size, bound argument block): a
+  :class:`~helion_mlir_backend.PreparedCall`, so a call is a shape check and
+  one native launch.
+
+A cache is valid while the parameters it was made from are unchanged as far
+as their data pointers, ``_version`` counters, shapes, dtypes and devices
+tell, and the input keeps its dtype, device and row count: in-place updates
+and ``load_state_dict`` invalidate it, a write through ``.data`` does not
+(pass ``cache=None`` after one).
 """
 
 from __future__ import annotations
 
+import functools
 import os
 from typing import TYPE_CHECKING, Callable, NamedTuple
 
 import torch
 
-from helion_mlir_backend import output_pool, prepared_call
+from helion_mlir_backend import prepared_call
 from helion_mlir_backend._compiler import native
 
 from ._gpu import epilogue_code, identity_epilogue, is_gpu
-from .matmul import GemmLaunch, _vectors, matmul, matmul_prepacked_b, pack_b_vnni_t, prepacked_b_call
+from .matmul import GemmLaunch, _vectors, matmul, pack_b_vnni_t, prepacked_b_call
 
 if TYPE_CHECKING:
     from torch import Tensor, nn
@@ -41,13 +52,13 @@ __all__ = [
 ]
 
 CACHE_PREPACKED_WEIGHTS_ENV = "HELION_MLIR_CACHE_PREPACKED_WEIGHTS"
+_SWITCHED_OFF = frozenset({"0", "false", "no"})
 
 
 def cache_prepacked_weights() -> bool:
-    """Whether constant weights are prepared once and reused (the default);
-    ``HELION_MLIR_CACHE_PREPACKED_WEIGHTS=0`` prepares them on every call."""
-    value = os.environ.get(CACHE_PREPACKED_WEIGHTS_ENV)
-    return value is None or value.strip().lower() not in ("0", "false", "no")
+    """False when ``HELION_MLIR_CACHE_PREPACKED_WEIGHTS`` is 0 / false / no:
+    then every call prepares the weight again and returns no cache."""
+    return os.environ.get(CACHE_PREPACKED_WEIGHTS_ENV, "").strip().lower() not in _SWITCHED_OFF
 
 
 class LinearCache(NamedTuple):
@@ -56,7 +67,7 @@ class LinearCache(NamedTuple):
     bias: Tensor | None
     out_features: int
     call: tuple | None = None
-    """``(epilogue, prepared call)`` of the last call."""
+    """``(epilogue, prepared call)`` made for the last epilogue used."""
 
 
 class AffineLinearCache(NamedTuple):
@@ -69,66 +80,73 @@ class AffineLinearCache(NamedTuple):
     call: tuple | None = None
 
 
-def _parameter_key(parameter: Tensor | None) -> tuple | None:
-    if parameter is None:
+def _fingerprint(t: Tensor | None) -> tuple | None:
+    """What identifies a parameter's contents without reading them."""
+    if t is None:
         return None
-    return (
-        parameter.data_ptr(),
-        parameter._version,
-        tuple(parameter.shape),
-        parameter.dtype,
-        parameter.device,
-    )
+    return (t.data_ptr(), t._version, tuple(t.shape), t.dtype, t.device)
 
 
-def _combine_biases(biases: tuple[Tensor, ...], x: Tensor) -> Tensor | None:
-    if not biases:
+def _as_input(x: Tensor, t: Tensor | None) -> Tensor | None:
+    """``t`` detached, in ``x``'s dtype, on ``x``'s device."""
+    return None if t is None else t.detach().to(dtype=x.dtype, device=x.device)
+
+
+def _one_bias(parts: tuple[Tensor, ...], x: Tensor) -> Tensor | None:
+    """The given bias vectors added left to right in ``x``'s dtype (each sum
+    rounded to it, as adding the tensors one by one would)."""
+    if not parts:
         return None
-    bias = biases[0].to(dtype=x.dtype, device=x.device)
-    for extra_bias in biases[1:]:
-        bias = bias + extra_bias.to(dtype=x.dtype, device=x.device)
-    return bias
+    return functools.reduce(torch.add, (_as_input(x, p) for p in parts))
 
 
-def _pack_weight(weight: Tensor, panel: int | None) -> Tensor:
-    """The weight as the kernel reads it: ``[N, K]`` row-major, or VNNI panels
-    of ``panel`` columns when asked (bf16, even K)."""
-    if panel is not None and weight.dtype == torch.bfloat16 and not weight.shape[1] % 2:
+def _kernel_weight(weight: Tensor, panel: int | None) -> Tensor:
+    """The weight as the kernel will read it: ``[N, K]`` contiguous, or VNNI
+    panels of ``panel`` columns when asked for (bf16, even K)."""
+    if panel is not None and weight.dtype == torch.bfloat16 and weight.shape[1] % 2 == 0:
         return pack_b_vnni_t(weight, panel)
     return weight.contiguous()
 
 
-def _weight_call(
+def _launcher(
     x: Tensor,
-    packed: Tensor,
+    weight: Tensor,
     n: int,
     bias: Tensor | None,
     epilogue: Callable[[Tensor], Tensor],
     scale: Tensor | None = None,
     shift: Tensor | None = None,
 ) -> Callable[[Tensor], Tensor]:
-    """A prepared ``epilogue((x @ W^T + bias) * scale + shift)`` for inputs
-    like ``x``."""
-    if packed.dim() != 2:
-        return prepacked_b_call(x, packed, n, bias, epilogue, scale, shift)
+    """A prepared ``epilogue((x @ W^T + bias) * scale + shift)`` for inputs of
+    ``x``'s shape, dtype and device; any other input goes through the general
+    entry point, which checks it."""
+    if weight.dim() != 2:  # VNNI panels
+        return prepacked_b_call(x, weight, n, bias, epilogue, scale, shift)
 
     def general(a: Tensor) -> Tensor:
-        return matmul(a, packed, trans_b=True, bias=bias, epilogue=epilogue, scale=scale, shift=shift)
+        return matmul(a, weight, trans_b=True, bias=bias, epilogue=epilogue, scale=scale, shift=shift)
 
-    if x.dim() != 2 or not is_gpu(x, packed) or x.dtype != packed.dtype:
+    m, k = (int(d) for d in x.shape) if x.dim() == 2 else (0, 0)
+    plain = (x.dim() == 2 and is_gpu(x, weight) and x.dtype == weight.dtype and m > 0 and n > 0 and k > 0
+             and int(weight.shape[1]) == k)
+    if not plain:
         return general
-    m, k = map(int, x.shape)
-    if m == 0 or n == 0 or k == 0 or int(packed.shape[1]) != k:
-        return general
-    code = epilogue_code(epilogue)
-    bias_, scale_, shift_, vec_dtype = _vectors(bias, scale, shift, n, x)
-    dtype, device = x.dtype, x.device
-
+    vec_bias, vec_scale, vec_shift, vec_dtype = _vectors(bias, scale, shift, n, x)
     launch = GemmLaunch(
-        native.dtype_code(dtype), dtype, device, (m, n), k, False, k, native.B_TRANS, 0, 0, m, n, k,
-        bias=bias_, scale=scale_, shift=shift_, vec_dtype=vec_dtype, epilogue=code,
+        native.dtype_code(x.dtype), x.dtype, x.device, (m, n), k, False, k, native.B_TRANS, 0, 0, m, n, k,
+        bias=vec_bias, scale=vec_scale, shift=vec_shift, vec_dtype=vec_dtype, epilogue=epilogue_code(epilogue),
     )
-    return prepared_call(lambda a: launch.run(a, packed), [x], general)
+    return prepared_call(lambda a: launch.run(a, weight), [x], general)
+
+
+def _with_call(cache, epilogue, make: Callable[[], Callable[[Tensor], Tensor]]):
+    """``(call, cache)``: the cache's prepared call if it was made for this
+    epilogue, else a new one, kept in the returned cache."""
+    held = cache.call
+    if held is not None and held[0] is epilogue:
+        return held[1], cache
+    call = make()
+    return call, cache._replace(call=(epilogue, call))
 
 
 def linear(
@@ -140,45 +158,27 @@ def linear(
     panel: int | None = None,
     whole_rows: bool = False,
 ) -> tuple[Tensor, LinearCache | None]:
-    """``epilogue(x @ layer.weight.T + bias)`` and the cache to pass next time
-    (``linear.py:97-180``). ``biases`` replaces ``layer.bias`` by the sum of
-    the given vectors. ``panel`` packs a bf16 weight into VNNI panels of that
-    width; ``whole_rows`` is accepted for the reference's API (on the GPU a
-    row of output tiles always runs on one XCD)."""
-    del whole_rows
-    if biases is None:
-        bias = layer.bias
-        source_biases = () if bias is None else (bias,)
-    else:
-        source_biases = biases
+    """``(epilogue(x @ layer.weight.T + bias), cache)`` (``linear.py:97-180``).
+
+    ``biases`` replaces ``layer.bias`` by the sum of the given vectors.
+    ``panel`` keeps a bf16 weight as VNNI panels of that many columns.
+    ``whole_rows`` asks that each row block of ``x`` be read by one cache
+    domain: on the GPU each 256-row block of the output's tiles is walked by
+    the workgroups of one XCD, which share its L2, whatever the flag says; it
+    is kept in the cache key, as in the reference."""
+    parts = tuple(biases) if biases is not None else (() if layer.bias is None else (layer.bias,))
     if not cache_prepacked_weights():
-        weight = layer.weight.detach().to(dtype=x.dtype, device=x.device)
-        return (
-            matmul(x, weight, trans_b=True, bias=_combine_biases(source_biases, x), epilogue=epilogue),
-            None,
-        )
-    key = (
-        _parameter_key(layer.weight),
-        tuple(map(_parameter_key, source_biases)),
-        x.dtype,
-        x.device,
-        x.shape[0],
-        panel,
-    )
+        y = matmul(x, _as_input(x, layer.weight), trans_b=True, bias=_one_bias(parts, x), epilogue=epilogue)
+        return y, None
+    key = (_fingerprint(layer.weight), tuple(_fingerprint(p) for p in parts), x.dtype, x.device,
+           x.shape[0], panel, bool(whole_rows))
     if cache is None or cache.key != key:
-        weight = layer.weight.detach().to(dtype=x.dtype, device=x.device)
-        cache = LinearCache(
-            key,
-            _pack_weight(weight, panel),
-            _combine_biases(tuple(b.detach() for b in source_biases), x),
-            int(layer.out_features),
-        )
-    prepared = cache.call
-    if prepared is None or prepared[0] is not epilogue:
-        call = _weight_call(x, cache.packed_weight, cache.out_features, cache.bias, epilogue)
-        cache = cache._replace(call=(epilogue, call))
-    else:
-        call = prepared[1]
+        cache = LinearCache(key, _kernel_weight(_as_input(x, layer.weight), panel), _one_bias(parts, x),
+                            int(layer.out_features))
+    fresh = cache
+    call, cache = _with_call(
+        cache, epilogue, lambda: _launcher(x, fresh.packed_weight, fresh.out_features, fresh.bias, epilogue)
+    )
     return call(x), cache
 
 
@@ -190,39 +190,22 @@ def linear_affine(
     epilogue: Callable[[Tensor], Tensor] = identity_epilogue,
     cache: AffineLinearCache | None = None,
 ) -> tuple[Tensor, AffineLinearCache | None]:
-    """``epilogue(linear(x) * post_scale + post_bias)``; ``post_scale`` and
-    ``post_bias`` are ``[1]`` or ``[out_features]`` (``linear.py:183-261``).
-    Cached like :func:`linear`."""
-    use_cache = cache_prepacked_weights()
-    key = (
-        _parameter_key(layer.weight),
-        _parameter_key(layer.bias),
-        _parameter_key(post_scale),
-        _parameter_key(post_bias),
-        x.dtype,
-        x.device,
-        x.shape[0],
+    """``(epilogue(linear(x) * post_scale + post_bias), cache)``;
+    ``post_scale`` and ``post_bias`` are ``[1]`` or ``[out_features]``
+    (``linear.py:183-261``). Cached like :func:`linear`."""
+    if not cache_prepacked_weights():
+        y = matmul(x, _as_input(x, layer.weight), trans_b=True, bias=_as_input(x, layer.bias), epilogue=epilogue,
+                   scale=_as_input(x, post_scale), shift=_as_input(x, post_bias))
+        return y, None
+    key = (_fingerprint(layer.weight), _fingerprint(layer.bias), _fingerprint(post_scale),
+           _fingerprint(post_bias), x.dtype, x.device, x.shape[0])
+    if cache is None or cache.key != key:
+        cache = AffineLinearCache(key, _kernel_weight(_as_input(x, layer.weight), None), _as_input(x, layer.bias),
+                                  _as_input(x, post_scale), _as_input(x, post_bias), int(layer.out_features))
+    fresh = cache
+    call, cache = _with_call(
+        cache, epilogue,
+        lambda: _launcher(x, fresh.packed_weight, fresh.out_features, fresh.bias, epilogue, fresh.post_scale,
+                          fresh.post_bias),
     )
-    if not use_cache or cache is None or cache.key != key:
-        weight = layer.weight.detach().to(dtype=x.dtype, device=x.device)
-        bias = None if layer.bias is None else layer.bias.detach().to(dtype=x.dtype, device=x.device)
-        cache = AffineLinearCache(
-            key,
-            _pack_weight(weight, None),
-            bias,
-            post_scale.detach().to(dtype=x.dtype, device=x.device),
-            None if post_bias is None else post_bias.detach().to(dtype=x.dtype, device=x.device),
-            int(layer.out_features),
-        )
-    if not use_cache:
-        result = matmul(x, cache.packed_weight, trans_b=True, bias=cache.bias, epilogue=epilogue,
-                        scale=cache.post_scale, shift=cache.post_bias)
-        return result, None
-    prepared = cache.call
-    if prepared is None or prepared[0] is not epilogue:
-        call = _weight_call(x, cache.packed_weight, cache.out_features, cache.bias, epilogue,
-                            cache.post_scale, cache.post_bias)
-        cache = cache._replace(call=(epilogue, call))
-    else:
-        call = prepared[1]
     return call(x), cache
