@@ -21,10 +21,15 @@ pass of K steps gives each step its own event pair, recorded by the step's
 first and last kernels themselves (``hmx_time_launches``):
 ``roofline.achieved`` is the algorithmic work per launch of the dominant
 kernel over the mean of those pairs (its average launch duration, as a kernel
-trace measures it). ``roofline.traffic`` is the HBM bytes per launch measured
-with rocprofv3 counters (``profiles/traffic.json``), or null when not measured.
-``cpu_baseline`` times the CPU oracle (``oracle/restate.py``, numpy) on the
-host cores on a bounded sample of the same workload.
+trace measures it). ``roofline.traffic`` is the bytes per launch that left the L2 caches for the
+memory fabric, measured with rocprofv3 counters (``profiles/traffic.json``:
+the L2's read requests to memory by size, and WRITE_SIZE); reads that hit the
+256 MB last-level cache (MALL) in front of HBM count too, so for operands
+that fit it the figure is L2-miss traffic, an upper bound on HBM bytes. Null
+when not measured. ``cpu_baseline`` times the same math on the host with
+torch (one thread per usable core: the process's CPU affinity, capped by
+OMP_NUM_THREADS) on a bounded sample of the workload, with the CPU oracle
+(``oracle/restate.py``, numpy) on the same sample beside it.
 """
 
 from __future__ import annotations
@@ -59,16 +64,38 @@ def _cpu_model() -> str:
     return platform.processor() or platform.machine()
 
 
-def _blas_threads() -> int:
+def _cpu_cores() -> int:
+    """Host cores this process may use: its CPU affinity, capped by
+    OMP_NUM_THREADS when that is set (a GPU box's share of its host)."""
+    cores = len(os.sched_getaffinity(0))
     try:
-        from threadpoolctl import threadpool_info
-
-        counts = [info.get("num_threads", 1) for info in threadpool_info() if info.get("user_api") == "blas"]
-        if counts:
-            return int(max(counts))
-    except Exception:  # noqa: BLE001 - only for reporting
+        cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+    except ValueError:
         pass
-    return len(os.sched_getaffinity(0))
+    return max(cores, 1)
+
+
+def _torch_cpu(fn, work: float, budget_s: float = 10.0) -> tuple[float, int, int]:
+    """(work units per second, reps, threads) of ``fn`` run by torch on the
+    host with one thread per usable core."""
+    import torch
+
+    threads = _cpu_cores()
+    torch.set_num_threads(threads)
+    rate, reps = _time_cpu(fn, work, budget_s=budget_s)
+    return rate, reps, threads
+
+
+def _blas_limited(threads: int):
+    """numpy's BLAS limited to ``threads`` threads (a context manager)."""
+    try:
+        from threadpoolctl import threadpool_limits
+
+        return threadpool_limits(limits=threads, user_api="blas")
+    except Exception:  # noqa: BLE001 - no limiter: numpy runs as configured
+        import contextlib
+
+        return contextlib.nullcontext()
 
 
 class Workload:
@@ -135,14 +162,25 @@ class Gemm(Workload):
         return self.U.matmul(self.a, self.b, out_dtype=self.out_dtype)
 
     def cpu_baseline(self) -> dict:
+        """torch's CPU bf16 matmul (oneDNN, f32 accumulation) on the first
+        512 rows of A -- the restatement the reference's CPU path is timed
+        as -- and, beside it, the numpy oracle on the same rows."""
+        import torch
+
         from oracle import restate as R
 
-        a = self.cpu_a.float().numpy()
-        b = self.cpu_b.float().numpy()
-        rate, reps = _time_cpu(lambda: R.matmul(a, b, out="bf16"), self.work)
-        return {"value": rate / 1e12, "unit": "TFLOP/s", "cores": _blas_threads(), "kind": "port",
-                "sample": f"oracle.restate.matmul on the full 4096^3 problem (f32 accumulate, bf16 out), "
-                          f"{reps} reps, {_cpu_model()}"}
+        rows = 512
+        a16, b16 = self.cpu_a[:rows].contiguous(), self.cpu_b
+        work = 2.0 * rows * 4096 * 4096
+        rate, reps, threads = _torch_cpu(lambda: torch.matmul(a16, b16), work)
+        a, b = a16.float().numpy(), b16.float().numpy()
+        with _blas_limited(threads):
+            o_rate, o_reps = _time_cpu(lambda: R.matmul(a, b, out="bf16"), work, budget_s=5.0)
+        return {"value": rate / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                "sample": f"torch.matmul bf16 on the CPU (oneDNN, f32 accumulate) of A[:{rows}] @ B, 4096 x 4096 "
+                          f"B, {reps} reps, {threads} threads, {_cpu_model()}",
+                "oracle": {"value": o_rate / 1e12, "unit": "TFLOP/s",
+                           "sample": f"oracle.restate.matmul (numpy f32 BLAS) on the same rows, {o_reps} reps"}}
 
 
 class Linear(Workload):
@@ -179,16 +217,26 @@ class Linear(Workload):
         return y
 
     def cpu_baseline(self) -> dict:
+        """torch's CPU bf16 F.linear + SiLU (oneDNN) on the first 256 of 8192
+        rows, and the numpy oracle on the same rows."""
+        import torch
+        import torch.nn.functional as F
+
         from oracle import restate as R
 
-        rows = 1024
-        x = self.cpu["x"][:rows].float().numpy()
-        w = self.cpu["w"].float().numpy()
-        b = self.cpu["b"].float().numpy()
+        rows = 256
+        x16, w16, b16 = self.cpu["x"][:rows].contiguous(), self.cpu["w"], self.cpu["b"]
         work = 2.0 * rows * 11008 * 4096
-        rate, reps = _time_cpu(lambda: R.matmul(x, w, False, True, b, act="silu", out="bf16"), work)
-        return {"value": rate / 1e12, "unit": "TFLOP/s", "cores": _blas_threads(), "kind": "port",
-                "sample": f"oracle.restate.matmul on the first {rows} of 8192 rows, {reps} reps, {_cpu_model()}"}
+        rate, reps, threads = _torch_cpu(lambda: F.silu(F.linear(x16, w16, b16).float()).to(torch.bfloat16), work)
+        x, w, b = x16.float().numpy(), w16.float().numpy(), b16.float().numpy()
+        with _blas_limited(threads):
+            o_rate, o_reps = _time_cpu(lambda: R.matmul(x, w, False, True, b, act="silu", out="bf16"), work,
+                                       budget_s=5.0)
+        return {"value": rate / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                "sample": f"torch F.linear bf16 + SiLU on the CPU (oneDNN) of the first {rows} of 8192 rows, "
+                          f"{reps} reps, {threads} threads, {_cpu_model()}",
+                "oracle": {"value": o_rate / 1e12, "unit": "TFLOP/s",
+                           "sample": f"oracle.restate.matmul (numpy) on the same rows, {o_reps} reps"}}
 
 
 class LinearDecode(Linear):
@@ -210,14 +258,15 @@ class LinearDecode(Linear):
         self.config = {"workload": self.description, "m": r, "n": 11008, "k": 4096, "seed": 3}
 
     def cpu_baseline(self) -> dict:
-        from oracle import restate as R
+        import torch
+        import torch.nn.functional as F
 
-        x = self.cpu["x"][: self.ROWS].float().numpy()
-        w = self.cpu["w"].float().numpy()
-        b = self.cpu["b"].float().numpy()
-        rate, reps = _time_cpu(lambda: R.matmul(x, w, False, True, b, act="silu", out="bf16"), self.work)
-        return {"value": rate / 1e9, "unit": "GB/s", "cores": _blas_threads(), "kind": "port",
-                "sample": f"oracle.restate.matmul on the whole {self.ROWS}-row problem, {reps} reps, {_cpu_model()}"}
+        x16, w16, b16 = self.cpu["x"][: self.ROWS].contiguous(), self.cpu["w"], self.cpu["b"]
+        rate, reps, threads = _torch_cpu(lambda: F.silu(F.linear(x16, w16, b16).float()).to(torch.bfloat16),
+                                         self.work)
+        return {"value": rate / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": f"torch F.linear bf16 + SiLU on the CPU (oneDNN) of the whole {self.ROWS}-row problem, "
+                          f"{reps} reps, {threads} threads, {_cpu_model()}"}
 
 
 class RowOp(Workload):
@@ -250,18 +299,37 @@ class RowOp(Workload):
         return self.U.rms_norm(self.x, self.w, self.eps)
 
     def cpu_baseline(self) -> dict:
+        """torch on the host (f32 inside, one rounding to the input dtype, as
+        the kernels compute) over the first 4096 rows, and the numpy oracle
+        on the same rows."""
+        import torch
+
         from oracle import restate as R
 
         rows = 4096
-        x = self.cpu["x"][:rows].float().numpy()
-        w = self.cpu["weight"].float().numpy()
-        out = self.dtype
-        fn = (lambda: R.softmax(x, out)) if self.op == "softmax" else (lambda: R.rms_norm(x, w, self.eps, out))
+        xt = self.cpu["x"][:rows].contiguous()
+        wt = self.cpu["weight"].float()
+        dtype, eps = xt.dtype, self.eps
+        if self.op == "softmax":
+            def fn():
+                return torch.softmax(xt.float(), -1).to(dtype)
+        else:
+            def fn():
+                xf = xt.float()
+                return (xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps) * wt).to(dtype)
         work = self.work * rows / self.x.shape[0]
-        rate, reps = _time_cpu(fn, work)
-        return {"value": rate / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-                "sample": f"oracle.restate.{self.op if self.op == 'softmax' else 'rms_norm'} on the first "
-                          f"{rows} of {self.x.shape[0]} rows, {reps} reps, {_cpu_model()}"}
+        rate, reps, threads = _torch_cpu(fn, work, budget_s=5.0)
+        x = xt.float().numpy()
+        w = wt.numpy()
+        out = self.dtype
+        ofn = (lambda: R.softmax(x, out)) if self.op == "softmax" else (lambda: R.rms_norm(x, w, eps, out))
+        o_rate, o_reps = _time_cpu(ofn, work, budget_s=3.0)
+        name = "softmax" if self.op == "softmax" else "rms_norm"
+        return {"value": rate / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": f"torch {name} on the CPU (f32 inside) of the first {rows} of {self.x.shape[0]} rows, "
+                          f"{reps} reps, {threads} threads, {_cpu_model()}",
+                "oracle": {"value": o_rate / 1e9, "unit": "GB/s", "cores": 1,
+                           "sample": f"oracle.restate.{name} (numpy, one thread) on the same rows, {o_reps} reps"}}
 
 
 class MemOp(Workload):
@@ -391,16 +459,31 @@ class Bmm(Workload):
         return self.U.bmm(self.a, self.b, out_dtype=torch.float32)
 
     def cpu_baseline(self) -> dict:
+        """torch.bmm on the CPU (f32 out) of 2 of the 16 batch slices, and the
+        numpy oracle's split-K bmm of one slice."""
+        import torch
+
         from oracle import restate as R
 
+        a2, b2 = self.cpu["a"][:2].contiguous(), self.cpu["b"][:2].contiguous()
+        if a2.dtype == torch.bfloat16:
+            def fn():
+                return torch.bmm(a2, b2).float()
+        else:
+            def fn():
+                return torch.bmm(a2, b2)
+        rate, reps, threads = _torch_cpu(fn, self.work / 8)
         a = self.cpu["a"][:1].float().numpy()
         b = self.cpu["b"][:1].float().numpy()
         s = self.plan["splits"]
-        work = self.work / 16
-        rate, reps = _time_cpu(lambda: R.split_k_bmm(a, b, s), work, max_reps=20)
+        with _blas_limited(threads):
+            o_rate, o_reps = _time_cpu(lambda: R.split_k_bmm(a, b, s), self.work / 16, budget_s=5.0, max_reps=20)
         scale = 1e12 if self.unit == "TFLOP/s" else 1e9
-        return {"value": rate / scale, "unit": self.unit, "cores": _blas_threads(), "kind": "port",
-                "sample": f"oracle.restate.split_k_bmm of 1 of 16 batch slices, S={s}, {reps} reps, {_cpu_model()}"}
+        return {"value": rate / scale, "unit": self.unit, "cores": threads, "kind": "port",
+                "sample": f"torch.bmm on the CPU of 2 of 16 batch slices, {reps} reps, {threads} threads, "
+                          f"{_cpu_model()}",
+                "oracle": {"value": o_rate / scale, "unit": self.unit,
+                           "sample": f"oracle.restate.split_k_bmm of 1 slice, S={s}, {o_reps} reps"}}
 
 
 class MatmulF32(Workload):
@@ -425,12 +508,20 @@ class MatmulF32(Workload):
         return self.U.matmul(self.a, self.b, block_sizes=[64, 64, 64])
 
     def cpu_baseline(self) -> dict:
+        import torch
+
         from oracle import restate as R
 
-        a, b = self.cpu["a"].numpy(), self.cpu["b"].numpy()
-        rate, reps = _time_cpu(lambda: R.matmul(a, b), self.work, budget_s=5.0, max_reps=2000)
-        return {"value": rate / 1e12, "unit": "TFLOP/s", "cores": _blas_threads(), "kind": "port",
-                "sample": f"oracle.restate.matmul 512^3 f32, {reps} reps, {_cpu_model()}"}
+        at, bt = self.cpu["a"], self.cpu["b"]
+        torch.set_num_threads(_cpu_cores())
+        rate, reps = _time_cpu(lambda: torch.matmul(at, bt), self.work, budget_s=5.0, max_reps=2000)
+        a, b = at.numpy(), bt.numpy()
+        with _blas_limited(_cpu_cores()):
+            o_rate, o_reps = _time_cpu(lambda: R.matmul(a, b), self.work, budget_s=3.0, max_reps=2000)
+        return {"value": rate / 1e12, "unit": "TFLOP/s", "cores": _cpu_cores(), "kind": "port",
+                "sample": f"torch.matmul 512^3 f32 on the CPU, {reps} reps, {_cpu_cores()} threads, {_cpu_model()}",
+                "oracle": {"value": o_rate / 1e12, "unit": "TFLOP/s",
+                           "sample": f"oracle.restate.matmul 512^3 f32 (numpy), {o_reps} reps"}}
 
 
 class Copy(Workload):
@@ -638,6 +729,8 @@ def main() -> int:
                 "config": cw.config,
             }
             print(f"bench: {name} {r['ms']:.4f} ms/step {r['value']:.1f} GB/s", file=sys.stderr, flush=True)
+            if not args.no_cpu_baseline:
+                components[name + "_bf16"]["cpu_baseline"] = cw.cpu_baseline()
             del cw
         line["components"] = components
     if not args.no_cpu_baseline:
