@@ -54,6 +54,28 @@ int set_error(int status, const char* fmt, ...) {
 
 void clear_error() { g_error[0] = 0; }
 
+int check_epilogue(const char* what, int code, const hmx_program* program, hmx_program* out) {
+  *out = hmx_program{};
+  if (!valid_activation(code)) return set_error(HMX_ERR_INVALID, "%s: unknown epilogue %d", what, code);
+  if (code != HMX_EPI_PROGRAM) return HMX_OK;
+  if (program == nullptr) return set_error(HMX_ERR_INVALID, "%s: epilogue program is null", what);
+  if (program->count < 1 || program->count > HMX_PROGRAM_MAX)
+    return set_error(HMX_ERR_INVALID, "%s: epilogue program of %d instructions (1..%d)", what, program->count,
+                     HMX_PROGRAM_MAX);
+  if (program->result < 0 || program->result >= HMX_PROGRAM_REGS)
+    return set_error(HMX_ERR_INVALID, "%s: epilogue program result register %d", what, program->result);
+  for (int i = 0; i < program->count; ++i) {
+    const hmx_instr& in = program->code[i];
+    if (in.op >= HMX_OP_COUNT)
+      return set_error(HMX_ERR_INVALID, "%s: epilogue program instruction %d: unknown opcode %d", what, i, in.op);
+    if (in.dst >= HMX_PROGRAM_REGS || in.a >= HMX_PROGRAM_REGS || in.b >= HMX_PROGRAM_REGS)
+      return set_error(HMX_ERR_INVALID, "%s: epilogue program instruction %d: register past %d", what, i,
+                       HMX_PROGRAM_REGS - 1);
+  }
+  *out = *program;
+  return HMX_OK;
+}
+
 int check_launch(const char* what) {
   hipError_t err = hipGetLastError();
   if (err != hipSuccess)

@@ -138,4 +138,116 @@ __device__ __forceinline__ float apply_activation(int code, float x, float arg) 
   }
 }
 
+// max / min that return NaN when either operand is NaN (torch.maximum /
+// torch.minimum / clamp), unlike fmaxf / fminf.
+__device__ __forceinline__ float max_nan(float a, float b) {
+  return (a != a || b != b) ? a + b : fmaxf(a, b);
+}
+__device__ __forceinline__ float min_nan(float a, float b) {
+  return (a != a || b != b) ? a + b : fminf(a, b);
+}
+
+// One instruction of an epilogue program (hmx_program): the f32 result of
+// op on registers a, b and the constants. The formulas are the ones torch
+// evaluates for the same operation on f32 tensors.
+__device__ __forceinline__ float program_op(int op, float a, float b, float c0, float c1) {
+  switch (op) {
+    case HMX_OP_COPY: return a;
+    case HMX_OP_NEG: return -a;
+    case HMX_OP_ABS: return fabsf(a);
+    case HMX_OP_RELU: return a > 0.f ? a : (a != a ? a : 0.f);
+    case HMX_OP_SIGMOID: return 1.f / (1.f + expf(-a));
+    case HMX_OP_TANH: return tanhf(a);
+    case HMX_OP_SILU: return a / (1.f + expf(-a));
+    case HMX_OP_GELU: return a * 0.5f * (1.f + erff(a * 0.7071067811865476f));
+    case HMX_OP_GELU_TANH: {
+      const float inner = 0.7978845608028654f * (a + 0.044715f * a * a * a);
+      return 0.5f * a * (1.f + tanhf(inner));
+    }
+    case HMX_OP_EXP: return expf(a);
+    case HMX_OP_LOG: return logf(a);
+    case HMX_OP_SQRT: return sqrtf(a);
+    case HMX_OP_RSQRT: return 1.f / sqrtf(a);
+    case HMX_OP_RECIP: return 1.f / a;
+    case HMX_OP_ERF: return erff(a);
+    case HMX_OP_SIN: return sinf(a);
+    case HMX_OP_COS: return cosf(a);
+    case HMX_OP_LOG1P: return log1pf(a);
+    case HMX_OP_EXPM1: return expm1f(a);
+    case HMX_OP_FLOOR: return floorf(a);
+    case HMX_OP_CEIL: return ceilf(a);
+    case HMX_OP_TRUNC: return truncf(a);
+    case HMX_OP_ROUND: return rintf(a);
+    case HMX_OP_SOFTPLUS: return a * c0 > c1 ? a : log1pf(expf(a * c0)) / c0;
+    case HMX_OP_MISH: return a * tanhf(log1pf(expf(a)));
+    case HMX_OP_HARDSWISH: return a * min_nan(max_nan(a + 3.f, 0.f), 6.f) / 6.f;
+    case HMX_OP_HARDSIGMOID: return min_nan(max_nan(a + 3.f, 0.f), 6.f) / 6.f;
+    case HMX_OP_ELU: return a <= 0.f ? expm1f(a) * (c0 * c1) : a * c1;
+    case HMX_OP_LEAKY_RELU: return a > 0.f ? a : a * c0;
+    case HMX_OP_CLAMP: return min_nan(max_nan(a, c0), c1);
+    case HMX_OP_ADD_C: return a + c0;
+    case HMX_OP_MUL_C: return a * c0;
+    case HMX_OP_DIV_C: return a / c0;
+    case HMX_OP_RSUB_C: return c0 - a;
+    case HMX_OP_RDIV_C: return c0 / a;
+    case HMX_OP_POW_C: return powf(a, c0);
+    case HMX_OP_ADD: return a + b;
+    case HMX_OP_SUB: return a - b;
+    case HMX_OP_MUL: return a * b;
+    case HMX_OP_DIV: return a / b;
+    case HMX_OP_MAX: return max_nan(a, b);
+    case HMX_OP_MIN: return min_nan(a, b);
+    case HMX_OP_POW: return powf(a, b);
+    default: return a;
+  }
+}
+
+// Register i of a program's register file. The index is uniform across the
+// wave (it comes from the program), so a chain of selects reads it without
+// dynamic indexing of private memory.
+__device__ __forceinline__ float program_reg(const float (&r)[HMX_PROGRAM_REGS], int i) {
+  float v = r[0];
+#pragma unroll
+  for (int j = 1; j < HMX_PROGRAM_REGS; ++j) v = i == j ? r[j] : v;
+  return v;
+}
+
+// Runs program `p` on the value x (register 0) and extra (register 1).
+__device__ __forceinline__ float run_program(const hmx_program& p, float x, float extra) {
+  float r[HMX_PROGRAM_REGS];
+  r[0] = x;
+  r[1] = extra;
+#pragma unroll
+  for (int j = 2; j < HMX_PROGRAM_REGS; ++j) r[j] = 0.f;
+#pragma unroll 1
+  for (int i = 0; i < p.count; ++i) {
+    const hmx_instr ins = p.code[i];
+    const float y = program_op(ins.op, program_reg(r, ins.a), program_reg(r, ins.b), ins.c0, ins.c1);
+#pragma unroll
+    for (int j = 0; j < HMX_PROGRAM_REGS; ++j) r[j] = ins.dst == j ? y : r[j];
+  }
+  return program_reg(r, p.result);
+}
+
+// Applies the epilogue (activation code or program) to n values in place,
+// one value per pass of a loop that is not unrolled: the values rotate
+// through v[0], so the program's code is emitted once however large n is.
+template <int N>
+__device__ __forceinline__ void run_program_n(const hmx_program& p, float (&v)[N], const float (&extra)[N]) {
+  float e[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) e[i] = extra[i];
+#pragma unroll 1
+  for (int t = 0; t < N; ++t) {
+    const float y = run_program(p, v[0], e[0]);
+#pragma unroll
+    for (int i = 0; i + 1 < N; ++i) {
+      v[i] = v[i + 1];
+      e[i] = e[i + 1];
+    }
+    v[N - 1] = y;
+    e[N - 1] = 0.f;
+  }
+}
+
 }  // namespace hmx

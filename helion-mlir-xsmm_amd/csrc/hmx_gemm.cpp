@@ -153,9 +153,10 @@ bool skinny_shape(int ab_dtype, int64_t m, int64_t k, int64_t batch, int trans_a
 // takes that tile, and the split count is rounded the same way both times.
 int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int trans_a,
               int b_layout, int splits, int64_t max_ws, int tile_m, int tile_n, int tile_k,
-              int cus, Plan& plan) {
+              int cus, bool program, Plan& plan) {
   const bool bf16 = ab_dtype == HMX_DTYPE_BF16;
-  plan.skinny = skinny_shape(ab_dtype, m, k, batch, trans_a, b_layout, splits, tile_m, tile_n, tile_k);
+  plan.skinny = !program &&
+                skinny_shape(ab_dtype, m, k, batch, trans_a, b_layout, splits, tile_m, tile_n, tile_k);
   if (plan.skinny) {
     plan.tile = kSkinny;
     plan.splits = 1;
@@ -227,7 +228,11 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
     plan.k_chunk = k;
   }
   plan.splits = splits;
-  const int64_t partial_bytes = splits > 1 ? (int64_t)splits * batch * m * n * 4 : 0;
+  // An epilogue program runs fused in the direct-to-LDS kernels; the others
+  // write f32 products to the workspace (as one split) for the split-K
+  // reduction to finish, so its plan holds those partials even unsplit.
+  const int64_t partial_bytes =
+      splits > 1 || program ? (int64_t)std::max(splits, 1) * batch * m * n * 4 : 0;
   plan.bt_bytes = ceil_div(n * k * 2, 256) * 256;
   // The direct-to-LDS kernels read row-major B in place (256 x 256 tiles,
   // ragged M and N too, or transposed A on whole tiles; 128 x 128 tiles of
@@ -275,14 +280,53 @@ int64_t whole_round_columns(int64_t tiles_m, int64_t tiles_n, int cus) {
   return (tiles - tail) / tiles_m;
 }
 
-// The direct-to-LDS kernel finishes C with the register epilogue only:
-// identity, ReLU or SiLU, and 4-byte aligned column pairs for bf16 C.
+// The direct-to-LDS kernels finish C from registers for identity, ReLU and
+// SiLU, which store bf16 C as 4-byte aligned column pairs; every other
+// activation and epilogue programs go through their LDS-staged epilogue,
+// which takes any alignment.
 bool dma_direct_ok(const GemmArgs& g) {
-  const bool act_ok = g.act == HMX_EPI_IDENTITY || g.act == HMX_EPI_RELU || g.act == HMX_EPI_SILU;
+  const bool direct = g.act == HMX_EPI_IDENTITY || g.act == HMX_EPI_RELU || g.act == HMX_EPI_SILU;
   const bool pair_ok = g.c_dtype != HMX_DTYPE_BF16 ||
                        (g.ldc % 2 == 0 && g.stride_c % 2 == 0 && g.stride_split % 2 == 0 &&
                         (((uintptr_t)g.c) & 3) == 0);
-  return act_ok && pair_ok && g.k_chunk % 32 == 0 && g.k > 0;
+  return (!direct || pair_ok) && g.k_chunk % 32 == 0 && g.k > 0;
+}
+
+// The kernel families a launch can take.
+enum class Kernel { SKINNY, SKINNY_TILES, DMA, DMA_TA, DMA128, BF16, F32_DMA, F32 };
+
+// Whether a family runs epilogue programs fused (the direct-to-LDS bf16
+// kernels, through their LDS-staged epilogue); the others leave them to the
+// split-K reduction.
+bool runs_programs(Kernel kind) {
+  return kind == Kernel::DMA || kind == Kernel::DMA_TA || kind == Kernel::DMA128;
+}
+
+// The kernel family for the arguments `g` of a planned launch: the
+// direct-to-LDS kernels wherever their shape, layout and alignment rules
+// hold (HMX_GEMM_DMA=0 turns them off, for comparison), else the
+// register-staged kernels.
+Kernel select_kernel(const GemmArgs& g, const Plan& plan, int ab_dtype, int la, int lb, bool whole,
+                     bool bytes_ok) {
+  const bool aligned = g.a.vec && g.b.vec && bytes_ok;
+  const bool plain_b = lb == L_KCONTIG || lb == L_RCONTIG;
+  if (plan.skinny) return aligned && dma_enabled() ? Kernel::SKINNY : Kernel::SKINNY_TILES;
+  if (ab_dtype == HMX_DTYPE_BF16) {
+    const TileChoice t = plan.tile;
+    const bool k64 = g.k % 64 == 0 && plan.k_chunk % 64 == 0;
+    // Whole 256 x 256 tiles, or ragged M and N with K chunks of whole
+    // 64-element stages and B K-contiguous or row-major.
+    const bool dma_shape = aligned && (whole || (plain_b && k64));
+    const bool ok = dma_direct_ok(g) && dma_enabled();
+    if (t.bm == 256 && dma_shape && la == L_KCONTIG && (plain_b || gemm_bf16_dma_packed_ok(g, lb)) && ok)
+      return Kernel::DMA;
+    if (t.bm == 256 && la == L_RCONTIG && whole && aligned && plain_b && ok) return Kernel::DMA_TA;
+    if (t.bm == 128 && la == L_KCONTIG && plain_b && aligned && k64 && ok) return Kernel::DMA128;
+    return Kernel::BF16;
+  }
+  const bool guard = !(whole && aligned);
+  if (plan.tile.bm == 256 && !guard && plain_b && g.k_chunk % 32 == 0 && dma_enabled()) return Kernel::F32_DMA;
+  return Kernel::F32;
 }
 
 // hmx_gemm and hmx_gemm_noalloc: checks, plan, launches. The workspace is
@@ -296,12 +340,15 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
               void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int64_t batch,
               int64_t stride_a, int64_t stride_b, int64_t stride_c, const void* bias,
               const void* scale, const void* shift, int vec_dtype, int epilogue,
-              float epilogue_arg, int splits, void* workspace, int64_t workspace_bytes,
-              bool use_scratch, int tile_m, int tile_n, int tile_k, void* stream) {
+              float epilogue_arg, const hmx_program* program, int splits, void* workspace,
+              int64_t workspace_bytes, bool use_scratch, int tile_m, int tile_n, int tile_k,
+              void* stream) {
   HMX_REQUIRE(valid_dtype(ab_dtype) && valid_dtype(c_dtype), "gemm: unknown dtype");
   HMX_REQUIRE((bias == nullptr && scale == nullptr && shift == nullptr) || valid_dtype(vec_dtype),
               "gemm: unknown vector dtype %d", vec_dtype);
-  HMX_REQUIRE(valid_activation(epilogue), "gemm: unknown epilogue %d", epilogue);
+  hmx_program prog;
+  const int pst = check_epilogue("gemm", epilogue, program, &prog);
+  if (pst != HMX_OK) return pst;
   const int lb = layout_code(b_layout);
   HMX_REQUIRE(lb >= 0, "gemm: unknown B layout %d", b_layout);
   HMX_REQUIRE(ab_dtype == HMX_DTYPE_BF16 || lb == L_KCONTIG || lb == L_RCONTIG ||
@@ -331,9 +378,10 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
 
   const DeviceShape dev = current_device_shape();
   Plan plan;
+  const bool program_epi = epilogue == HMX_EPI_PROGRAM;
   make_plan(ab_dtype, m, n, k, batch, trans_a, b_layout, splits,
             use_scratch ? kScratchBytes : (workspace ? workspace_bytes : 0), tile_m, tile_n, tile_k, dev.cus,
-            plan);
+            program_epi, plan);
   if (use_scratch) {
     HMX_REQUIRE(plan.workspace_bytes <= kScratchBytes,
                 "gemm_noalloc: the launch needs %lld bytes of workspace and the library's scratch holds "
@@ -345,10 +393,11 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
       workspace_bytes = kScratchBytes;
     }
   }
-  if (plan.splits > 1) {
+  if (plan.splits > 1 || program_epi) {
     HMX_REQUIRE(workspace != nullptr && workspace_bytes >= plan.workspace_bytes,
-                "gemm: split-K needs %lld workspace bytes, got %lld",
-                (long long)plan.workspace_bytes, (long long)workspace_bytes);
+                "gemm: %s needs %lld workspace bytes, got %lld",
+                plan.splits > 1 ? "split-K" : "an epilogue program", (long long)plan.workspace_bytes,
+                (long long)workspace_bytes);
   }
   void* partials = workspace ? (char*)workspace + plan.bt_bytes : nullptr;
   int lb_run = lb;
@@ -404,7 +453,22 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
   g.vec_dtype = vec_dtype;
   g.act = epilogue;
   g.act_arg = epilogue_arg;
-  if (plan.splits > 1) {
+  g.prog = prog;
+  g.c = c;
+  g.c_dtype = c_dtype;
+  g.ldc = ldc;
+  g.stride_c = stride_c;
+  g.stride_split = 0;
+
+  const bool whole = m % plan.tile.bm == 0 && n % plan.tile.bn == 0 &&
+                     plan.k_chunk % plan.tile.bk == 0 && k % plan.tile.bk == 0;
+  const bool guard = !(whole && g.a.vec && g.b.vec && bytes_ok);
+  Kernel kind = select_kernel(g, plan, ab_dtype, la, lb_run, whole, bytes_ok);
+  // Split-K, and epilogue programs on kernels that do not run them fused:
+  // the GEMM writes f32 partials ([splits, batch, M, N]) with the identity
+  // epilogue, and the reduction applies bias, scale, shift and the epilogue.
+  const bool staged = plan.splits > 1 || (program_epi && !runs_programs(kind));
+  if (staged) {
     // Split-K grids of one tile per batch slice share no operand data between
     // workgroups: each walks its K chunk from a stage of its own, so the
     // workgroups in flight read different K positions of their rows (bf16 bmm
@@ -417,7 +481,7 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
       const char* e = getenv("HMX_GEMM_STAGGER");
       return !(e && e[0] == '0');
     }();
-    g.k_stagger = stagger && tiles_m * tiles_n == 1;
+    g.k_stagger = stagger && plan.splits > 1 && tiles_m * tiles_n == 1;
     g.c = partials;
     g.c_dtype = HMX_DTYPE_F32;
     g.ldc = n;
@@ -425,41 +489,24 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
     g.stride_split = batch * m * n;
     g.bias = g.scale = g.shift = nullptr;
     g.act = HMX_EPI_IDENTITY;
-  } else {
-    g.c = c;
-    g.c_dtype = c_dtype;
-    g.ldc = ldc;
-    g.stride_c = stride_c;
-    g.stride_split = 0;
+    kind = select_kernel(g, plan, ab_dtype, la, lb_run, whole, bytes_ok);
   }
 
-  const bool whole = m % plan.tile.bm == 0 && n % plan.tile.bn == 0 &&
-                     plan.k_chunk % plan.tile.bk == 0 && k % plan.tile.bk == 0;
-  const bool guard = !(whole && g.a.vec && g.b.vec && bytes_ok);
   const dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)plan.splits, (unsigned)batch);
   auto s = (hipStream_t)stream;
-  if (plan.skinny) {
-    // The skinny kernel's loads need the aligned, 2^31-bounded operands of
-    // the direct-to-LDS kernels; otherwise the register-staged kernel runs
-    // the same product on one 128 x 128 tile row.
-    if (g.a.vec && g.b.vec && bytes_ok && dma_enabled()) {
+  switch (kind) {
+    case Kernel::SKINNY:
       launch_gemm_bf16_skinny(g, s);
-    } else {
+      break;
+    case Kernel::SKINNY_TILES:
+      // The skinny kernel's loads need the aligned, 2^31-bounded operands of
+      // the direct-to-LDS kernels; otherwise the register-staged kernel runs
+      // the same product on one 128 x 128 tile row.
       g.tiles_m = 1;
       g.tiles_n = (int)ceil_div(n, 128);
       launch_gemm_bf16(g, 128, la, lb_run, true, dim3((unsigned)g.tiles_n, 1, 1), s);
-    }
-  } else if (ab_dtype == HMX_DTYPE_BF16) {
-    const TileChoice t = plan.tile;
-    // The direct-to-LDS kernels: row-major A, 16-byte aligned operands whose
-    // spans fit buffer loads, whole 256 x 256 tiles, or ragged M and N with K
-    // chunks of whole 64-element stages and B K-contiguous or row-major.
-    const bool dma_shape = g.a.vec && g.b.vec && bytes_ok &&
-                           (whole || ((lb_run == L_KCONTIG || lb_run == L_RCONTIG) && k % 64 == 0 &&
-                                      plan.k_chunk % 64 == 0));
-    if (t.bm == 256 && dma_shape && la == L_KCONTIG &&
-        (lb_run == L_KCONTIG || lb_run == L_RCONTIG || gemm_bf16_dma_packed_ok(g, lb_run)) &&
-        dma_direct_ok(g) && dma_enabled()) {
+      break;
+    case Kernel::DMA: {
       const int64_t n1 = whole && (lb_run == L_KCONTIG || lb_run == L_RCONTIG) && plan.splits == 1 &&
                                  batch == 1 && g.k_chunk % 64 == 0
                              ? whole_round_columns(tiles_m, tiles_n, dev.cus)
@@ -487,28 +534,31 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
       } else {
         launch_gemm_bf16_dma(g, lb_run, grid, s);
       }
-    } else if (t.bm == 256 && la == L_RCONTIG && whole && g.a.vec && g.b.vec && bytes_ok &&
-               (lb_run == L_KCONTIG || lb_run == L_RCONTIG) && dma_direct_ok(g) && dma_enabled()) {
+      break;
+    }
+    case Kernel::DMA_TA:
       launch_gemm_bf16_dma_ta(g, lb_run, grid, s);
-    } else if (t.bm == 128 && la == L_KCONTIG && (lb_run == L_KCONTIG || lb_run == L_RCONTIG) && g.a.vec &&
-               g.b.vec && bytes_ok && k % 64 == 0 && plan.k_chunk % 64 == 0 && dma_direct_ok(g) && dma_enabled()) {
+      break;
+    case Kernel::DMA128:
       launch_gemm_bf16_dma128(g, lb_run, grid, s);
-    } else
-      launch_gemm_bf16(g, t.bm, la, lb_run, guard, grid, s);
-  } else {
-    // The 256 x 256 f32 tile is planned only for row-major A, B [N, K] or
-    // [K, N] and two or more splits: its kernel writes f32 partials with the
-    // identity epilogue.
-    if (plan.tile.bm == 256 && (plan.splits < 2 || la != L_KCONTIG))
-      return set_error(HMX_ERR_INVALID, "gemm: internal f32 plan without split-K");
-    if (plan.tile.bm == 256 && !guard && (lb == L_KCONTIG || lb == L_RCONTIG) &&
-        g.k_chunk % 32 == 0 && dma_enabled())
+      break;
+    case Kernel::BF16:
+      launch_gemm_bf16(g, plan.tile.bm, la, lb_run, guard, grid, s);
+      break;
+    case Kernel::F32_DMA:
       launch_gemm_f32_dma(g, lb, grid, s);
-    else
+      break;
+    case Kernel::F32:
+      // The 256 x 256 f32 tile is planned only for row-major A, B [N, K] or
+      // [K, N] and two or more splits: its kernel writes f32 partials with the
+      // identity epilogue.
+      if (plan.tile.bm == 256 && (plan.splits < 2 || la != L_KCONTIG))
+        return set_error(HMX_ERR_INVALID, "gemm: internal f32 plan without split-K");
       launch_gemm_f32(g, plan.tile.bm, la, lb, guard, grid, s);
+      break;
   }
   int st = check_launch("gemm");
-  if (st != HMX_OK || plan.splits <= 1) return st;
+  if (st != HMX_OK || !staged) return st;
 
   GemmArgs r = g;
   r.c = c;
@@ -535,8 +585,8 @@ extern "C" {
 
 int hmx_gemm_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int trans_a,
                   int b_layout, int splits, int64_t max_workspace_bytes, int tile_m,
-                  int tile_n, int tile_k, int compute_units, int* out_splits, int* out_tile_m,
-                  int* out_tile_n, int* out_tile_k, int64_t* out_workspace_bytes) {
+                  int tile_n, int tile_k, int compute_units, int epilogue, int* out_splits,
+                  int* out_tile_m, int* out_tile_n, int* out_tile_k, int64_t* out_workspace_bytes) {
   HMX_REQUIRE(valid_dtype(ab_dtype), "gemm_plan: unknown dtype %d", ab_dtype);
   HMX_REQUIRE(layout_code(b_layout) >= 0, "gemm_plan: unknown B layout %d", b_layout);
   HMX_REQUIRE(m >= 0 && n >= 0 && k >= 0 && batch >= 1, "gemm_plan: invalid shape");
@@ -544,8 +594,9 @@ int hmx_gemm_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, 
   HMX_REQUIRE(compute_units >= 0 && compute_units < 65536, "gemm_plan: invalid CU count %d", compute_units);
   const int cus = compute_units > 0 ? compute_units : current_device_shape().cus;
   Plan plan;
+  HMX_REQUIRE(valid_activation(epilogue), "gemm_plan: unknown epilogue %d", epilogue);
   int st = make_plan(ab_dtype, m, n, k, batch, trans_a, b_layout, splits, max_workspace_bytes, tile_m,
-                     tile_n, tile_k, cus, plan);
+                     tile_n, tile_k, cus, epilogue == HMX_EPI_PROGRAM, plan);
   if (st != HMX_OK) return st;
   if (out_splits) *out_splits = plan.splits;
   if (out_tile_m) *out_tile_m = plan.tile.bm;
@@ -560,11 +611,12 @@ int hmx_gemm(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
              void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int64_t batch,
              int64_t stride_a, int64_t stride_b, int64_t stride_c, const void* bias,
              const void* scale, const void* shift, int vec_dtype, int epilogue,
-             float epilogue_arg, int splits, void* workspace, int64_t workspace_bytes,
-             int tile_m, int tile_n, int tile_k, void* stream) {
+             float epilogue_arg, const hmx_program* program, int splits, void* workspace,
+             int64_t workspace_bytes, int tile_m, int tile_n, int tile_k, void* stream) {
   return gemm_impl(ab_dtype, c_dtype, a, lda, trans_a, b, ldb, b_layout, b_panel, b_kpad, c, ldc, m, n, k,
                    batch, stride_a, stride_b, stride_c, bias, scale, shift, vec_dtype, epilogue,
-                   epilogue_arg, splits, workspace, workspace_bytes, false, tile_m, tile_n, tile_k, stream);
+                   epilogue_arg, program, splits, workspace, workspace_bytes, false, tile_m, tile_n, tile_k,
+                   stream);
 }
 
 int hmx_gemm_noalloc(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
@@ -572,11 +624,11 @@ int hmx_gemm_noalloc(int ab_dtype, int c_dtype, const void* a, int64_t lda, int 
                      void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int64_t batch,
                      int64_t stride_a, int64_t stride_b, int64_t stride_c, const void* bias,
                      const void* scale, const void* shift, int vec_dtype, int epilogue,
-                     float epilogue_arg, int splits, int tile_m, int tile_n, int tile_k,
-                     void* stream) {
+                     float epilogue_arg, const hmx_program* program, int splits, int tile_m,
+                     int tile_n, int tile_k, void* stream) {
   return gemm_impl(ab_dtype, c_dtype, a, lda, trans_a, b, ldb, b_layout, b_panel, b_kpad, c, ldc, m, n, k,
                    batch, stride_a, stride_b, stride_c, bias, scale, shift, vec_dtype, epilogue,
-                   epilogue_arg, splits, nullptr, 0, true, tile_m, tile_n, tile_k, stream);
+                   epilogue_arg, program, splits, nullptr, 0, true, tile_m, tile_n, tile_k, stream);
 }
 
 }  // extern "C"

@@ -98,6 +98,9 @@ struct GemmArgs {
   // The device's compute units and XCDs (workgroups are dealt to the XCDs
   // in turn; each XCD has its own L2).
   int cus, xcds;
+  // act == HMX_EPI_PROGRAM: the epilogue program (last: the kernels that do
+  // not run programs never read it).
+  hmx_program prog;
 };
 
 // blockIdx.x -> (tile_m, tile_n). Consecutive workgroups are dealt to the
@@ -127,6 +130,22 @@ __device__ __forceinline__ void column_vectors(const GemmArgs& g, int64_t col, b
 }
 
 
+// The epilogue's activation on N values in place: a named code, or with
+// PROG (kernels instantiated for epilogue programs only, so the others do not
+// carry the interpreter's registers) the program.
+template <int N, bool PROG>
+__device__ __forceinline__ void activate_all(const GemmArgs& g, float (&v)[N]) {
+  if (PROG && g.act == HMX_EPI_PROGRAM) {
+    float none[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) none[i] = 0.f;
+    run_program_n<N>(g.prog, v, none);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = apply_activation(g.act, v[i], g.act_arg);
+  }
+}
+
 // Epilogue, staged through LDS (free once the K loop is done). Each wave owns
 // a region of 32 x (WN + 8) f32; for each of its FM fragment rows it writes
 // the accumulators there (element e of lane l of a 32 x 32 fragment is row
@@ -136,8 +155,9 @@ __device__ __forceinline__ void column_vectors(const GemmArgs& g, int64_t col, b
 template <int WN>
 constexpr int epi_pitch() { return WN + 8; }
 
-// Activation classes compiled into the register epilogue.
-enum : int { ACT_ID = 0, ACT_RELU = 1, ACT_SILU = 2 };
+// Activation classes compiled into the register epilogue. ACT_ANY: any
+// code or program, finished by the LDS-staged epilogue.
+enum : int { ACT_ID = 0, ACT_RELU = 1, ACT_SILU = 2, ACT_ANY = 3 };
 
 template <int ACT>
 __device__ __forceinline__ float activate(float v) {
@@ -222,7 +242,7 @@ __device__ __forceinline__ void epilogue_direct(const GemmArgs& g, int split, in
   }
 }
 
-template <int FM, int FN, int WM, int WN, bool GUARD>
+template <int FM, int FN, int WM, int WN, bool GUARD, bool PROG = false>
 __device__ __forceinline__ void epilogue_staged(const GemmArgs& g, float* lds, int split, int batch,
                                          int64_t m0, int64_t n0, int wm, int wn, int wave,
                                          int lane, const f32x16_t (&acc)[FM][FN]) {
@@ -253,8 +273,9 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& g, float* lds, i
         const bool in = !GUARD || col + t < g.n;
         float bias, scale, shift;
         column_vectors(g, col + t, in, bias, scale, shift);
-        v[t] = apply_activation(g.act, (v[t] + bias) * scale + shift, g.act_arg);
+        v[t] = (v[t] + bias) * scale + shift;
       }
+      activate_all<4, PROG>(g, v);
       const int64_t o = off + row * g.ldc + col;
       if ((!GUARD || col + 4 <= g.n) && vec_ok) {
         if (bf16)

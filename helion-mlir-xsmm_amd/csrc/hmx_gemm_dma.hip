@@ -226,7 +226,15 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(GemmArgs g) {
     __builtin_amdgcn_sched_barrier(0);
   }
   wait_vmem<0>();  // no load into LDS outlives the loop
-  epilogue_direct<FM, FN, WM, WN, false, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
+  if constexpr (ACT == ACT_ANY) {
+    // Any other activation or a program: through LDS, once every wave is
+    // done reading its last stage.
+    static_assert(4 * 32 * epi_pitch<WN>() * 4 <= S * STAGE, "staged epilogue fits the stages");
+    __syncthreads();
+    epilogue_staged<FM, FN, WM, WN, false, true>(g, (float*)lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
+  } else {
+    epilogue_direct<FM, FN, WM, WN, false, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -561,10 +569,21 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
   }
   wait_vmem<0>();  // no load into LDS outlives the loop
   // RAGGED: tiles that cross M or N store element by element, guarded.
-  if (!RAGGED || (m0 + BM <= g.m && n0 + BN <= g.n))
-    epilogue_direct<FM, FN, WM, WN, false, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
-  else
-    epilogue_direct<FM, FN, WM, WN, true, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
+  if constexpr (ACT == ACT_ANY) {
+    // Any other activation or a program: through LDS, once every wave is
+    // done reading its last stage.
+    static_assert(NW * 32 * epi_pitch<WN>() * 4 <= 2 * STAGE, "staged epilogue fits the stages");
+    __syncthreads();
+    if (!RAGGED || (m0 + BM <= g.m && n0 + BN <= g.n))
+      epilogue_staged<FM, FN, WM, WN, false, true>(g, (float*)lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
+    else
+      epilogue_staged<FM, FN, WM, WN, true, true>(g, (float*)lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
+  } else {
+    if (!RAGGED || (m0 + BM <= g.m && n0 + BN <= g.n))
+      epilogue_direct<FM, FN, WM, WN, false, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
+    else
+      epilogue_direct<FM, FN, WM, WN, true, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -937,13 +956,15 @@ void launch_bf16_dma_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
     switch (g.act) {
       case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, NW, 256>, grid, NW * 64, s, g); break;
       case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, NW, 256>, grid, NW * 64, s, g); break;
-      default: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, NW, 256>, grid, NW * 64, s, g); break;
+      case HMX_EPI_IDENTITY: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, NW, 256>, grid, NW * 64, s, g); break;
+      default: launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, NW, 256>, grid, NW * 64, s, g); break;
     }
   } else if constexpr (LB != L_VNNI_PANELS) {
     switch (g.act) {
       case HMX_EPI_RELU: launch(gemm_bf16_dma_kernel<LB, ACT_RELU, BF16>, grid, 256, s, g); break;
       case HMX_EPI_SILU: launch(gemm_bf16_dma_kernel<LB, ACT_SILU, BF16>, grid, 256, s, g); break;
-      default: launch(gemm_bf16_dma_kernel<LB, ACT_ID, BF16>, grid, 256, s, g); break;
+      case HMX_EPI_IDENTITY: launch(gemm_bf16_dma_kernel<LB, ACT_ID, BF16>, grid, 256, s, g); break;
+      default: launch(gemm_bf16_dma_kernel<LB, ACT_ANY, BF16>, grid, 256, s, g); break;
     }
   }
 }
@@ -997,7 +1018,8 @@ void launch_bf16_dma_narrow(const GemmArgs& g, dim3 grid, hipStream_t s) {
   switch (g.act) {
     case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 4, 128>, grid, 256, s, g); break;
     case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 4, 128>, grid, 256, s, g); break;
-    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 4, 128>, grid, 256, s, g); break;
+    case HMX_EPI_IDENTITY: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 4, 128>, grid, 256, s, g); break;
+    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, 4, 128>, grid, 256, s, g); break;
   }
 }
 
@@ -1020,7 +1042,8 @@ void launch_bf16_dma_ragged(const GemmArgs& g, dim3 grid, hipStream_t s) {
   switch (g.act) {
     case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 8, 256, true>, grid, 512, s, g); break;
     case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 8, 256, true>, grid, 512, s, g); break;
-    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 8, 256, true>, grid, 512, s, g); break;
+    case HMX_EPI_IDENTITY: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 8, 256, true>, grid, 512, s, g); break;
+    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, 8, 256, true>, grid, 512, s, g); break;
   }
 }
 
@@ -1031,7 +1054,8 @@ void launch_bf16_dma128_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
   switch (g.act) {
     case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
     case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
-    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
+    case HMX_EPI_IDENTITY: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
+    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
   }
 }
 
@@ -1062,7 +1086,8 @@ void launch_bf16_dma_ta_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
   switch (g.act) {
     case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 8, 256, false, 256, true>, grid, 512, s, g); break;
     case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 8, 256, false, 256, true>, grid, 512, s, g); break;
-    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 8, 256, false, 256, true>, grid, 512, s, g); break;
+    case HMX_EPI_IDENTITY: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 8, 256, false, 256, true>, grid, 512, s, g); break;
+    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, 8, 256, false, 256, true>, grid, 512, s, g); break;
   }
 }
 

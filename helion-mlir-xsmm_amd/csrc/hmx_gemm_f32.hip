@@ -174,7 +174,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm_f32_kernel(GemmArgs g) {
 // increasing order, so the result never depends on scheduling. V consecutive
 // columns per thread: 16-byte partial loads and 8/16-byte C stores when rows
 // and C keep that alignment (V = 4), else one element (V = 1).
-template <int V>
+template <int V, bool PROG>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws,
                                                             int splits, int64_t batch,
                                                             GemmArgs g) {
@@ -206,8 +206,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     for (int e = 0; e < V; ++e) {
       float bias, scale, shift;
       column_vectors(g, col + e, true, bias, scale, shift);
-      v[e] = apply_activation(g.act, (acc[e] + bias) * scale + shift, g.act_arg);
+      v[e] = (acc[e] + bias) * scale + shift;
     }
+    activate_all<V, PROG>(g, v);
     const int64_t off = b * g.stride_c + row * g.ldc + col;
     if (g.c_dtype == HMX_DTYPE_BF16) {
       uint16_t* c = (uint16_t*)g.c + off;
@@ -272,12 +273,15 @@ void launch_gemm_f32(const GemmArgs& g, int tile_bm, int la, int lb, bool guard,
 void launch_splitk_reduce(const float* partials, int splits, int64_t batch, const GemmArgs& r,
                           bool vec4, hipStream_t s) {
   const int64_t total = batch * r.m * r.n;
+  const bool prog = r.act == HMX_EPI_PROGRAM;
   if (vec4) {
     const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(total / 4, 256), 16384);
-    launch(splitk_reduce_kernel<4>, blocks, 256, s, partials, splits, batch, r);
+    if (prog) launch(splitk_reduce_kernel<4, true>, blocks, 256, s, partials, splits, batch, r);
+    else launch(splitk_reduce_kernel<4, false>, blocks, 256, s, partials, splits, batch, r);
   } else {
     const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(total, 256), 16384);
-    launch(splitk_reduce_kernel<1>, blocks, 256, s, partials, splits, batch, r);
+    if (prog) launch(splitk_reduce_kernel<1, true>, blocks, 256, s, partials, splits, batch, r);
+    else launch(splitk_reduce_kernel<1, false>, blocks, 256, s, partials, splits, batch, r);
   }
 }
 

@@ -70,8 +70,15 @@ inline bool valid_dtype(int dtype) {
 }
 inline int64_t dtype_bytes(int dtype) { return dtype == HMX_DTYPE_BF16 ? 2 : 4; }
 inline bool valid_activation(int code) {
-  return code >= HMX_EPI_IDENTITY && code <= HMX_EPI_LEAKY_RELU;
+  return code >= HMX_EPI_IDENTITY && code <= HMX_EPI_PROGRAM;
 }
+
+// Checks the epilogue (activation code, program) of an entry point `what`
+// and copies the program into `out` (zeroed when the code is not
+// HMX_EPI_PROGRAM). Returns HMX_OK or the HMX_ERR_INVALID of a bad code or
+// program: a null program, a count outside 1..HMX_PROGRAM_MAX, an unknown
+// opcode, or a register past HMX_PROGRAM_REGS.
+int check_epilogue(const char* what, int code, const hmx_program* program, hmx_program* out);
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

@@ -350,6 +350,7 @@ struct GroupNormArgs {
   int extra_op;
   int act;
   float act_arg;
+  hmx_program prog;  // act == HMX_EPI_PROGRAM: the whole epilogue, y = prog(value, extra)
   // w, b and extra are 16-byte aligned: with vectorizable rows (gs a
   // multiple of EPV), each row vector's EPV channels load as one piece.
   bool vec_ok;
@@ -371,13 +372,34 @@ __device__ __forceinline__ void load_vec_any(const void* p, int dtype, int64_t i
   }
 }
 
-__device__ __forceinline__ float group_norm_out(const GroupNormArgs& a, float centered,
-                                                float r, int64_t ch) {
+// The value of channel ch before the activation: the normalized value, the
+// extra op applied; with a program, the normalized value and (in `extra`)
+// the extra operand the program reads.
+__device__ __forceinline__ float group_norm_pre(const GroupNormArgs& a, float centered, float r,
+                                                int64_t ch, float& extra) {
   float yv = centered * r * (a.w ? load_any(a.w, a.vec_dtype, ch) : 1.f);
   if (a.b) yv += load_any(a.b, a.vec_dtype, ch);
+  extra = 0.f;
+  if (a.act == HMX_EPI_PROGRAM) {
+    if (a.extra) extra = load_any(a.extra, a.vec_dtype, ch);
+    return yv;
+  }
   if (a.extra_op == HMX_EXTRA_ADD) yv += load_any(a.extra, a.vec_dtype, ch);
   if (a.extra_op == HMX_EXTRA_MUL) yv *= load_any(a.extra, a.vec_dtype, ch);
-  return apply_activation(a.act, yv, a.act_arg);
+  return yv;
+}
+
+// The activation on N pre-activation values in place: a named code, or with
+// PROG (the kernel instantiated for epilogue programs) the program.
+template <int N, bool PROG>
+__device__ __forceinline__ void group_norm_finish(const GroupNormArgs& a, float (&v)[N],
+                                                  const float (&extra)[N]) {
+  if (PROG && a.act == HMX_EPI_PROGRAM) {
+    run_program_n<N>(a.prog, v, extra);
+  } else if (a.act != HMX_EPI_IDENTITY) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = apply_activation(a.act, v[i], a.act_arg);
+  }
 }
 
 template <typename T, int EPV, int VPL, bool WHOLE>
@@ -402,23 +424,27 @@ __global__ __launch_bounds__(kMaxBlock) void group_norm_cached(const T* x, T* y,
     if (WHOLE || col_of<EPV>(i / EPV, p.li, p.tpr, i % EPV) < n) q += c * c;
   }
   const float r = rsqrtf(row_sum_all(q, red_var, tpr) / (float)n + a.eps);
+  const bool prog = a.act == HMX_EPI_PROGRAM;
+  float ex[VPL * EPV];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     if constexpr (EPV > 1) {
       const int64_t col0 = col_of<EPV>(j, p.li, p.tpr, 0);
       if (a.vec_ok && (WHOLE || col0 + EPV <= n)) {
-        // The same arithmetic as group_norm_out, on whole vectors of w, b, extra.
+        // The same arithmetic as group_norm_pre, on whole vectors of w, b, extra.
         float wv[EPV], bv[EPV], ev[EPV];
         load_vec_any<EPV>(a.w, a.vec_dtype, g * n + col0, wv, 1.f);
         load_vec_any<EPV>(a.b, a.vec_dtype, g * n + col0, bv, 0.f);
-        load_vec_any<EPV>(a.extra_op != HMX_EXTRA_NONE ? a.extra : nullptr, a.vec_dtype, g * n + col0, ev, 0.f);
+        load_vec_any<EPV>(a.extra_op != HMX_EXTRA_NONE || prog ? a.extra : nullptr, a.vec_dtype, g * n + col0,
+                          ev, 0.f);
 #pragma unroll
         for (int e = 0; e < EPV; ++e) {
           float yv = (v[j * EPV + e] - mean) * r * wv[e];
           yv += bv[e];
-          if (a.extra_op == HMX_EXTRA_ADD) yv += ev[e];
-          if (a.extra_op == HMX_EXTRA_MUL) yv *= ev[e];
-          v[j * EPV + e] = apply_activation(a.act, yv, a.act_arg);
+          if (!prog && a.extra_op == HMX_EXTRA_ADD) yv += ev[e];
+          if (!prog && a.extra_op == HMX_EXTRA_MUL) yv *= ev[e];
+          v[j * EPV + e] = yv;
+          ex[j * EPV + e] = ev[e];
         }
         continue;
       }
@@ -426,13 +452,16 @@ __global__ __launch_bounds__(kMaxBlock) void group_norm_cached(const T* x, T* y,
 #pragma unroll
     for (int e = 0; e < EPV; ++e) {
       const int64_t col = col_of<EPV>(j, p.li, p.tpr, e);
-      if (WHOLE || col < n) v[j * EPV + e] = group_norm_out(a, v[j * EPV + e] - mean, r, g * n + col);
+      ex[j * EPV + e] = 0.f;
+      if (WHOLE || col < n)
+        v[j * EPV + e] = group_norm_pre(a, v[j * EPV + e] - mean, r, g * n + col, ex[j * EPV + e]);
     }
   }
+  group_norm_finish<VPL * EPV, false>(a, v, ex);
   store_row<T, EPV, VPL, WHOLE>(y + unit * n, n, p.li, p.tpr, v);
 }
 
-template <typename T, int EPV>
+template <typename T, int EPV, bool PROG>
 __global__ __launch_bounds__(kBlock) void group_norm_stream(const T* x,
                                                             T* y,
                                                             GroupNormArgs a) {
@@ -462,9 +491,13 @@ __global__ __launch_bounds__(kBlock) void group_norm_stream(const T* x,
   const float r = rsqrtf(wave_sum(q) / (float)n + a.eps);
   for (int64_t col = (int64_t)lane * EPV; col < n; col += step) {
     load_chunk<T, EPV>(xr, n, col, v, 0.f);
+    float ex[EPV];
 #pragma unroll
-    for (int e = 0; e < EPV; ++e)
-      if (col + e < n) v[e] = group_norm_out(a, v[e] - mean, r, g * n + col + e);
+    for (int e = 0; e < EPV; ++e) {
+      ex[e] = 0.f;
+      if (col + e < n) v[e] = group_norm_pre(a, v[e] - mean, r, g * n + col + e, ex[e]);
+    }
+    group_norm_finish<EPV, PROG>(a, v, ex);
     store_chunk<T, EPV>(yr, n, col, v);
   }
 }
@@ -472,11 +505,18 @@ __global__ __launch_bounds__(kBlock) void group_norm_stream(const T* x,
 // ---------------------------------------------------------------------------
 // Row reductions read each element once: streaming is their natural form.
 // mode 0: sum x; mode 1: sum x * v (v f32); mode 2: sum x * v (v of type T).
+// A reduction's epilogue: an activation code (and its argument) or a program.
+struct RowEpilogue {
+  int act;
+  float arg;
+  hmx_program prog;
+};
+
 template <typename T, int EPV, int MODE>
 __global__ __launch_bounds__(kBlock) void row_reduce(const T* x,
                                                      const void* __restrict__ vec,
                                                      T* y, int64_t m,
-                                                     int64_t n, int act, float act_arg) {
+                                                     int64_t n, RowEpilogue epi) {
   const int64_t row = unit_index();
   if (row >= m) return;
   const int lane = threadIdx.x & (kWave - 1);
@@ -502,7 +542,8 @@ __global__ __launch_bounds__(kBlock) void row_reduce(const T* x,
     }
   }
   s = wave_sum(s);
-  if (lane == 0) Elem<T>::store(y + row, apply_activation(act, s, act_arg));
+  s = epi.act == HMX_EPI_PROGRAM ? run_program(epi.prog, s, 0.f) : apply_activation(epi.act, s, epi.arg);
+  if (lane == 0) Elem<T>::store(y + row, s);
 }
 
 // Column sums: one thread per column walks all rows (each row read by a wave
@@ -773,7 +814,8 @@ int hmx_rmsnorm_rows(int dtype, const void* x, const void* w, int w_dtype, void*
 int hmx_group_norm_rows(int dtype, const void* x, const void* w, const void* b,
                         const void* extra, int vec_dtype, void* y, int64_t m,
                         int64_t groups, int64_t group_size, float eps, int extra_op,
-                        int activation, float activation_arg, void* stream) {
+                        int activation, float activation_arg, const hmx_program* program,
+                        void* stream) {
   HMX_REQUIRE(valid_dtype(dtype) && valid_dtype(vec_dtype), "group_norm: unknown dtype");
   HMX_REQUIRE(m >= 0 && groups >= 1 && group_size >= 1, "group_norm: invalid shape");
   HMX_REQUIRE(x && y, "group_norm: null operand");
@@ -781,20 +823,41 @@ int hmx_group_norm_rows(int dtype, const void* x, const void* w, const void* b,
               "group_norm: unknown extra op %d", extra_op);
   HMX_REQUIRE(extra_op == HMX_EXTRA_NONE || extra != nullptr,
               "group_norm: extra op without an extra operand");
-  HMX_REQUIRE(valid_activation(activation), "group_norm: unknown activation %d", activation);
+  hmx_program prog;
+  const int pst = check_epilogue("group_norm", activation, program, &prog);
+  if (pst != HMX_OK) return pst;
+  HMX_REQUIRE(activation != HMX_EPI_PROGRAM || extra_op == HMX_EXTRA_NONE,
+              "group_norm: an epilogue program reads the extra operand itself (extra op must be none)");
   const int64_t units = m * groups;
   HMX_REQUIRE(units <= kMaxGrid, "group_norm: too many rows");
   if (units == 0) return HMX_OK;
-  GroupNormArgs a{w, b, extra, vec_dtype, units, groups, group_size, eps,
-                  extra_op, activation, activation_arg,
-                  aligned16(w) && aligned16(b) && aligned16(extra)};
+  GroupNormArgs a{};
+  a.w = w;
+  a.b = b;
+  a.extra = extra;
+  a.vec_dtype = vec_dtype;
+  a.units = units;
+  a.groups = groups;
+  a.gs = group_size;
+  a.eps = eps;
+  a.extra_op = extra_op;
+  a.act = activation;
+  a.act_arg = activation_arg;
+  a.prog = prog;
+  a.vec_ok = aligned16(w) && aligned16(b) && aligned16(extra);
   auto s = (hipStream_t)stream;
   with_type(dtype, rows_vectorizable(x, y, group_size, dtype), [&](auto tp, auto epv_c) {
     using T = std::remove_pointer_t<decltype(tp)>;
     constexpr int EPV = decltype(epv_c)::value;
     const RowShape r = row_shape(group_size, EPV);
+    if (activation == HMX_EPI_PROGRAM) {
+      // Epilogue programs run in the streaming kernel only: the cached
+      // kernels stay free of the interpreter's registers.
+      launch(group_norm_stream<T, EPV, true>, unit_grid(units), kBlock, s, (const T*)x, (T*)y, a);
+      return;
+    }
     if (r.vpl == 0) {
-      launch(group_norm_stream<T, EPV>, unit_grid(units), kBlock, s, (const T*)x, (T*)y, a);
+      launch(group_norm_stream<T, EPV, false>, unit_grid(units), kBlock, s, (const T*)x, (T*)y, a);
       return;
     }
     with_shape<EPV>(r, [&](auto vpl_c, auto whole_c) {
@@ -807,13 +870,15 @@ int hmx_group_norm_rows(int dtype, const void* x, const void* w, const void* b,
 
 static int row_reduce_launch(const char* name, int mode, int dtype, const void* x,
                              const void* vec, void* y, int64_t m, int64_t n, int act,
-                             float act_arg, void* stream) {
+                             float act_arg, const hmx_program* program, void* stream) {
   HMX_REQUIRE(valid_dtype(dtype), "%s: unknown dtype %d", name, dtype);
   HMX_REQUIRE(m >= 0 && n >= 0, "%s: invalid shape", name);
   // Rows of no columns read nothing: x and vec may then be null (an empty
   // tensor's data pointer).
   HMX_REQUIRE((x || n == 0) && y && (mode == 0 || vec || n == 0), "%s: null operand", name);
-  HMX_REQUIRE(valid_activation(act), "%s: unknown activation %d", name, act);
+  RowEpilogue epi{act, act_arg, {}};
+  const int pst = check_epilogue(name, act, program, &epi.prog);
+  if (pst != HMX_OK) return pst;
   HMX_REQUIRE(m <= ((int64_t)1 << 31) * kRowsPerBlock, "%s: too many rows", name);
   if (m == 0) return HMX_OK;
   auto s = (hipStream_t)stream;
@@ -823,33 +888,30 @@ static int row_reduce_launch(const char* name, int mode, int dtype, const void* 
     using T = std::remove_pointer_t<decltype(tp)>;
     constexpr int EPV = decltype(epv_c)::value;
     if (mode == 0)
-      launch(row_reduce<T, EPV, 0>, unit_grid(m), kBlock, s, (const T*)x, vec, (T*)y, m, n, act,
-             act_arg);
+      launch(row_reduce<T, EPV, 0>, unit_grid(m), kBlock, s, (const T*)x, vec, (T*)y, m, n, epi);
     else if (mode == 1)
-      launch(row_reduce<T, EPV, 1>, unit_grid(m), kBlock, s, (const T*)x, vec, (T*)y, m, n, act,
-             act_arg);
+      launch(row_reduce<T, EPV, 1>, unit_grid(m), kBlock, s, (const T*)x, vec, (T*)y, m, n, epi);
     else
-      launch(row_reduce<T, EPV, 2>, unit_grid(m), kBlock, s, (const T*)x, vec, (T*)y, m, n, act,
-             act_arg);
+      launch(row_reduce<T, EPV, 2>, unit_grid(m), kBlock, s, (const T*)x, vec, (T*)y, m, n, epi);
   });
   return check_launch(name);
 }
 
 int hmx_row_sum(int dtype, const void* x, void* y, int64_t m, int64_t n, int activation,
-                float activation_arg, void* stream) {
+                float activation_arg, const hmx_program* program, void* stream) {
   return row_reduce_launch("row_sum", 0, dtype, x, nullptr, y, m, n, activation,
-                           activation_arg, stream);
+                           activation_arg, program, stream);
 }
 
 int hmx_row_dot(int dtype, const void* x, const float* v, void* y, int64_t m, int64_t n,
-                int activation, float activation_arg, void* stream) {
+                int activation, float activation_arg, const hmx_program* program, void* stream) {
   return row_reduce_launch("row_dot", 1, dtype, x, v, y, m, n, activation, activation_arg,
-                           stream);
+                           program, stream);
 }
 
 int hmx_matvec(int dtype, const void* a, const void* x, void* y, int64_t m, int64_t k,
                void* stream) {
-  return row_reduce_launch("matvec", 2, dtype, a, x, y, m, k, HMX_EPI_IDENTITY, 0.f, stream);
+  return row_reduce_launch("matvec", 2, dtype, a, x, y, m, k, HMX_EPI_IDENTITY, 0.f, nullptr, stream);
 }
 
 // Row chunks of a column sum: about 2048 workgroups, at least 256 rows each.

@@ -25,7 +25,7 @@ import torch
 from ..support.errors import UnsupportedTargetError
 
 LIBRARY_ENV = "HMX_LIBRARY"
-ABI_VERSION = 3  # HMX_ABI_VERSION of include/hmx.h
+ABI_VERSION = 4  # HMX_ABI_VERSION of include/hmx.h
 NATIVE_CALL_ENV = "HELION_MLIR_NATIVE_CALL"
 _DEFAULT = Path(__file__).resolve().parents[3] / "csrc" / "libhmx.so"
 
@@ -34,6 +34,35 @@ OK, ERR_INVALID, ERR_HIP, ERR_UNSUPPORTED = 0, 1, 2, 3
 DTYPE_F32, DTYPE_BF16 = 0, 1
 EPI_IDENTITY, EPI_RELU, EPI_SILU, EPI_SIGMOID = 0, 1, 2, 3
 EPI_GELU, EPI_GELU_TANH, EPI_TANH, EPI_LEAKY_RELU = 4, 5, 6, 7
+EPI_PROGRAM = 8
+PROGRAM_MAX, PROGRAM_REGS = 16, 8  # HMX_PROGRAM_MAX, HMX_PROGRAM_REGS
+# Epilogue program opcodes (HMX_OP_*), in order.
+OPCODES = (
+    "copy", "neg", "abs", "relu", "sigmoid", "tanh", "silu", "gelu", "gelu_tanh", "exp", "log",
+    "sqrt", "rsqrt", "recip", "erf", "sin", "cos", "log1p", "expm1", "floor", "ceil", "trunc",
+    "round", "softplus", "mish", "hardswish", "hardsigmoid", "elu", "leaky_relu", "clamp",
+    "add_c", "mul_c", "div_c", "rsub_c", "rdiv_c", "pow_c", "add", "sub", "mul", "div", "max",
+    "min", "pow",
+)
+OP = {name: code for code, name in enumerate(OPCODES)}
+
+
+class Instr(ctypes.Structure):
+    """``hmx_instr``: ``dst = op(a[, b][, c0, c1])``."""
+
+    _fields_ = [("op", ctypes.c_uint8), ("dst", ctypes.c_uint8), ("a", ctypes.c_uint8),
+                ("b", ctypes.c_uint8), ("c0", ctypes.c_float), ("c1", ctypes.c_float)]
+
+
+class Program(ctypes.Structure):
+    """``hmx_program``: an epilogue of at most PROGRAM_MAX instructions."""
+
+    _fields_ = [("count", ctypes.c_int32), ("result", ctypes.c_int32), ("code", Instr * PROGRAM_MAX)]
+
+
+def program_arg(program: "Program | None") -> "int | None":
+    """The address to pass for an ``hmx_program*`` argument (None: NULL)."""
+    return None if program is None else ctypes.addressof(program)
 B_ROW, B_TRANS, B_VNNI_PANELS, B_BLOCKED_VNNI, B_PANELS, B_BLOCKED = range(6)
 GEMM_SCRATCH_BYTES = 64 << 20  # HMX_GEMM_SCRATCH_BYTES
 EXTRA_NONE, EXTRA_ADD, EXTRA_MUL = 0, 1, 2
@@ -72,7 +101,7 @@ SIGNATURES: dict[str, list[object]] = {
         _L, _L, _L,  # m, n, k
         _L, _L, _L, _L,  # batch, stride_a, stride_b, stride_c
         _P, _P, _P, _I,  # bias, scale, shift, vec_dtype
-        _I, _F,  # epilogue, epilogue_arg
+        _I, _F, _P,  # epilogue, epilogue_arg, program
         _I, _P, _L,  # splits, workspace, workspace_bytes
         _I, _I, _I,  # tile_m, tile_n, tile_k
         _P,  # stream
@@ -85,22 +114,22 @@ SIGNATURES: dict[str, list[object]] = {
         _L, _L, _L,  # m, n, k
         _L, _L, _L, _L,  # batch, stride_a, stride_b, stride_c
         _P, _P, _P, _I,  # bias, scale, shift, vec_dtype
-        _I, _F,  # epilogue, epilogue_arg
+        _I, _F, _P,  # epilogue, epilogue_arg, program
         _I,  # splits
         _I, _I, _I,  # tile_m, tile_n, tile_k
         _P,  # stream
     ],
     "hmx_gemm_plan": [
-        _I, _L, _L, _L, _L, _I, _I, _I, _L, _I, _I, _I, _I,
+        _I, _L, _L, _L, _L, _I, _I, _I, _L, _I, _I, _I, _I, _I,
         _IP, _IP, _IP, _IP, _LP,
     ],
     "hmx_softmax_rows": [_I, _P, _P, _L, _L, _P],
     "hmx_rmsnorm_rows": [_I, _P, _P, _I, _P, _L, _L, _F, _P],
-    "hmx_group_norm_rows": [_I, _P, _P, _P, _P, _I, _P, _L, _L, _L, _F, _I, _I, _F, _P],
-    "hmx_row_sum": [_I, _P, _P, _L, _L, _I, _F, _P],
+    "hmx_group_norm_rows": [_I, _P, _P, _P, _P, _I, _P, _L, _L, _L, _F, _I, _I, _F, _P, _P],
+    "hmx_row_sum": [_I, _P, _P, _L, _L, _I, _F, _P, _P],
     "hmx_column_sum": [_I, _P, _P, _L, _L, _P, _L, _P],
     "hmx_column_sum_plan": [_L, _L, _P],
-    "hmx_row_dot": [_I, _P, _P, _P, _L, _L, _I, _F, _P],
+    "hmx_row_dot": [_I, _P, _P, _P, _L, _L, _I, _F, _P, _P],
     "hmx_matvec": [_I, _P, _P, _P, _L, _L, _P],
     "hmx_elementwise": [_I, _I, _P, _P, _L, _F, _P],
     "hmx_pack": [_I, _I, _P, _L, _L, _L, _P, _L, _L, _L, _P],

@@ -3,7 +3,8 @@
 The entry points and signatures are those of the reference's
 ``helion_mlir_utils`` (``helion_mlir_utils/__init__.py:5-69``); tensors on a
 ROCm device run hand-written gfx950 kernels through ``libhmx.so``. New here:
-``rms_norm``, ``layer_norm``, ``Activation`` epilogues, ``out_dtype`` of
+``rms_norm``, ``layer_norm``, ``Activation`` epilogues, epilogue programs
+(:func:`compile_epilogue`: any elementwise callable, fused), ``out_dtype`` of
 ``matmul``/``bmm``, and the benchmarks' panel packers and panel-major
 product (:mod:`.block_pack`).
 """
@@ -11,7 +12,9 @@ product (:mod:`.block_pack`).
 from __future__ import annotations
 
 from . import block_pack
+from . import _gpu
 from ._gpu import Activation, register_epilogue
+from ._program import EpilogueProgram, compile_epilogue
 from .block_pack import matmul_packed_b_f32, pack_b_panels_f32, unpack_panel_major
 from .elementwise import leaky_relu, relu, scalar_mul
 from .heuristics import tall_output_tiles, vnni_panel, whole_row_tiles
@@ -51,11 +54,13 @@ __all__ = [
     "CACHE_PREPACKED_WEIGHTS_ENV",
     "Activation",
     "AffineLinearCache",
+    "EpilogueProgram",
     "GroupNormEpilogue",
     "LinearCache",
     "bmm",
     "cache_prepacked_weights",
     "column_sum",
+    "compile_epilogue",
     "gemm_plan",
     "group_norm",
     "identity_epilogue",

@@ -5,7 +5,7 @@ from __future__ import annotations
 
 import contextlib
 import functools
-from typing import Callable, Iterator
+from typing import Callable, Iterator, Optional, Tuple
 
 import torch
 import torch.nn.functional as F
@@ -92,26 +92,50 @@ def register_epilogue(fn: Callable[[torch.Tensor], torch.Tensor], name: str, arg
     _KNOWN[fn] = (act.code, act.arg)
 
 
-def epilogue_code(epilogue: Callable[[torch.Tensor], torch.Tensor]) -> tuple[int, float]:
-    """The (activation code, argument) the kernels fuse for ``epilogue``.
+# What the kernels fuse for an epilogue: (activation code, its argument, the
+# epilogue program for code EPI_PROGRAM, else None).
+Epilogue = Tuple[int, float, Optional[native.Program]]
+IDENTITY: Epilogue = (native.EPI_IDENTITY, 0.0, None)
+
+# Single-operation programs that are one of the named activations: those
+# keep the kernels' register epilogues.
+_NAMED_PROGRAMS = {
+    native.OP["relu"]: native.EPI_RELU,
+    native.OP["silu"]: native.EPI_SILU,
+    native.OP["sigmoid"]: native.EPI_SIGMOID,
+    native.OP["gelu"]: native.EPI_GELU,
+    native.OP["gelu_tanh"]: native.EPI_GELU_TANH,
+    native.OP["tanh"]: native.EPI_TANH,
+    native.OP["leaky_relu"]: native.EPI_LEAKY_RELU,
+}
+
+
+def epilogue_code(epilogue: Callable[[torch.Tensor], torch.Tensor]) -> Epilogue:
+    """What the kernels fuse for ``epilogue``: one of the named activations,
+    or any other elementwise callable traced into an epilogue program
+    (:func:`compile_epilogue`).
 
     Raises ``ValueError`` for a callable they cannot fuse: an epilogue is
     never run as a separate eager pass behind the caller's back."""
+    from ._program import compile_epilogue
+
     if isinstance(epilogue, Activation):
-        return epilogue.code, epilogue.arg
+        return epilogue.code, epilogue.arg, None
     if epilogue in _KNOWN:
-        return _KNOWN[epilogue]
+        return (*_KNOWN[epilogue], None)
     if isinstance(epilogue, functools.partial) and not epilogue.args:
         kwargs = epilogue.keywords
         if epilogue.func is F.leaky_relu and set(kwargs) <= {"negative_slope"}:
-            return native.EPI_LEAKY_RELU, float(kwargs.get("negative_slope", 0.01))
+            return native.EPI_LEAKY_RELU, float(kwargs.get("negative_slope", 0.01)), None
         if epilogue.func is F.gelu and set(kwargs) <= {"approximate"}:
             approx = kwargs.get("approximate", "none")
-            return (native.EPI_GELU_TANH if approx == "tanh" else native.EPI_GELU), 0.0
+            return (native.EPI_GELU_TANH if approx == "tanh" else native.EPI_GELU), 0.0, None
     if epilogue is identity_epilogue or getattr(epilogue, "__name__", None) == "identity_epilogue":
-        return native.EPI_IDENTITY, 0.0
-    raise ValueError(
-        f"the gpu target cannot fuse the epilogue {epilogue!r}: use identity, torch.relu, "
-        "F.silu, torch.sigmoid, F.gelu (erf or tanh), torch.tanh, F.leaky_relu, an "
-        "Activation, or register_epilogue()"
-    )
+        return IDENTITY
+    program = compile_epilogue(epilogue, 1)
+    if program is None:
+        return IDENTITY
+    if len(program.code) == 1 and program.code[0].a == 0 and program.code[0].op in _NAMED_PROGRAMS:
+        ins = program.code[0]
+        return _NAMED_PROGRAMS[ins.op], ins.c0, None
+    return native.EPI_PROGRAM, 0.0, program.struct

@@ -35,7 +35,7 @@ from torch import Tensor
 from helion_mlir_backend import output_pool
 from helion_mlir_backend._compiler import native
 
-from ._gpu import SUPPORTED_DTYPES, epilogue_code, identity_epilogue, is_gpu, on_device
+from ._gpu import IDENTITY, SUPPORTED_DTYPES, Epilogue, epilogue_code, identity_epilogue, is_gpu, on_device
 
 __all__ = [
     "BLOCK_K",
@@ -144,11 +144,13 @@ _PLANS_MAX = 1024
 
 
 def _plan(ab: int, m: int, n: int, k: int, batch: int, trans_a: bool, layout: int,
-          splits: int, tiles: Sequence[int] | None, units: int = 0) -> tuple[int, int, int, int, int]:
+          splits: int, tiles: Sequence[int] | None, units: int = 0,
+          epilogue: int = native.EPI_IDENTITY) -> tuple[int, int, int, int, int]:
     """hmx_gemm_plan for a device of ``units`` compute units (0: the
-    library's default): (splits, tile_m, tile_n, tile_k, workspace bytes)."""
+    library's default) and the epilogue code: (splits, tile_m, tile_n,
+    tile_k, workspace bytes)."""
     tm, tn, tk = (list(tiles) + [0, 0, 0])[:3] if tiles else (0, 0, 0)
-    key = (ab, m, n, k, batch, bool(trans_a), layout, splits, int(tm), int(tn), int(tk), units)
+    key = (ab, m, n, k, batch, bool(trans_a), layout, splits, int(tm), int(tn), int(tk), units, epilogue)
     hit = _PLANS.get(key)
     if hit is not None:
         return hit
@@ -156,7 +158,7 @@ def _plan(ab: int, m: int, n: int, k: int, batch: int, trans_a: bool, layout: in
     ws = ctypes.c_int64()
     native.check(
         native.lib().hmx_gemm_plan(ab, m, n, k, batch, int(trans_a), layout, splits, -1,
-                                   int(tm), int(tn), int(tk), units, *[ctypes.byref(o) for o in out],
+                                   int(tm), int(tn), int(tk), units, epilogue, *[ctypes.byref(o) for o in out],
                                    ctypes.byref(ws)),
         "hmx_gemm_plan",
     )
@@ -202,17 +204,18 @@ class GemmLaunch:
         m: int, n: int, k: int, batch: int = 1, stride_a: int = 0, stride_b: int = 0,
         stride_c: int = 0, bias: Tensor | None = None, scale: Tensor | None = None,
         shift: Tensor | None = None, vec_dtype: int = native.DTYPE_F32,
-        epilogue: tuple[int, float] = (native.EPI_IDENTITY, 0.0), splits: int = 0,
+        epilogue: Epilogue = IDENTITY, splits: int = 0,
         tiles: Sequence[int] | None = None,
     ) -> None:
         # The launch passes the plan's own splits and tile back with a
         # workspace of the planned size, which reproduces the plan exactly.
         s, tm, tn, tk, ws_bytes = _plan(ab, m, n, k, batch, trans_a, layout, splits, tiles,
-                                        native.device_units(device))
+                                        native.device_units(device), epilogue[0])
         self._fn = native.lib().hmx_gemm
-        self._vectors = (bias, scale, shift)
+        # The bound vectors and the epilogue program stay alive with the launch.
+        self._vectors = (bias, scale, shift, epilogue[2])
         # The arguments of hmx_gemm in order (include/hmx.h); slots 2 (A),
-        # 5 (B), 10 (C), 26 (workspace) and 31 (stream) are filled per call.
+        # 5 (B), 10 (C), 27 (workspace) and 32 (stream) are filled per call.
         self._args = [
             ab, native.dtype_code(c_dtype),
             None, lda, int(trans_a),
@@ -221,7 +224,7 @@ class GemmLaunch:
             m, n, k,
             batch, stride_a, stride_b, stride_c,
             native.ptr(bias), native.ptr(scale), native.ptr(shift), vec_dtype,
-            epilogue[0], epilogue[1],
+            epilogue[0], epilogue[1], native.program_arg(epilogue[2]),
             s, None, ws_bytes,
             int(tm), int(tn), int(tk),
             None,
@@ -243,15 +246,15 @@ class GemmLaunch:
         ws = None
         if self._ws_bytes > 0:
             ws = torch.empty(self._ws_bytes, dtype=torch.uint8, device=self._device)
-            args[26] = ws.data_ptr()
+            args[27] = ws.data_ptr()
         device = self._device
         if device.index is None or device.index == torch.cuda.current_device():
             native.ensure_device(device)
-            args[31] = native.stream_of(device)
+            args[32] = native.stream_of(device)
             status = self._fn(*args)
         else:
             with on_device(device) as stream:
-                args[31] = stream
+                args[32] = stream
                 status = self._fn(*args)
         native.count_call()
         if status:
@@ -265,7 +268,7 @@ def _launch_gemm(
     c: Tensor, m: int, n: int, k: int,
     batch: int = 1, stride_a: int = 0, stride_b: int = 0, stride_c: int = 0,
     bias: Tensor | None = None, scale: Tensor | None = None, shift: Tensor | None = None,
-    vec_dtype: int = native.DTYPE_F32, epilogue: tuple[int, float] = (native.EPI_IDENTITY, 0.0),
+    vec_dtype: int = native.DTYPE_F32, epilogue: Epilogue = IDENTITY,
     splits: int = 0, tiles: Sequence[int] | None = None,
 ) -> Tensor:
     launch = GemmLaunch(

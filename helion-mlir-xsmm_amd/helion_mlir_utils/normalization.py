@@ -90,18 +90,22 @@ _EXTRA_OPS: dict[object, int] = {
 }
 
 
-def _extra_op(epilogue: Callable[[Tensor, Tensor], Tensor]) -> tuple[int, int, float]:
-    """(extra op, activation, activation arg) fused for a group-norm epilogue:
-    ``_second_operand`` (y), ``torch.add``/``torch.mul`` with the extra operand,
-    or ``GroupNormEpilogue``."""
-    if isinstance(epilogue, GroupNormEpilogue):
-        return epilogue.extra_op, *epilogue.activation
+def _extra_op(epilogue: Callable[[Tensor, Tensor], Tensor]) -> tuple[int, int, float, native.Program | None]:
+    """(extra op, activation, activation arg, program) fused for a group-norm
+    epilogue: ``_second_operand`` (y), ``torch.add``/``torch.mul`` with the
+    extra operand, ``GroupNormEpilogue``, or any other elementwise
+    ``epilogue(y, extra)`` traced into an epilogue program (extra op none: the
+    program reads the extra operand itself)."""
+    from ._program import compile_epilogue
+
+    if isinstance(epilogue, GroupNormEpilogue) and epilogue.activation[0] != native.EPI_PROGRAM:
+        return epilogue.extra_op, epilogue.activation[0], epilogue.activation[1], None
     if epilogue in _EXTRA_OPS:
-        return _EXTRA_OPS[epilogue], native.EPI_IDENTITY, 0.0
-    raise ValueError(
-        f"the gpu target cannot fuse the group_norm epilogue {epilogue!r}: use the default, "
-        "torch.add, torch.mul or GroupNormEpilogue"
-    )
+        return _EXTRA_OPS[epilogue], native.EPI_IDENTITY, 0.0, None
+    program = compile_epilogue(epilogue, 2)
+    if program is None:
+        return native.EXTRA_NONE, native.EPI_IDENTITY, 0.0, None
+    return native.EXTRA_NONE, native.EPI_PROGRAM, 0.0, program.struct
 
 
 class GroupNormEpilogue:
@@ -146,11 +150,12 @@ def group_norm(
         )
     _check("group_norm", x)
     m, c = map(int, x.shape)
-    extra_op, act, act_arg = _extra_op(epilogue)
-    if extra_op != native.EXTRA_NONE and extra is None:
-        extra = weight
+    extra_op, act, act_arg, program = _extra_op(epilogue)
+    reads_extra = extra_op != native.EXTRA_NONE or act == native.EPI_PROGRAM
+    if reads_extra and extra is None:
+        extra = weight  # the reference's default extra operand (normalization.py:190-192)
     vecs = []
-    for name, v in (("weight", weight), ("bias", bias), ("extra", extra if extra_op else None)):
+    for name, v in (("weight", weight), ("bias", bias), ("extra", extra if reads_extra else None)):
         if v is None:
             vecs.append(None)
             continue
@@ -163,7 +168,8 @@ def group_norm(
     with on_device(x.device) as stream:
         native.call("hmx_group_norm_rows", native.dtype_code(x.dtype), x.data_ptr(),
                     native.ptr(vecs[0]), native.ptr(vecs[1]), native.ptr(vecs[2]), native.DTYPE_F32,
-                    y.data_ptr(), m, num_groups, c // num_groups, float(eps), extra_op, act, act_arg, stream)
+                    y.data_ptr(), m, num_groups, c // num_groups, float(eps), extra_op, act, act_arg,
+                    native.program_arg(program), stream)
     return y
 
 

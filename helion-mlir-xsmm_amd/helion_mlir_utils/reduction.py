@@ -66,14 +66,15 @@ def matvec(a: Tensor, b: Tensor) -> Tensor:
 def row_sum(x: Tensor, epilogue: Callable[[Tensor], Tensor] = identity_epilogue) -> Tensor:
     """``epilogue(x.sum(1, keepdim=True))`` of a 2-D ``x``, summed in f32."""
     _check("row_sum", x)
-    code, arg = epilogue_code(epilogue)
+    code, arg, program = epilogue_code(epilogue)
     m, n = map(int, x.shape)
     x = x.contiguous()
     out = output_pool.empty((m, 1), dtype=x.dtype, device=x.device)
     if m == 0:
         return out
     with on_device(x.device) as stream:
-        native.call("hmx_row_sum", native.dtype_code(x.dtype), x.data_ptr(), out.data_ptr(), m, n, code, arg, stream)
+        native.call("hmx_row_sum", native.dtype_code(x.dtype), x.data_ptr(), out.data_ptr(), m, n, code, arg,
+                    native.program_arg(program), stream)
     return out
 
 
@@ -106,7 +107,7 @@ def row_dot(x: Tensor, v: Tensor, epilogue: Callable[[Tensor], Tensor] = identit
     if v.dtype != torch.float32:
         raise ValueError(f"row_dot() expects an f32 vector, got {v.dtype}")
     _check("row_dot", x)
-    code, arg = epilogue_code(epilogue)
+    code, arg, program = epilogue_code(epilogue)
     m, n = map(int, x.shape)
     x = x.contiguous()
     v = v.to(x.device).contiguous()
@@ -115,5 +116,5 @@ def row_dot(x: Tensor, v: Tensor, epilogue: Callable[[Tensor], Tensor] = identit
         return out
     with on_device(x.device) as stream:
         native.call("hmx_row_dot", native.dtype_code(x.dtype), x.data_ptr(), v.data_ptr(), out.data_ptr(),
-                    m, n, code, arg, stream)
+                    m, n, code, arg, native.program_arg(program), stream)
     return out

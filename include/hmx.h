@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 3
+#define HMX_ABI_VERSION 4
 
 /* Status codes. */
 #define HMX_OK 0
@@ -55,6 +55,81 @@ extern "C" {
 #define HMX_EPI_GELU_TANH 5  /* tanh approximation */
 #define HMX_EPI_TANH 6
 #define HMX_EPI_LEAKY_RELU 7 /* epilogue_arg = negative slope */
+#define HMX_EPI_PROGRAM 8    /* the elementwise program `program` */
+
+/*
+ * Epilogue programs: an elementwise function of f32 values, for epilogues
+ * that are not one of the activations above (the reference applies any
+ * callable to the f32 accumulator, helion_mlir_utils/matmul.py:321-327, and
+ * `epilogue(y, extra)` in group_norm, normalization.py:121). A program is a
+ * straight-line list of at most HMX_PROGRAM_MAX instructions over
+ * HMX_PROGRAM_REGS f32 registers. On entry register 0 holds the value (the
+ * GEMM's `(acc + bias) * scale + shift`, group_norm's normalized value),
+ * register 1 the extra operand (group_norm's per-channel `extra`, else 0) and
+ * the others 0; each instruction writes `dst`; the result is register
+ * `result`, rounded once to the output dtype. Every operation rounds to f32
+ * as the same torch operation on f32 tensors does; max/min/clamp/relu keep
+ * NaN.
+ */
+#define HMX_PROGRAM_MAX 16
+#define HMX_PROGRAM_REGS 8
+
+/* Opcodes: dst = f(a) | f(a, b) | f(a, c0[, c1]), registers a, b. */
+#define HMX_OP_COPY 0
+#define HMX_OP_NEG 1
+#define HMX_OP_ABS 2
+#define HMX_OP_RELU 3
+#define HMX_OP_SIGMOID 4
+#define HMX_OP_TANH 5
+#define HMX_OP_SILU 6
+#define HMX_OP_GELU 7         /* erf form */
+#define HMX_OP_GELU_TANH 8
+#define HMX_OP_EXP 9
+#define HMX_OP_LOG 10
+#define HMX_OP_SQRT 11
+#define HMX_OP_RSQRT 12
+#define HMX_OP_RECIP 13
+#define HMX_OP_ERF 14
+#define HMX_OP_SIN 15
+#define HMX_OP_COS 16
+#define HMX_OP_LOG1P 17
+#define HMX_OP_EXPM1 18
+#define HMX_OP_FLOOR 19
+#define HMX_OP_CEIL 20
+#define HMX_OP_TRUNC 21
+#define HMX_OP_ROUND 22       /* half to even */
+#define HMX_OP_SOFTPLUS 23    /* c0 = beta, c1 = threshold */
+#define HMX_OP_MISH 24
+#define HMX_OP_HARDSWISH 25
+#define HMX_OP_HARDSIGMOID 26
+#define HMX_OP_ELU 27         /* c0 = alpha, c1 = output scale (SELU: its scale) */
+#define HMX_OP_LEAKY_RELU 28  /* c0 = negative slope */
+#define HMX_OP_CLAMP 29       /* c0 = lower, c1 = upper bound (+-inf: none) */
+#define HMX_OP_ADD_C 30       /* a + c0 */
+#define HMX_OP_MUL_C 31       /* a * c0 */
+#define HMX_OP_DIV_C 32       /* a / c0 */
+#define HMX_OP_RSUB_C 33      /* c0 - a */
+#define HMX_OP_RDIV_C 34      /* c0 / a */
+#define HMX_OP_POW_C 35       /* a ** c0 */
+#define HMX_OP_ADD 36         /* a + b */
+#define HMX_OP_SUB 37         /* a - b */
+#define HMX_OP_MUL 38         /* a * b */
+#define HMX_OP_DIV 39         /* a / b */
+#define HMX_OP_MAX 40         /* max(a, b) */
+#define HMX_OP_MIN 41         /* min(a, b) */
+#define HMX_OP_POW 42         /* a ** b */
+#define HMX_OP_COUNT 43
+
+typedef struct hmx_instr {
+  uint8_t op, dst, a, b;
+  float c0, c1;
+} hmx_instr;
+
+typedef struct hmx_program {
+  int32_t count;  /* instructions, 1 .. HMX_PROGRAM_MAX */
+  int32_t result; /* the register holding the result */
+  hmx_instr code[HMX_PROGRAM_MAX];
+} hmx_program;
 
 /* Layouts of the GEMM's B operand (logical B is [K, N]).
  *   ROW           [K, N] row-major, row stride ldb
@@ -122,7 +197,8 @@ int hmx_time_launches(void* start_event, void* stop_event);
  *   C[b] = act(((op(A[b]) @ B[b]) + bias) * scale + shift)
  * op(A) is A [M, K] (lda) or, with trans_a, the transpose of A [K, M].
  * bias/scale/shift are [N] vectors of vec_dtype or NULL; accumulation is f32
- * and C (c_dtype) is rounded once. ab_dtype is HMX_DTYPE_BF16 (MFMA bf16) or
+ * and C (c_dtype) is rounded once. `act` is `epilogue` (HMX_EPI_*); with
+ * HMX_EPI_PROGRAM it is `program` (otherwise `program` is ignored). ab_dtype is HMX_DTYPE_BF16 (MFMA bf16) or
  * HMX_DTYPE_F32 (MFMA f32). `batch` slices are strided by stride_a/b/c
  * elements. `splits` > 1 divides K into that many chunks whose f32 partials
  * ([splits, batch, M, N] in `workspace`) are summed in a fixed order by a
@@ -147,7 +223,7 @@ int hmx_gemm(int ab_dtype, int c_dtype,
              int64_t m, int64_t n, int64_t k,
              int64_t batch, int64_t stride_a, int64_t stride_b, int64_t stride_c,
              const void* bias, const void* scale, const void* shift, int vec_dtype,
-             int epilogue, float epilogue_arg,
+             int epilogue, float epilogue_arg, const hmx_program* program,
              int splits, void* workspace, int64_t workspace_bytes,
              int tile_m, int tile_n, int tile_k,
              void* stream);
@@ -174,7 +250,7 @@ int hmx_gemm_noalloc(int ab_dtype, int c_dtype,
                      int64_t m, int64_t n, int64_t k,
                      int64_t batch, int64_t stride_a, int64_t stride_b, int64_t stride_c,
                      const void* bias, const void* scale, const void* shift, int vec_dtype,
-                     int epilogue, float epilogue_arg,
+                     int epilogue, float epilogue_arg, const hmx_program* program,
                      int splits,
                      int tile_m, int tile_n, int tile_k,
                      void* stream);
@@ -183,13 +259,16 @@ int hmx_gemm_noalloc(int ab_dtype, int c_dtype,
  * `compute_units` CUs (0 = the current device's; MI355X's 256 when no device
  * is visible), without launching: the K splits (after `splits` = 0 is
  * resolved; `max_workspace_bytes` < 0 means unlimited), the workgroup tile
- * and the workspace bytes needed. Host-only. Passing the result back to
+ * and the workspace bytes needed. `epilogue` is the launch's HMX_EPI_* code:
+ * an epilogue program plans f32 partials even unsplit (kernels that do not
+ * run programs fused leave them to the split-K reduction) and never the
+ * skinny kernel. Host-only. Passing the result back to
  * hmx_gemm -- its splits, its tile as tile_m/n/k and a workspace of its size --
  * makes exactly the planned launch. Stands in for the tile heuristics
  * _fused_pack_tiles / _split_k (helion_mlir_utils/matmul.py:368-446, 1257-1287). */
 int hmx_gemm_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch,
                   int trans_a, int b_layout, int splits, int64_t max_workspace_bytes,
-                  int tile_m, int tile_n, int tile_k, int compute_units,
+                  int tile_m, int tile_n, int tile_k, int compute_units, int epilogue,
                   int* out_splits, int* out_tile_m, int* out_tile_n, int* out_tile_k,
                   int64_t* out_workspace_bytes);
 
@@ -210,18 +289,21 @@ int hmx_rmsnorm_rows(int dtype, const void* x, const void* w, int w_dtype, void*
  *   y = act(extra_op((x - mean) * rsqrt(var + eps) * w + b, extra))
  * statistics per (row, group) in f32, centered variance; w, b, extra are
  * [G * S] of vec_dtype (b and extra may be NULL). G = 1 is LayerNorm.
- * x == y is allowed. Stands in for group_norm
+ * With activation HMX_EPI_PROGRAM the whole epilogue is `program` instead:
+ * y = program(normalized value, extra) (extra_op must be HMX_EXTRA_NONE; a
+ * NULL extra reads 0). x == y is allowed. Stands in for group_norm
  * (helion_mlir_utils/normalization.py:94-123, 156-196). */
 int hmx_group_norm_rows(int dtype, const void* x, const void* w, const void* b,
                         const void* extra, int vec_dtype, void* y,
                         int64_t m, int64_t groups, int64_t group_size, float eps,
                         int extra_op, int activation, float activation_arg,
-                        void* stream);
+                        const hmx_program* program, void* stream);
 
 /* y[i] = act(sum_j x[i, j]) of contiguous [M, N], f32 accumulation, y [M] in
  * dtype. Stands in for row_sum (helion_mlir_utils/reduction.py:79-121). */
 int hmx_row_sum(int dtype, const void* x, void* y, int64_t m, int64_t n,
-                int activation, float activation_arg, void* stream);
+                int activation, float activation_arg, const hmx_program* program,
+                void* stream);
 
 /* y[j] = sum_i x[i, j] of contiguous [M, N] into f32 y [N], in two passes
  * (row chunks into f32 partials in `workspace`, then the chunks added in
@@ -236,7 +318,8 @@ int hmx_column_sum_plan(int64_t m, int64_t n, int64_t* workspace_bytes);
 /* y[i] = act(sum_j x[i, j] * v[j]), v f32 [N], y [M] in dtype. Stands in for
  * row_dot (helion_mlir_utils/reduction.py:166-212). */
 int hmx_row_dot(int dtype, const void* x, const float* v, void* y, int64_t m,
-                int64_t n, int activation, float activation_arg, void* stream);
+                int64_t n, int activation, float activation_arg,
+                const hmx_program* program, void* stream);
 
 /* y = A @ x of contiguous A [M, K] and x [K] (both dtype), f32 accumulation,
  * y [M] in dtype. Stands in for matvec (helion_mlir_utils/reduction.py:24-67). */

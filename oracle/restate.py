@@ -92,6 +92,21 @@ def activation(name: str, x: np.ndarray, arg: float = 0.01) -> np.ndarray:
 # GEMM family
 
 
+def apply_epilogue(act, x: np.ndarray, arg: float = 0.01, extra: np.ndarray | None = None) -> np.ndarray:
+    """The epilogue on f32 values: a named activation (``activation``), or the
+    caller's own callable applied to f32 tensors, as the reference applies
+    ``epilogue(acc)`` to its f32 accumulator (helion_mlir_utils/matmul.py:321-327)
+    and ``epilogue(y, extra)`` to f32 group-norm values (normalization.py:121)."""
+    if not callable(act):
+        return activation(act, x, arg)
+    import torch
+
+    t = torch.from_numpy(np.ascontiguousarray(x, dtype=F32))
+    operands = (t,) if extra is None else (t, torch.from_numpy(np.ascontiguousarray(extra, dtype=F32)))
+    with torch.no_grad():
+        return act(*operands).numpy().astype(F32)
+
+
 def _op(x: np.ndarray, trans: bool) -> np.ndarray:
     return np.asarray(x, dtype=F32).T if trans else np.asarray(x, dtype=F32)
 
@@ -104,7 +119,7 @@ def matmul(
     bias: np.ndarray | None = None,
     scale: np.ndarray | None = None,
     shift: np.ndarray | None = None,
-    act: str = "identity",
+    act="identity",
     act_arg: float = 0.01,
     out: str = "f32",
 ) -> np.ndarray:
@@ -121,7 +136,7 @@ def matmul(
             acc = acc * np.asarray(scale, dtype=F32)
         if shift is not None:
             acc = acc + np.asarray(shift, dtype=F32)
-    return round_to(activation(act, acc, act_arg), out)
+    return round_to(apply_epilogue(act, acc, act_arg), out)
 
 
 def bmm(a: np.ndarray, b: np.ndarray, out: str = "f32") -> np.ndarray:
@@ -261,7 +276,7 @@ def group_norm(
     eps: float,
     extra: np.ndarray | None = None,
     extra_op: str | None = None,
-    act: str = "identity",
+    act="identity",
     act_arg: float = 0.01,
     out: str = "f32",
 ) -> np.ndarray:
@@ -284,13 +299,16 @@ def group_norm(
         y = y + np.asarray(extra, dtype=F32)
     elif extra_op == "mul":
         y = y * np.asarray(extra, dtype=F32)
-    return round_to(activation(act, y, act_arg), out)
+    elif extra_op == "callable":  # act is the caller's epilogue(y, extra)
+        extra_v = np.asarray(extra if extra is not None else w, dtype=F32)
+        return round_to(apply_epilogue(act, y, act_arg, np.broadcast_to(extra_v, y.shape)), out)
+    return round_to(apply_epilogue(act, y, act_arg), out)
 
 
-def row_sum(x: np.ndarray, act: str = "identity", out: str = "f32") -> np.ndarray:
+def row_sum(x: np.ndarray, act="identity", out: str = "f32") -> np.ndarray:
     """``epilogue(x.sum(1, keepdim=True))`` in f32 (reduction.py:79-91)."""
     s = np.asarray(x, dtype=F32).sum(axis=1, keepdims=True, dtype=F32)
-    return round_to(activation(act, s), out)
+    return round_to(apply_epilogue(act, s), out)
 
 
 def column_sum(x: np.ndarray) -> np.ndarray:
@@ -298,10 +316,10 @@ def column_sum(x: np.ndarray) -> np.ndarray:
     return (np.asarray(x, dtype=F32).sum(axis=0, dtype=F32) + F32(0)).astype(F32)
 
 
-def row_dot(x: np.ndarray, v: np.ndarray, act: str = "identity", out: str = "f32") -> np.ndarray:
+def row_dot(x: np.ndarray, v: np.ndarray, act="identity", out: str = "f32") -> np.ndarray:
     """``epilogue(x @ v)`` in f32, ``[M, 1]`` (reduction.py:166-182)."""
     s = (np.asarray(x, dtype=F32) * np.asarray(v, dtype=F32)[None, :]).sum(axis=1, keepdims=True, dtype=F32)
-    return round_to(activation(act, s), out)
+    return round_to(apply_epilogue(act, s), out)
 
 
 def matvec(a: np.ndarray, x: np.ndarray, out: str = "f32") -> np.ndarray:

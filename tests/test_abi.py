@@ -60,7 +60,7 @@ def test_binding_covers_the_header() -> None:
 
 
 def test_abi_version(lib: ctypes.CDLL) -> None:
-    assert lib.hmx_abi_version() == native.ABI_VERSION == 3
+    assert lib.hmx_abi_version() == native.ABI_VERSION == 4
 
 
 @pytest.mark.parametrize(
@@ -70,11 +70,13 @@ def test_abi_version(lib: ctypes.CDLL) -> None:
         ("hmx_softmax_rows", (0, 16, 16, 4, 0, None), "invalid shape"),
         ("hmx_softmax_rows", (0, None, 16, 4, 4, None), "null operand"),
         ("hmx_rmsnorm_rows", (1, 16, None, 0, 16, -1, 4, 1e-6, None), "invalid shape"),
-        ("hmx_group_norm_rows", (0, 16, 16, 16, None, 0, 16, 2, 3, 4, 1e-5, 1, 0, 0.0, None),
+        ("hmx_group_norm_rows", (0, 16, 16, 16, None, 0, 16, 2, 3, 4, 1e-5, 1, 0, 0.0, None, None),
          "extra op without an extra operand"),
-        ("hmx_group_norm_rows", (0, 16, 16, 16, 16, 0, 16, 2, 3, 4, 1e-5, 0, 99, 0.0, None),
-         "unknown activation"),
-        ("hmx_row_sum", (0, 16, 16, 2, 2, 42, 0.0, None), "unknown activation"),
+        ("hmx_group_norm_rows", (0, 16, 16, 16, 16, 0, 16, 2, 3, 4, 1e-5, 0, 99, 0.0, None, None),
+         "unknown epilogue"),
+        ("hmx_group_norm_rows", (0, 16, 16, 16, 16, 0, 16, 2, 3, 4, 1e-5, 0, 8, 0.0, None, None),
+         "epilogue program is null"),
+        ("hmx_row_sum", (0, 16, 16, 2, 2, 42, 0.0, None, None), "unknown epilogue"),
         ("hmx_elementwise", (9, 0, 16, 16, 4, 0.0, None), "unknown op"),
         ("hmx_pack", (42, 0, 16, 4, 4, 4, 16, 32, 32, 0, None), "unknown kind"),
         ("hmx_pack", (1, 0, 16, 4, 4, 4, 16, 40, 32, 0, None), "multiples of 32"),
@@ -91,9 +93,18 @@ def test_invalid_arguments_are_refused(lib: ctypes.CDLL, name: str, args: tuple,
 def _gemm(lib: ctypes.CDLL, **kw: object) -> int:
     args = dict(ab=1, c=1, a=16, lda=64, trans_a=0, b=16, ldb=64, layout=0, panel=0, kpad=0,
                 cp=16, ldc=64, m=64, n=64, k=64, batch=1, sa=0, sb=0, sc=0, bias=None,
-                scale=None, shift=None, vd=0, epi=0, arg=0.0, splits=1, ws=None, wsb=0,
+                scale=None, shift=None, vd=0, epi=0, arg=0.0, prog=None, splits=1, ws=None, wsb=0,
                 tm=0, tn=0, tk=0, stream=None)
     args.update(kw)
+    prog = args["prog"]
+    if isinstance(prog, str):
+        p = native.Program()
+        p.count = 0 if prog == "empty" else 1
+        p.code[0] = native.Instr(99 if prog == "bad_op" else native.OP["relu"], 9 if prog == "bad_reg" else 2, 0, 0,
+                                 0.0, 0.0)
+        p.result = 2
+        args["prog"] = native.program_arg(p)
+        return lib.hmx_gemm(*args.values())
     return lib.hmx_gemm(*args.values())
 
 
@@ -104,6 +115,11 @@ def _gemm(lib: ctypes.CDLL, **kw: object) -> int:
         ({"layout": 9}, "unknown B layout"),
         ({"ab": 0, "layout": native.B_VNNI_PANELS, "panel": 64, "kpad": 64}, "VNNI layouts"),
         ({"epi": 77}, "unknown epilogue"),
+        ({"epi": native.EPI_PROGRAM}, "epilogue program is null"),
+        ({"epi": native.EPI_PROGRAM, "prog": "empty"}, "0 instructions"),
+        ({"epi": native.EPI_PROGRAM, "prog": "bad_op"}, "unknown opcode"),
+        ({"epi": native.EPI_PROGRAM, "prog": "bad_reg"}, "register past"),
+        ({"epi": native.EPI_PROGRAM, "prog": "ok"}, "an epilogue program needs"),
         ({"lda": 8}, "lda"),
         ({"ldb": 8}, "ldb"),
         ({"ldc": 8}, "ldc"),
@@ -123,10 +139,11 @@ def test_gemm_refuses_bad_arguments(lib: ctypes.CDLL, kw: dict, message: str) ->
 
 def _plan(lib: ctypes.CDLL, ab: int, m: int, n: int, k: int, batch: int = 1, splits: int = 0,
           max_ws: int = -1, tiles: tuple[int, int, int] = (0, 0, 0),
-          b_layout: int = native.B_ROW, cus: int = 256, trans_a: int = 0) -> tuple[int, int, int, int, int]:
+          b_layout: int = native.B_ROW, cus: int = 256, trans_a: int = 0,
+          epi: int = native.EPI_IDENTITY) -> tuple[int, int, int, int, int]:
     outs = [ctypes.c_int() for _ in range(4)]
     ws = ctypes.c_int64()
-    assert lib.hmx_gemm_plan(ab, m, n, k, batch, trans_a, b_layout, splits, max_ws, *tiles, cus,
+    assert lib.hmx_gemm_plan(ab, m, n, k, batch, trans_a, b_layout, splits, max_ws, *tiles, cus, epi,
                              *[ctypes.byref(o) for o in outs], ctypes.byref(ws)) == 0
     return (*[o.value for o in outs], ws.value)
 
@@ -238,9 +255,24 @@ _PLAN_LAYOUTS = [(native.B_ROW, 0), (native.B_TRANS, 0), (native.B_ROW, 1), (nat
                  (native.B_BLOCKED, 0), (native.B_PANELS, 0)]
 
 
+def test_program_epilogues_plan_their_partials(lib: ctypes.CDLL) -> None:
+    bf16, f32 = native.DTYPE_BF16, native.DTYPE_F32
+    prog = native.EPI_PROGRAM
+    # An unsplit product plans f32 partials of the whole output for kernels
+    # that leave the program to the reduction; split products plan them anyway.
+    assert _plan(lib, bf16, 4096, 4096, 4096, epi=prog) == (1, 256, 256, 64, 4096 * 4096 * 4)
+    assert _plan(lib, f32, 512, 512, 512, epi=prog) == (4, 64, 64, 32, 4 * 512 * 512 * 4)
+    # Decode-shaped products never take the skinny kernel with a program.
+    assert _plan(lib, bf16, 32, 11008, 4096, b_layout=native.B_TRANS)[:4] == (1, 32, 32, 64)
+    assert _plan(lib, bf16, 32, 11008, 4096, b_layout=native.B_TRANS, epi=prog)[1:3] != (32, 32)
+    # Named activations plan as before.
+    assert _plan(lib, bf16, 4096, 4096, 4096, epi=native.EPI_GELU) == (1, 256, 256, 64, 0)
+
+
+@pytest.mark.parametrize("epi", [native.EPI_IDENTITY, native.EPI_PROGRAM])
 @pytest.mark.parametrize("cus", [256, 304, 80, 32])
 @pytest.mark.parametrize("ab", [native.DTYPE_BF16, native.DTYPE_F32])
-def test_a_plan_passed_back_is_the_same_plan(lib: ctypes.CDLL, cus: int, ab: int) -> None:
+def test_a_plan_passed_back_is_the_same_plan(lib: ctypes.CDLL, cus: int, ab: int, epi: int) -> None:
     # What a prepared launch does: plan with splits = 0 and no workspace
     # limit, then call hmx_gemm with the plan's splits, tile and workspace.
     # hmx_gemm plans again from those; the two plans must agree, or the kernel
@@ -249,10 +281,10 @@ def test_a_plan_passed_back_is_the_same_plan(lib: ctypes.CDLL, cus: int, ab: int
         for layout, trans_a in _PLAN_LAYOUTS:
             if ab == native.DTYPE_F32 and layout == native.B_VNNI_PANELS:
                 continue
-            first = _plan(lib, ab, m, n, k, batch, b_layout=layout, cus=cus, trans_a=trans_a)
+            first = _plan(lib, ab, m, n, k, batch, b_layout=layout, cus=cus, trans_a=trans_a, epi=epi)
             s, tm, tn, tk, ws = first
             again = _plan(lib, ab, m, n, k, batch, splits=s, max_ws=ws, tiles=(tm, tn, tk), b_layout=layout,
-                          cus=cus, trans_a=trans_a)
+                          cus=cus, trans_a=trans_a, epi=epi)
             assert again == first, ((m, n, k, batch, layout, trans_a, cus), first, again)
 
 
@@ -284,7 +316,7 @@ def test_noalloc_refuses_a_plan_beyond_its_scratch(lib: ctypes.CDLL) -> None:
     # scratch holds 64 MiB: refused on the host, before any device call.
     args = (native.DTYPE_F32, native.DTYPE_F32, 256, 8192, 0, 512, 256, native.B_ROW, 0, 0, 1024, 256,
             256, 256, 8192, 16, 256 * 8192, 8192 * 256, 256 * 256, None, None, None, native.DTYPE_F32,
-            native.EPI_IDENTITY, 0.0, 64, 0, 0, 0, None)
+            native.EPI_IDENTITY, 0.0, None, 64, 0, 0, 0, None)
     assert lib.hmx_gemm_noalloc(*args) == native.ERR_INVALID
     assert "scratch" in native.last_error() and str(native.GEMM_SCRATCH_BYTES) in native.last_error()
 

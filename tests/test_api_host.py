@@ -101,16 +101,22 @@ def test_shape_errors_come_first() -> None:
 
 
 def test_epilogue_codes() -> None:
-    assert epilogue_code(U.identity_epilogue) == (native.EPI_IDENTITY, 0.0)
+    assert epilogue_code(U.identity_epilogue) == (native.EPI_IDENTITY, 0.0, None)
     assert epilogue_code(torch.relu)[0] == native.EPI_RELU
     assert epilogue_code(F.silu)[0] == native.EPI_SILU
     assert epilogue_code(torch.sigmoid)[0] == native.EPI_SIGMOID
     assert epilogue_code(F.gelu)[0] == native.EPI_GELU
     assert epilogue_code(functools.partial(F.gelu, approximate="tanh"))[0] == native.EPI_GELU_TANH
-    assert epilogue_code(functools.partial(F.leaky_relu, negative_slope=0.3)) == (native.EPI_LEAKY_RELU, 0.3)
-    assert epilogue_code(U.Activation("leaky_relu", 0.2)) == (native.EPI_LEAKY_RELU, 0.2)
-    with pytest.raises(ValueError, match="cannot fuse the epilogue"):
-        epilogue_code(lambda x: x * 3)
+    assert epilogue_code(functools.partial(F.leaky_relu, negative_slope=0.3)) == (native.EPI_LEAKY_RELU, 0.3, None)
+    assert epilogue_code(U.Activation("leaky_relu", 0.2)) == (native.EPI_LEAKY_RELU, 0.2, None)
+    # Other elementwise callables are traced into programs; one named
+    # activation of the input keeps its code.
+    code, _, program = epilogue_code(lambda x: x * 3)
+    assert code == native.EPI_PROGRAM and program.count == 1
+    assert epilogue_code(lambda x: F.gelu(x, approximate="tanh"))[:2] == (native.EPI_GELU_TANH, 0.0)
+    assert epilogue_code(lambda x: x.float())[0] == native.EPI_IDENTITY
+    with pytest.raises(ValueError, match="cannot fuse"):
+        epilogue_code(lambda x: x.sum())
 
     def double(x: torch.Tensor) -> torch.Tensor:
         return torch.tanh(x)

@@ -1,0 +1,198 @@
+"""Parity of arbitrary elementwise epilogues on the GPU: callables traced into
+epilogue programs (helion_mlir_utils/_program.py) and the named activations,
+on every GEMM kernel family -- the direct-to-LDS kernels run them fused in
+their LDS-staged epilogue; the register-staged bf16 and f32 kernels, split-K
+and the skinny shapes leave them to the split-K reduction -- and on
+group_norm, row_sum and row_dot.
+
+The oracle applies the same callable with torch to its f32 values, as the
+reference applies ``epilogue(acc)`` to its f32 accumulator
+(helion_mlir_utils/matmul.py:321-327) and ``epilogue(y, extra)`` in group_norm
+(normalization.py:121). Tolerances: bf16-in / f32-accumulate rtol 1e-2 plus an
+atol scaled by sqrt(K), times the epilogues' largest slope (3); f32 rtol 1e-4.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+import helion_mlir_utils as U
+from helion_mlir_backend._compiler import native
+from oracle import restate as R
+from tests.helpers import assert_close, bf16_gemm_atol, tensor, to_np
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(23)
+
+EPILOGUES = {
+    "scale3": lambda x: x * 3,
+    "hardswish": F.hardswish,
+    "mish": F.mish,
+    "silu_mix": lambda x: F.silu(x) * 2 - x / 4,
+    "softplus": lambda x: F.softplus(x, beta=2.0, threshold=3.0),
+    "selu": F.selu,
+    "clamp": lambda x: torch.clamp(x, -0.5, 0.5),
+    "gelu_named": F.gelu,
+    "sigmoid_named": torch.sigmoid,
+    "module": nn.Sequential(nn.Hardtanh(-2.0, 2.0), nn.ELU(0.5)),
+}
+
+
+def _operands(m, n, k, trans_a, trans_b, dtype, device):
+    a = tensor(RNG.normal(0, 1, (k, m) if trans_a else (m, k)).astype(np.float32), dtype, device)
+    b = tensor(RNG.normal(0, 1, (n, k) if trans_b else (k, n)).astype(np.float32), dtype, device)
+    return a, b
+
+
+def _check(got, ref, k, a, b, out):
+    if out == "f32":
+        assert_close(got, ref, 1e-4, 3e-5 * np.sqrt(k))
+    else:
+        assert_close(got, ref, 1e-2, 3 * bf16_gemm_atol(k, a, b))
+
+
+# Shapes that reach each kernel family (planned for the device's CUs):
+# (m, n, k, trans_a, trans_b, dtype).
+SHAPES = {
+    "dma_256": (4096, 4096, 128, False, False, "bf16"),   # 256 x 256 tiles, eight waves
+    "dma_256_nk": (4096, 4096, 128, False, True, "bf16"),  # B [N, K]
+    "dma_k32": (4096, 4096, 96, False, False, "bf16"),    # 32-wide K stages
+    "dma_ragged": (4000, 4100, 128, False, True, "bf16"),  # ragged M and N
+    "dma_trans_a": (4096, 4096, 128, True, False, "bf16"),
+    "dma_128": (512, 512, 256, False, False, "bf16"),     # 128 x 128 tiles
+    "bf16_general": (300, 200, 100, False, False, "bf16"),  # K not whole stages: reduction finishes
+    "split_k": (256, 256, 8192, False, False, "bf16"),    # split-K: reduction finishes
+    "skinny_shape": (32, 1024, 256, False, True, "bf16"),  # never the skinny kernel with a program
+    "f32": (300, 200, 130, False, False, "f32"),
+    "f32_split": (512, 512, 512, False, False, "f32"),
+}
+
+
+@pytest.mark.parametrize("shape", list(SHAPES))
+@pytest.mark.parametrize("epi", ["scale3", "hardswish", "silu_mix", "gelu_named", "module"])
+def test_matmul_epilogues_on_every_kernel(gpu_device, shape: str, epi: str) -> None:
+    m, n, k, ta, tb, dtype = SHAPES[shape]
+    fn = EPILOGUES[epi]
+    a, b = _operands(m, n, k, ta, tb, dtype, gpu_device)
+    bias = tensor(RNG.normal(0, 1, n).astype(np.float32), dtype, gpu_device)
+    got = to_np(U.matmul(a, b, trans_a=ta, trans_b=tb, bias=bias, epilogue=fn))
+    ref = R.matmul(to_np(a), to_np(b), ta, tb, to_np(bias), act=fn, out=dtype)
+    _check(got, ref, k, to_np(a), to_np(b), dtype)
+
+
+@pytest.mark.parametrize("epi", list(EPILOGUES))
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+def test_each_epilogue_with_scale_shift_and_f32_output(gpu_device, epi: str, out: str) -> None:
+    m, n, k = 4096, 4096, 64
+    fn = EPILOGUES[epi]
+    a, b = _operands(m, n, k, False, True, "bf16", gpu_device)
+    scale = torch.from_numpy(RNG.uniform(0.5, 1.5, n).astype(np.float32)).to(gpu_device)
+    shift = torch.from_numpy(RNG.normal(0, 0.5, n).astype(np.float32)).to(gpu_device)
+    got = to_np(U.matmul(a, b, trans_b=True, epilogue=fn, scale=scale, shift=shift,
+                         out_dtype=torch.float32 if out == "f32" else None))
+    ref = R.matmul(to_np(a), to_np(b), False, True, None, to_np(scale), to_np(shift), act=fn, out=out)
+    if out == "f32":
+        # bf16 operands, f32 accumulation in different orders: the tolerance
+        # of the products themselves, not of f32 operands.
+        assert_close(got, ref, 1e-4, 2 * 3 * bf16_gemm_atol(k, to_np(a), to_np(b)))
+    else:
+        _check(got, ref, k, to_np(a), to_np(b), out)
+
+
+def test_special_values_through_a_program(gpu_device) -> None:
+    # NaN / inf accumulators through max/min/clamp-based programs: NaN stays
+    # NaN (torch.clamp, torch.maximum), infinities saturate as torch's do.
+    m, n, k = 256, 256, 64
+    a = np.zeros((m, k), np.float32)
+    b = np.zeros((k, n), np.float32)
+    a[:, 0] = np.linspace(-3, 3, m)
+    b[0, :] = 1.0
+    a[0, 1], b[1, 0] = np.inf, 1.0   # C[0, 0] = +inf
+    a[1, 1], b[1, 1] = np.nan, 1.0   # C[1, 1] = NaN
+    a[2, 2], b[2, 2] = -np.inf, 1.0  # C[2, 2] = -inf
+    fn = lambda x: torch.maximum(F.hardswish(x), x * 0.5).clamp(-1.0, 2.0)  # noqa: E731
+    for dtype in ("bf16", "f32"):
+        ta, tb = tensor(a, dtype, gpu_device), tensor(b, dtype, gpu_device)
+        got = to_np(U.matmul(ta, tb, epilogue=fn))
+        ref = R.matmul(to_np(ta), to_np(tb), act=fn, out=dtype)
+        assert_close(got, ref, 1e-2 if dtype == "bf16" else 1e-5, 1e-6)
+
+
+def test_prepacked_and_linear_take_programs(gpu_device) -> None:
+    m, n, k = 512, 768, 256
+    fn = EPILOGUES["silu_mix"]
+    a, w = _operands(m, n, k, False, True, "bf16", gpu_device)
+    bias = tensor(RNG.normal(0, 1, n).astype(np.float32), "bf16", gpu_device)
+    ref = R.matmul(to_np(a), to_np(w), False, True, to_np(bias), act=fn, out="bf16")
+    for panel in (64, 256):
+        got = to_np(U.matmul_prepacked_b(a, U.pack_b_vnni_t(w, panel), n, bias, fn))
+        _check(got, ref, k, to_np(a), to_np(w), "bf16")
+    layer = nn.Linear(k, n, device=gpu_device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        layer.weight.copy_(w)
+        layer.bias.copy_(bias)
+    y, cache = U.linear(a, layer, epilogue=fn)
+    _check(to_np(y), ref, k, to_np(a), to_np(w), "bf16")
+    y2, _ = U.linear(a, layer, epilogue=fn, cache=cache)
+    assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("groups", [1, 32])
+def test_group_norm_programs(gpu_device, dtype: str, groups: int) -> None:
+    m, c = 256, 4096
+    x = tensor(RNG.normal(0, 2, (m, c)).astype(np.float32), dtype, gpu_device)
+    w = torch.from_numpy(RNG.uniform(0.5, 1.5, c).astype(np.float32)).to(gpu_device)
+    b = torch.from_numpy(RNG.normal(0, 0.5, c).astype(np.float32)).to(gpu_device)
+    extra = torch.from_numpy(RNG.normal(0, 1, c).astype(np.float32)).to(gpu_device)
+    fn = lambda y, e: F.silu(y * e + 1) - torch.abs(e)  # noqa: E731
+    got = to_np(U.group_norm(x, groups, w, b, 1e-5, epilogue=fn, extra=extra))
+    ref = R.group_norm(to_np(x), groups, to_np(w), to_np(b), 1e-5, to_np(extra), "callable", fn, out=dtype)
+    assert_close(got, ref, 1e-2 if dtype == "bf16" else 1e-4, 5e-3 if dtype == "bf16" else 1e-4)
+    # No extra operand: the epilogue's second operand is the weight.
+    got = to_np(U.group_norm(x, groups, w, b, 1e-5, epilogue=lambda y, e: y * e))
+    ref = R.group_norm(to_np(x), groups, to_np(w), to_np(b), 1e-5, None, "callable", lambda y, e: y * e, out=dtype)
+    assert_close(got, ref, 1e-2 if dtype == "bf16" else 1e-4, 5e-3 if dtype == "bf16" else 1e-4)
+    # GroupNormEpilogue with an activation that is a program.
+    epi = U.GroupNormEpilogue("add", F.hardswish)
+    got = to_np(U.group_norm(x, groups, w, b, 1e-5, epilogue=epi, extra=extra))
+    ref = R.group_norm(to_np(x), groups, to_np(w), to_np(b), 1e-5, to_np(extra), "callable",
+                       lambda y, e: F.hardswish(y + e), out=dtype)
+    assert_close(got, ref, 1e-2 if dtype == "bf16" else 1e-4, 5e-3 if dtype == "bf16" else 1e-4)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_reduction_programs(gpu_device, dtype: str) -> None:
+    m, n = 1000, 777
+    x = tensor(RNG.normal(0, 1, (m, n)).astype(np.float32), dtype, gpu_device)
+    v = torch.from_numpy(RNG.normal(0, 1, n).astype(np.float32)).to(gpu_device)
+    fn = lambda s: F.softplus(s / 8) * 3  # noqa: E731
+    tol = (1e-2, 1e-2) if dtype == "bf16" else (1e-4, 1e-4)
+    assert_close(to_np(U.row_sum(x, fn)), R.row_sum(to_np(x), fn, out=dtype), *tol)
+    assert_close(to_np(U.row_dot(x, v, fn)), R.row_dot(to_np(x), to_np(v), fn, out=dtype), *tol)
+
+
+def test_noalloc_runs_programs(gpu_device) -> None:
+    # The allocation-free entry point stages the program's f32 products in
+    # its scratch when the kernel leaves the program to the reduction.
+    m, n, k = 300, 200, 100
+    fn = EPILOGUES["mish"]
+    program = U.compile_epilogue(fn)
+    a, b = _operands(m, n, k, False, False, "bf16", gpu_device)
+    c = torch.empty(m, n, dtype=torch.bfloat16, device=gpu_device)
+    stream = torch.cuda.current_stream(gpu_device).cuda_stream
+    status = native.lib().hmx_gemm_noalloc(
+        native.DTYPE_BF16, native.DTYPE_BF16, a.data_ptr(), k, 0, b.data_ptr(), n, native.B_ROW, 0, 0,
+        c.data_ptr(), n, m, n, k, 1, 0, 0, 0, None, None, None, native.DTYPE_F32,
+        native.EPI_PROGRAM, 0.0, ctypes.addressof(program.struct), 0, 0, 0, 0, stream)
+    assert status == native.OK, native.last_error()
+    torch.cuda.synchronize()
+    ref = R.matmul(to_np(a), to_np(b), act=fn, out="bf16")
+    _check(to_np(c), ref, k, to_np(a), to_np(b), "bf16")

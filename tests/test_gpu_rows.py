@@ -178,7 +178,7 @@ def test_group_norm_bf16_vectors_through_the_abi(gpu_device, dtype: str, c: int)
     y = torch.empty_like(x)
     native.call("hmx_group_norm_rows", native.dtype_code(x.dtype), x.data_ptr(), w.data_ptr(), b.data_ptr(),
                 e.data_ptr(), native.DTYPE_BF16, y.data_ptr(), m, groups, c // groups, 1e-5, native.EXTRA_ADD,
-                native.EPI_RELU, 0.0, torch.cuda.current_stream().cuda_stream)
+                native.EPI_RELU, 0.0, None, torch.cuda.current_stream().cuda_stream)
     ref = R.group_norm(to_np(x), groups, to_np(w), to_np(b), 1e-5, to_np(e), "add", "relu", out=dtype)
     rtol, atol = _tol(dtype)
     assert_close(to_np(y), ref, rtol, atol * 10)

@@ -168,6 +168,33 @@ def test_layer_norm_and_group_norm_epilogues() -> None:
     np.testing.assert_allclose(added, np.maximum(ln + extra, 0), rtol=1e-4, atol=2e-4)
     multiplied = R.group_norm(x, 1, w, b, 1e-5, extra, "mul")
     np.testing.assert_allclose(multiplied, ln * extra, rtol=1e-4, atol=2e-4)
+    # A callable epilogue(y, extra) gets the normalized values and the extra
+    # operand broadcast over rows (normalization.py:121); without an extra
+    # operand, the weight (normalization.py:190-192).
+    called = R.group_norm(x, 1, w, b, 1e-5, extra, "callable", lambda y, e: torch.tanh(y) * e - y)
+    np.testing.assert_allclose(called, np.tanh(ln) * extra - ln, rtol=1e-4, atol=2e-4)
+    defaulted = R.group_norm(x, 1, w, b, 1e-5, None, "callable", lambda y, e: y + e)
+    np.testing.assert_allclose(defaulted, ln + w, rtol=1e-4, atol=2e-4)
+
+
+def test_callable_epilogues_are_applied_in_f32() -> None:
+    x = RNG.normal(0, 4, (64, 33)).astype(np.float32)
+    # A callable naming a known activation gives that activation.
+    for name, fn in (("silu", F.silu), ("gelu", F.gelu), ("tanh", torch.tanh), ("relu", torch.relu)):
+        np.testing.assert_allclose(R.apply_epilogue(fn, x), R.activation(name, x), rtol=2e-6, atol=1e-6)
+    # Any other callable: its f32 value (the reference applies it to the f32
+    # accumulator), checked against float64 evaluation.
+    got = R.apply_epilogue(lambda t: F.hardswish(t) * 3 - t / 7, x)
+    ref = (F.hardswish(_f64(x)) * 3 - _f64(x) / 7).numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6)
+    assert got.dtype == np.float32
+    # In the GEMM: after bias, scale and shift, before the one rounding.
+    a = RNG.normal(0, 1, (20, 30)).astype(np.float32)
+    b = RNG.normal(0, 1, (30, 40)).astype(np.float32)
+    bias = RNG.normal(0, 1, 40).astype(np.float32)
+    got = R.matmul(a, b, bias=bias, act=lambda t: F.mish(t) + 1, out="bf16")
+    ref = (F.mish(_f64(a) @ _f64(b) + _f64(bias)) + 1).float().to(torch.bfloat16).float().numpy()
+    np.testing.assert_allclose(got, ref, rtol=2**-7, atol=1e-6)
 
 
 # ---------------------------------------------------------------------------

@@ -27,11 +27,12 @@ pytestmark = pytest.mark.gpu
 RNG = np.random.default_rng(31)
 
 
-def _plan(a: torch.Tensor, m: int, n: int, k: int, batch: int) -> tuple[int, int, int, int, int]:
+def _plan(a: torch.Tensor, m: int, n: int, k: int, batch: int,
+          act: int = native.EPI_IDENTITY) -> tuple[int, int, int, int, int]:
     out = [ctypes.c_int() for _ in range(4)]
     ws = ctypes.c_int64()
     native.check(native.lib().hmx_gemm_plan(native.dtype_code(a.dtype), m, n, k, batch, 0, native.B_ROW, 0, -1,
-                                            0, 0, 0, native.device_units(a.device),
+                                            0, 0, 0, native.device_units(a.device), act,
                                             *[ctypes.byref(o) for o in out], ctypes.byref(ws)), "hmx_gemm_plan")
     return (*[o.value for o in out], ws.value)
 
@@ -47,11 +48,11 @@ def _gemm(a: torch.Tensor, b: torch.Tensor, noalloc: bool, bias: torch.Tensor | 
     head = (native.dtype_code(a.dtype), native.dtype_code(c.dtype), a.data_ptr(), k, 0,
             b.data_ptr(), n, native.B_ROW, 0, 0, c.data_ptr(), n, m, n, k, batch, m * k, k * n, m * n,
             native.ptr(bias), None, None, native.dtype_code(a.dtype) if bias is not None else native.DTYPE_F32,
-            act, 0.0, splits)
+            act, 0.0, None, splits)
     if noalloc:
         status = native.lib().hmx_gemm_noalloc(*head, 0, 0, 0, stream)
     else:
-        ws_bytes = _plan(a, m, n, k, batch)[4] if splits == 0 else 0
+        ws_bytes = _plan(a, m, n, k, batch, act)[4] if splits == 0 else 0
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=a.device)
         status = native.lib().hmx_gemm(*head, ws.data_ptr(), ws_bytes, 0, 0, 0, stream)
     torch.cuda.synchronize()
