@@ -183,6 +183,65 @@ class Gemm(Workload):
                            "sample": f"oracle.restate.matmul (numpy f32 BLAS) on the same rows, {o_reps} reps"}}
 
 
+class GemmLongK(Workload):
+    """bf16 GEMM 4096 x 4096 x 16384 through the library: the steady state of
+    the config-3 kernel (the per-launch fixed cost -- first loads, the
+    epilogue's C writes -- is a quarter as large a share as at K = 4096)."""
+
+    def __init__(self, device) -> None:
+        import torch
+
+        import helion_mlir_utils as U
+
+        g = torch.Generator().manual_seed(2)
+        m = n = 4096
+        k = 16384
+        self.a = (torch.rand(m, k, generator=g) * 2 - 1).to(torch.bfloat16).to(device)
+        self.b = (torch.rand(k, n, generator=g) * 2 - 1).to(torch.bfloat16).to(device)
+        self.U = U
+        self.name = "gemm_longk"
+        self.description = "bf16 GEMM 4096 x 4096 x 16384 (config 3 kernel, long K)"
+        self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_BF16_TFLOPS
+        self.work = 2.0 * m * n * k
+        self.dtype = "bf16"
+        self.kernel = "gemm_bf16_dma64_kernel"
+        self.config = {"workload": self.description, "m": m, "n": n, "k": k, "seed": 2, "values": "U[-1,1]"}
+
+    def step(self):
+        return self.U.matmul(self.a, self.b)
+
+    def cpu_baseline(self) -> dict:
+        return {"value": None, "unit": "TFLOP/s", "cores": 0, "kind": "port", "sample": "none (steady-state probe)"}
+
+
+class VendorGemm(Workload):
+    """torch.matmul (hipBLASLt) on config 3's operands, or on the long-K
+    shape: the vendor library's kernel as a reference point for clock and
+    MFMA-utilisation counters, not a hot-path op."""
+
+    def __init__(self, device, k: int = 4096) -> None:
+        import torch
+
+        g = torch.Generator().manual_seed(2)
+        m = n = 4096
+        self.a = (torch.rand(m, k, generator=g) * 2 - 1).to(torch.bfloat16).to(device)
+        self.b = (torch.rand(k, n, generator=g) * 2 - 1).to(torch.bfloat16).to(device)
+        self.name = "gemm_hipblaslt" if k == 4096 else "gemm_longk_hipblaslt"
+        self.description = f"torch.matmul (hipBLASLt) bf16 4096 x 4096 x {k} (reference point)"
+        self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_BF16_TFLOPS
+        self.work = 2.0 * m * n * k
+        self.dtype = "bf16"
+        self.kernel = "Cijk"
+        self.library_kernels = False
+        self.config = {"workload": self.description, "m": m, "n": n, "k": k, "seed": 2, "values": "U[-1,1]"}
+
+    def step(self):
+        return self.a @ self.b
+
+    def cpu_baseline(self) -> dict:
+        return {"value": None, "unit": "TFLOP/s", "cores": 0, "kind": "port", "sample": "none (reference point)"}
+
+
 class Linear(Workload):
     def __init__(self, device) -> None:
         import torch
@@ -557,6 +616,9 @@ def make(name: str, device) -> Workload:
         "gemm": lambda: Gemm(device),
         "gemm_f32c": lambda: Gemm(device, "f32"),
         "gemm_prepacked": lambda: Gemm(device, prepacked=True),
+        "gemm_longk": lambda: GemmLongK(device),
+        "gemm_hipblaslt": lambda: VendorGemm(device),
+        "gemm_longk_hipblaslt": lambda: VendorGemm(device, 16384),
         "linear": lambda: Linear(device),
         "linear_decode": lambda: LinearDecode(device),
         "softmax": lambda: RowOp(device, "softmax", "bf16"),

@@ -30,55 +30,11 @@
 // compiler's own waits for other memory operations stay correct.
 #include <cstdlib>
 
-#include "hmx_gemm_common.hpp"
+#include "hmx_gemm_lds.hpp"
 
 namespace hmx {
 namespace {
 
-typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ i32x4_t make_srd(const void* p, int32_t bytes) {
-  const uint64_t a = (uint64_t)p;
-  return i32x4_t{(int32_t)(uint32_t)a, (int32_t)((a >> 32) & 0xffff), bytes, 0x00020000};
-}
-
-// One 16-byte-per-lane load from buffer `srd` at voff + soff bytes into LDS
-// bytes [lds, lds + 1024) (lane l at lds + 16 l). An LDS load must not read M0
-// in the cycle after the SALU write of it (one wait state, the s_nop). The
-// kernel has no other use of M0, so clobbering it is safe. NT: the load is
-// non-temporal (streamed past the caches' retention), for operand data no
-// other workgroup reads: the split-K bf16 bmm of config 5 runs 203 -> 189 us
-// with it, while GEMMs whose tiles share panels through L2 run 15 % slower.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-template <bool NT = false>
-__device__ __forceinline__ void lds_dma16(i32x4_t srd, int32_t voff, int32_t soff, uint32_t lds) {
-  if constexpr (NT)
-    asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen nt lds"
-                 :: "v"(voff), "s"(srd), "s"(soff), "s"(lds) : "memory", "m0");
-  else
-    asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-                 :: "v"(voff), "s"(srd), "s"(soff), "s"(lds) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-template <int N>
-__device__ __forceinline__ void wait_vmem() {
-  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
-}
-
-__device__ __forceinline__ int swz_k(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
-__device__ __forceinline__ int swz_n(int r) { return ((r & 3) << 1) ^ ((r & 3) << 2); }
-__device__ __forceinline__ int swz64(int r) { return (r >> 1) & 7; }
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
-}
-
-__device__ __forceinline__ bf16x4_t lds_read_tr(const uint8_t* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_t*)p);
-}
 
 // One instantiation per B orientation, register-epilogue class and C dtype:
 // a single straight-line epilogue keeps the accumulators out of scratch.
@@ -587,6 +543,231 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
 }
 
 // ---------------------------------------------------------------------------
+// The eight-wave 64-wide kernel with v_mfma_f32_16x16x32_bf16 in place of
+// 32x32x16: whole 256 x 256 tiles, B [N, K] or [K, N], K chunks of whole
+// 64-element stages, the register epilogue (identity, ReLU, SiLU). The tiles,
+// their swizzles, the loads and the waves' 128 x 64 outputs are those of
+// gemm_bf16_dma64_kernel; each wave's outputs are 8 x 4 fragments of 16 x 16.
+// A stage is two k-steps of 32 (32 MFMAs each). The GEMM runs at the power
+// limit, where what counts is the energy per flop: with random bf16 operands
+// a stream of 16x16x32 MFMAs sustains 12 % more than one of 32x32x16 (each
+// moves half the accumulator bytes per flop through the register file).
+//
+// Fragments (lane l, 16-lane group g = l / 16): A (and K-contiguous B) row
+// l % 16 of the fragment, K values 8 g .. 8 g + 7 of the k-step (16-byte
+// chunk 4 ks + g of the 128-byte tile row, slot chunk ^ swz64(row)); row-major
+// B through two transposing reads, of K rows 32 ks + 8 g + 0..3 and + 4..7, lane
+// s of each group addressing row + s / 4, columns n + 4 (s % 4) .. + 3 of the
+// fragment's 16, so lane j receives column n + j (chunk slot 2 j' + (s % 4) / 2
+// ^ swz_n(s / 4), byte 8 (s % 2)). An accumulator holds column l % 16, rows
+// 4 g .. 4 g + 3.
+//
+// Slots: 64 MFMAs per stage. The first 12 slots of k-step 0 read k-step 1's
+// fragments; at slot 32 the wave waits for its loads of stage t + 1 and its
+// reads of stage t, and the barrier publishes t + 1 and frees t; slots 32-51
+// issue the 8 loads of stage t + 2 into it and slots 52-63 read stage t + 1's
+// k-step 0 fragments.
+template <int LB, int ACT, bool BF16>
+__global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
+  static_assert(LB == L_KCONTIG || LB == L_RCONTIG, "B [N, K] or [K, N]");
+  static_assert(ACT == ACT_ID || ACT == ACT_RELU || ACT == ACT_SILU, "register epilogue");
+  typedef float f32x4_t __attribute__((ext_vector_type(4)));
+  constexpr bool BT = LB == L_RCONTIG;
+  constexpr int NW = 8, BM = 256, BN = 256, BK = 64;
+  constexpr int ROWB = BK * 2, NROWB = BN * 2;
+  constexpr int A_BYTES = BM * ROWB;            // 32 KiB
+  constexpr int STAGE = A_BYTES + BN * BK * 2;  // 64 KiB
+  constexpr int WM = 128, WN = 64, FM = 8, FN = 4;
+  constexpr int LA = BM / 8 / NW, LBN = BN / 8 / NW, LOADS = LA + LBN;  // 4 + 4
+  constexpr int NS = FM * FN, SLOTS = 2 * NS, NF = FM + FN;            // 32, 64, 12
+  constexpr int BAR = NS, LOAD_END = SLOTS - NF;                         // 32, 52
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
+
+  int tm, tn;
+  tile_coords(g.tiles_m, g.tiles_n, g.xcds, tm, tn);
+  const int split = blockIdx.y, batch = blockIdx.z;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t k_begin = (int64_t)split * g.k_chunk;
+  const int64_t k_end = min(g.k, k_begin + g.k_chunk);
+  const int ktiles = (int)((k_end - k_begin) / BK);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / 4, wn = wave % 4;
+
+  const i32x4_t srd_a = make_srd((const uint16_t*)g.a.p + batch * g.stride_a, g.a.bytes);
+  const i32x4_t srd_b = make_srd((const uint16_t*)g.b.p + batch * g.stride_b, g.b.bytes);
+  // Loads, as gemm_bf16_dma64_kernel with eight waves: wave w copies tile rows
+  // 32 w .. 32 w + 31 of A (and of K-contiguous B), 8 rows per 1 KiB load, or
+  // K rows 8 w .. 8 w + 7 of row-major B in pairs.
+  const int rr = lane >> 3, slot = lane & 7;
+  auto kc_voff = [&](int64_t ld, int par) {
+    return (int32_t)((rr * ld + (slot ^ ((rr >> 1) | (par << 2))) * 8) * 2);
+  };
+  const int32_t voff_a0 = kc_voff(g.a.ld, 0), voff_a1 = kc_voff(g.a.ld, 1);
+  const int32_t soff_a = (int32_t)((m0 + wave * (BM / NW)) * g.a.ld * 2);
+  const int32_t blk_a = (int32_t)(8 * g.a.ld * 2);
+  int32_t voff_b0, voff_b1, soff_b, blk_b;
+  if constexpr (BT) {
+    const int r = lane >> 5, c = lane & 31;
+    voff_b0 = (int32_t)((r * g.b.ld + (c ^ swz_n(r)) * 8) * 2);
+    voff_b1 = (int32_t)((r * g.b.ld + (c ^ swz_n(r + 2)) * 8) * 2);
+    soff_b = (int32_t)((wave * (64 / NW) * g.b.ld + n0) * 2);
+    blk_b = (int32_t)(2 * g.b.ld * 2);
+  } else {
+    voff_b0 = kc_voff(g.b.ld, 0);
+    voff_b1 = kc_voff(g.b.ld, 1);
+    soff_b = (int32_t)((n0 + wave * (BN / NW)) * g.b.ld * 2);
+    blk_b = (int32_t)(8 * g.b.ld * 2);
+  }
+  const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + wave * LA * 1024;
+  const uint32_t lds_wb = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + A_BYTES + wave * LBN * 1024;
+  auto dma = [&](int t, int q) {
+    const int64_t k0 = k_begin + (int64_t)min(t, ktiles - 1) * BK;
+    const uint32_t st = lds_w + (uint32_t)((t & 1) * STAGE);
+    const uint32_t sb = lds_wb + (uint32_t)((t & 1) * STAGE);
+    if (q < LA) {
+      lds_dma16(srd_a, (q & 1) ? voff_a1 : voff_a0, soff_a + q * blk_a + (int32_t)(k0 * 2), st + q * 1024);
+    } else {
+      const int qb = q - LA;
+      const int32_t kb = BT ? (int32_t)(k0 * g.b.ld * 2) : (int32_t)(k0 * 2);
+      lds_dma16(srd_b, (qb & 1) ? voff_b1 : voff_b0, soff_b + qb * blk_b + kb, sb + qb * 1024);
+    }
+  };
+
+  f32x4_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int frow = lane & 15, fg = lane >> 4, fswz = swz64(frow);
+  const uint8_t* a_frag = lds + (wm * WM + frow) * ROWB;
+  const uint8_t* b_frag = lds + A_BYTES + (wn * WN + frow) * ROWB;
+  int b_tr[FN];
+  {
+    const int sl = lane & 15;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      b_tr[j] = A_BYTES + (8 * fg + (sl >> 2)) * NROWB +
+                ((wn * (WN / 8) + 2 * j + ((sl & 3) >> 1)) ^ swz_n(sl >> 2)) * 16 + 8 * (sl & 1);
+  }
+  auto a_read = [&](int stage, int ks, int i) -> bf16x8_t {
+    return *(const bf16x8_t*)(a_frag + stage * STAGE + i * 16 * ROWB + ((4 * ks + fg) ^ fswz) * 16);
+  };
+  auto b_read = [&](int stage, int ks, int j) -> bf16x8_t {
+    if constexpr (BT) {
+      const uint8_t* p = lds + stage * STAGE + b_tr[j] + 32 * ks * NROWB;
+      return __builtin_shufflevector(lds_read_tr(p), lds_read_tr(p + 4 * NROWB), 0, 1, 2, 3, 4, 5, 6, 7);
+    } else {
+      return *(const bf16x8_t*)(b_frag + stage * STAGE + j * 16 * ROWB + ((4 * ks + fg) ^ fswz) * 16);
+    }
+  };
+
+  // The host launches this kernel only with at least one K stage per split.
+  bf16x8_t fa[2][FM], fb[2][FN];
+#pragma unroll
+  for (int q = 0; q < LOADS; ++q) dma(0, q);
+#pragma unroll
+  for (int q = 0; q < LOADS; ++q) dma(1, q);
+  wait_vmem<LOADS>();  // stage 0 landed
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < FM; ++i) fa[0][i] = a_read(0, 0, i);
+#pragma unroll
+  for (int j = 0; j < FN; ++j) fb[0][j] = b_read(0, 0, j);
+
+  for (int t = 0; t < ktiles; ++t) {
+    const int cur = t & 1, nxt = cur ^ 1;
+#pragma unroll
+    for (int x = 0; x < SLOTS; ++x) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int ks = x / NS, sub = x % NS;
+      if (x == BAR) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (ks == 0 && sub < NF) {
+        if (sub < FM) fa[1][sub] = a_read(cur, 1, sub);
+        else fb[1][sub - FM] = b_read(cur, 1, sub - FM);
+      }
+      // The stage's loads, spread over the slots from the barrier to the
+      // next stage's fragment reads.
+#pragma unroll
+      for (int q = (x - BAR) * LOADS / (LOAD_END - BAR); q < (x + 1 - BAR) * LOADS / (LOAD_END - BAR); ++q)
+        if (x >= BAR && x < LOAD_END) dma(t + 2, q);
+      if (x >= SLOTS - NF) {
+        const int f = x - (SLOTS - NF);
+        if (f < FM) fa[0][f] = a_read(nxt, 0, f);
+        else fb[0][f - FM] = b_read(nxt, 0, f - FM);
+      }
+      const int i = sub / FN, j = sub % FN;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  wait_vmem<0>();  // no load into LDS outlives the loop
+
+  // Epilogue: lane l finishes column l % 16 of each fragment, rows
+  // 4 g .. 4 g + 3 (bias, scale, shift, activation, one rounding).
+  const int64_t off = split * g.stride_split + batch * g.stride_c;
+  const bool odd = lane & 1;
+  if constexpr (BF16) {
+    // bf16 C goes through LDS (free once every wave is done with the last
+    // stage) as the whole 256 x 256 tile, 512-byte rows whose 16-byte chunk c
+    // sits in slot c ^ cswz(row), then leaves in whole rows: written straight
+    // from the fragments, each store would cover 32-byte pieces of 8 rows,
+    // and the tile's writes would cost ~25 us per launch more. Lanes 2c and
+    // 2c + 1 exchange rows so that each writes one 4-byte word (two columns);
+    // the 8 rows x 32 bytes of one LDS write meet 16 distinct chunk slots.
+    auto cswz = [](int r) { return 2 * ((r & 1) | (((r >> 2) & 3) << 1)); };
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int cl = wn * WN + j * 16 + (lane & 15);  // tile column
+      float bias, scale, shift;
+      column_vectors(g, n0 + cl, true, bias, scale, shift);
+      const int pc = cl & ~1;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const float v0 = activate<ACT>((acc[i][j][2 * q] + bias) * scale + shift);
+          const float v1 = activate<ACT>((acc[i][j][2 * q + 1] + bias) * scale + shift);
+          const float recv = swap_pair(odd ? v0 : v1);
+          const int r = wm * WM + i * 16 + 4 * fg + 2 * q + (odd ? 1 : 0);
+          const uint32_t word = odd ? pack_bf16x2(recv, v1) : pack_bf16x2(v0, recv);
+          *(uint32_t*)(lds + r * 512 + (((pc >> 3) ^ cswz(r)) << 4) + (pc & 7) * 2) = word;
+        }
+      }
+    }
+    __syncthreads();
+    // Wave w stores tile rows 32 w .. 32 w + 31, two rows per instruction
+    // (lanes 0-31 and 32-63, 16 bytes each).
+    uint16_t* c = (uint16_t*)g.c + off;
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      const int r = wave * 32 + 2 * p + (lane >> 5), ch = lane & 31;
+      const uint4 v = *(const uint4*)(lds + r * 512 + ((ch ^ cswz(r)) << 4));
+      store16_stream(c + (m0 + r) * g.ldc + n0 + ch * 8, v);
+    }
+  } else {
+    float* c = (float*)g.c + off;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int64_t col = n0 + wn * WN + j * 16 + (lane & 15);
+      float bias, scale, shift;
+      column_vectors(g, col, true, bias, scale, shift);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int64_t row0 = m0 + wm * WM + i * 16 + 4 * fg;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          store_c32(c + (row0 + e) * g.ldc + col,
+                    __float_as_uint(activate<ACT>((acc[i][j][e] + bias) * scale + shift)));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // f32 direct-to-LDS kernel (v_mfma_f32_32x32x2_f32) for whole 256 x 256 tiles
 // of long-K split-K products: row-major A, B [N, K] or [K, N], f32 partials
 // with the identity epilogue. The register-staged f32 kernel has to hold the
@@ -942,8 +1123,31 @@ __global__ __launch_bounds__(NW * 64) void gemm_bf16_skinny_kernel(GemmArgs g) {
   }
 }
 
+// The 16x16x32 MFMA kernel for the eight-wave 256 x 256 tiles unless the
+// environment sets HMX_GEMM_MFMA=32 (the 32x32x16 kernel, for comparison).
+bool mfma16_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("HMX_GEMM_MFMA");
+    return !(e && e[0] == '3');
+  }();
+  return on;
+}
+
 template <int LB, bool BF16, bool K64, int NW = 4>
 void launch_bf16_dma_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  if constexpr (K64 && NW == 8 && (LB == L_KCONTIG || LB == L_RCONTIG)) {
+    // bf16 C leaves the 16x16x32 kernel in 16-byte row pieces.
+    const bool rows16 = !BF16 || ((((uintptr_t)g.c) & 15) == 0 && g.ldc % 8 == 0 && g.stride_c % 8 == 0 &&
+                                  g.stride_split % 8 == 0);
+    if (!g.k_stagger && rows16 && mfma16_enabled()) {
+      switch (g.act) {
+        case HMX_EPI_IDENTITY: launch(gemm_bf16_mi16_kernel<LB, ACT_ID, BF16>, grid, 512, s, g); return;
+        case HMX_EPI_RELU: launch(gemm_bf16_mi16_kernel<LB, ACT_RELU, BF16>, grid, 512, s, g); return;
+        case HMX_EPI_SILU: launch(gemm_bf16_mi16_kernel<LB, ACT_SILU, BF16>, grid, 512, s, g); return;
+        default: break;
+      }
+    }
+  }
   if constexpr (K64) {
     if constexpr (!BF16 && NW == 8 && (LB == L_KCONTIG || LB == L_RCONTIG)) {
       // Split-K grids of one tile per slice (k_stagger): no other workgroup

@@ -108,6 +108,16 @@ def _kernel_weight(weight: Tensor, panel: int | None) -> Tensor:
     return weight.contiguous()
 
 
+def _row_tiles(x: Tensor, n: int, k: int, whole_rows: bool, panel: int | None) -> tuple[int, int] | None:
+    """The ``(rows, columns)`` whole-row tiles a ``whole_rows`` call asks for
+    (bf16, even K: :func:`~.heuristics.whole_row_tiles`), else None."""
+    if not whole_rows or x.dtype != torch.bfloat16 or k % 2 or x.dim() != 2:
+        return None
+    from .heuristics import whole_row_tiles
+
+    return whole_row_tiles(int(x.shape[0]), n, panel)
+
+
 def _launcher(
     x: Tensor,
     weight: Tensor,
@@ -116,12 +126,14 @@ def _launcher(
     epilogue: Callable[[Tensor], Tensor],
     scale: Tensor | None = None,
     shift: Tensor | None = None,
+    tile_m: int | None = None,
 ) -> Callable[[Tensor], Tensor]:
     """A prepared ``epilogue((x @ W^T + bias) * scale + shift)`` for inputs of
-    ``x``'s shape, dtype and device; any other input goes through the general
-    entry point, which checks it."""
+    ``x``'s shape, dtype and device (``tile_m``: the workgroup rows asked
+    for); any other input goes through the general entry point, which checks
+    it."""
     if weight.dim() != 2:  # VNNI panels
-        return prepacked_b_call(x, weight, n, bias, epilogue, scale, shift)
+        return prepacked_b_call(x, weight, n, bias, epilogue, scale, shift, tile_m=tile_m)
 
     def general(a: Tensor) -> Tensor:
         return matmul(a, weight, trans_b=True, bias=bias, epilogue=epilogue, scale=scale, shift=shift)
@@ -135,6 +147,7 @@ def _launcher(
     launch = GemmLaunch(
         native.dtype_code(x.dtype), x.dtype, x.device, (m, n), k, False, k, native.B_TRANS, 0, 0, m, n, k,
         bias=vec_bias, scale=vec_scale, shift=vec_shift, vec_dtype=vec_dtype, epilogue=epilogue_code(epilogue),
+        tiles=(tile_m, 0, 0) if tile_m else None,
     )
     return prepared_call(lambda a: launch.run(a, weight), [x], general)
 
@@ -162,22 +175,28 @@ def linear(
 
     ``biases`` replaces ``layer.bias`` by the sum of the given vectors.
     ``panel`` keeps a bf16 weight as VNNI panels of that many columns.
-    ``whole_rows`` asks that each row block of ``x`` be read by one cache
-    domain: on the GPU each 256-row block of the output's tiles is walked by
-    the workgroups of one XCD, which share its L2, whatever the flag says; it
-    is kept in the cache key, as in the reference."""
+    ``whole_rows`` (bf16, even ``in_features``, cached weights) takes the
+    reference's whole-row tiles (``linear.py:88-94,156-171``): the weight is
+    kept as VNNI panels of the tile's columns and the launch asks for the
+    tile's rows (:func:`~.heuristics.whole_row_tiles`, the GPU tile table's
+    answer); shapes it cannot tile keep the default launch. The results are
+    those of the default launch. The flag is part of the cache key, as in the
+    reference."""
     parts = tuple(biases) if biases is not None else (() if layer.bias is None else (layer.bias,))
     if not cache_prepacked_weights():
         y = matmul(x, _as_input(x, layer.weight), trans_b=True, bias=_one_bias(parts, x), epilogue=epilogue)
         return y, None
     key = (_fingerprint(layer.weight), tuple(_fingerprint(p) for p in parts), x.dtype, x.device,
            x.shape[0], panel, bool(whole_rows))
+    tiles = _row_tiles(x, int(layer.out_features), int(layer.in_features), whole_rows, panel)
     if cache is None or cache.key != key:
-        cache = LinearCache(key, _kernel_weight(_as_input(x, layer.weight), panel), _one_bias(parts, x),
-                            int(layer.out_features))
+        cache = LinearCache(key, _kernel_weight(_as_input(x, layer.weight), tiles[1] if tiles else panel),
+                            _one_bias(parts, x), int(layer.out_features))
     fresh = cache
     call, cache = _with_call(
-        cache, epilogue, lambda: _launcher(x, fresh.packed_weight, fresh.out_features, fresh.bias, epilogue)
+        cache, epilogue,
+        lambda: _launcher(x, fresh.packed_weight, fresh.out_features, fresh.bias, epilogue,
+                          tile_m=tiles[0] if tiles else None),
     )
     return call(x), cache
 

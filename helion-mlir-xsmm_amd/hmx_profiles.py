@@ -4,13 +4,18 @@ launch from counter runs.
 
     python helion-mlir-xsmm_amd/hmx_profiles.py trace WORKLOAD TRACE_DIR BENCH_LOG OUT.md "TITLE" "COMMAND"
     python helion-mlir-xsmm_amd/hmx_profiles.py traffic PMC_ROOT OUT.json
+    python helion-mlir-xsmm_amd/hmx_profiles.py clock PMC_ROOT OUT.md "TITLE" "COMMAND"
 
 ``TRACE_DIR`` holds ``run_kernel_trace.csv`` and ``run_kernel_stats.csv`` of
 ``rocprofv3 --kernel-trace --stats -o run -f csv -- python3 bench.py
 --workload WORKLOAD --steps S ...``; ``BENCH_LOG`` is that run's stderr (the
 ``bench:`` lines). ``PMC_ROOT`` holds one directory per counter run, named
 ``<tag>_<workload>`` (tag ``rd``: ``TCC_EA0_RDREQ_{32B,64B,128B}_sum``; tag
-``wr``: ``WRITE_SIZE``), each with ``run_counter_collection.csv``.
+``wr``: ``WRITE_SIZE``), each with ``run_counter_collection.csv``. For
+``clock``, ``PMC_ROOT`` holds one directory per workload, each a counter run
+with ``GRBM_GUI_ACTIVE`` and ``SQ_VALU_MFMA_BUSY_CYCLES`` (and its
+``run_agent_info.csv``): the clock each GEMM dispatch ran at and the share of
+SIMD cycles its MFMA unit was busy.
 """
 
 from __future__ import annotations
@@ -106,10 +111,49 @@ def traffic(pmc_root: Path) -> dict:
     return out
 
 
+def clock_summary(pmc_root: Path, title: str, command: str, last: int = 50) -> str:
+    """Per workload (a directory of ``pmc_root``): over the last ``last``
+    dispatches of its longest-running kernel, the mean duration, the clock
+    (GRBM_GUI_ACTIVE cycles, counted once per XCD, over the duration), the
+    MFMA-busy share of SIMD cycles (SQ_VALU_MFMA_BUSY_CYCLES, summed over the
+    SIMDs, over the XCD's cycles times the SIMD count) and their product, the
+    MFMA cycles per SIMD per nanosecond."""
+    out = [f"# {title}", "", "Command:", "", "```", command, "```", "",
+           "| Workload | Kernel | Dispatches | Duration (us) | Clock (GHz) | MFMA busy | Busy x clock |",
+           "|---|---|---|---|---|---|---|"]
+    for run in sorted(p for p in pmc_root.iterdir() if p.is_dir()):
+        path = run / "run_counter_collection.csv"
+        if not path.is_file():
+            continue
+        agent = next((r for r in _rows(run / "run_agent_info.csv") if r.get("Name", "").startswith("gfx")), {})
+        xcc, simds = int(agent.get("Num_Xcc", 8)), int(agent.get("Simd_Count", 1024))
+        disp: dict[int, dict] = collections.defaultdict(dict)
+        for r in _rows(path):
+            d = disp[int(r["Dispatch_Id"])]
+            d["name"] = r["Kernel_Name"]
+            d["dur"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            d[r["Counter_Name"]] = float(r["Counter_Value"])
+        totals: dict[str, float] = collections.defaultdict(float)
+        for d in disp.values():
+            totals[d["name"]] += d["dur"]
+        name = max(totals, key=totals.get)
+        rows = [d for _, d in sorted(disp.items()) if d["name"] == name][-last:]
+        dur = sum(d["dur"] for d in rows) / len(rows)
+        clocks = [d["GRBM_GUI_ACTIVE"] / xcc / (d["dur"] * 1e3) for d in rows]
+        busy = [d["SQ_VALU_MFMA_BUSY_CYCLES"] / simds / (d["GRBM_GUI_ACTIVE"] / xcc) for d in rows]
+        clk, util = sum(clocks) / len(rows), sum(busy) / len(rows)
+        out.append(f"| {run.name} | `{kernel_name(name)[:70]}` | {len(rows)} | {dur:.1f} | {clk:.3f} | "
+                   f"{util:.3f} | {clk * util:.3f} |")
+    return "\n".join(out) + "\n"
+
+
 def main(argv: list[str]) -> int:
     if len(argv) >= 7 and argv[1] == "trace":
         _, _, workload, trace_dir, log, out, title, command = argv[:8]
         Path(out).write_text(trace_summary(workload, Path(trace_dir), Path(log), title, command))
+        return 0
+    if len(argv) == 6 and argv[1] == "clock":
+        Path(argv[3]).write_text(clock_summary(Path(argv[2]), argv[4], argv[5]))
         return 0
     if len(argv) == 4 and argv[1] == "traffic":
         Path(argv[3]).write_text(json.dumps(traffic(Path(argv[2])), indent=1, sort_keys=True) + "\n")

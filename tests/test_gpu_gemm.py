@@ -342,6 +342,26 @@ def test_linear_affine_and_panel(gpu_device) -> None:
     _check(to_np(yp), R.matmul(xs, ws, False, True, bs, act="relu", out="bf16"), 96, xs, ws, "bf16")
 
 
+@pytest.mark.parametrize(("m", "n", "k"), [(1024, 1536, 512), (512, 11008, 256), (300, 768, 128)])
+def test_linear_whole_rows(gpu_device, m: int, n: int, k: int) -> None:
+    # whole_rows takes the whole-row tiles (the weight as VNNI panels of the
+    # tile's columns, the tile's rows asked for): the same products as the
+    # default launch, bit for bit, and its own cache entry.
+    layer = torch.nn.Linear(k, n).to(device=gpu_device, dtype=torch.bfloat16)
+    x = tensor(RNG.normal(0, 1, (m, k)).astype(np.float32), "bf16", gpu_device)
+    with torch.no_grad():
+        y, cache = U.linear(x, layer, F.silu)
+        yw, cache_w = U.linear(x, layer, F.silu, whole_rows=True)
+        yw2, cache_w2 = U.linear(x, layer, F.silu, cache=cache_w, whole_rows=True)
+    assert cache_w.key != cache.key and cache_w2.call is cache_w.call
+    tiles = U.whole_row_tiles(m, n)
+    if tiles is not None:
+        assert cache_w.packed_weight.dim() == 4 and cache_w.packed_weight.shape[2] == tiles[1]
+    assert torch.equal(y, yw) and torch.equal(yw, yw2)
+    xs, ws, bs = to_np(x), to_np(layer.weight), to_np(layer.bias)
+    _check(to_np(yw), R.matmul(xs, ws, False, True, bs, act="silu", out="bf16"), k, xs, ws, "bf16")
+
+
 # ---------------------------------------------------------------------------
 # bmm / split-K
 
