@@ -151,7 +151,8 @@ class Gemm(Workload):
         self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_BF16_TFLOPS
         self.work = 2.0 * m * n * k
         self.dtype = "bf16"
-        self.kernel = "gemm_bf16_dma64_kernel"
+        # Blocked VNNI B runs the 32x32x16 direct-to-LDS kernel; row-major B the 16x16x32 one.
+        self.kernel = "gemm_bf16_dma64_kernel" if prepacked else "gemm_bf16_mi16_kernel"
         self.config = {"workload": self.description, "m": m, "n": n, "k": k, "a": "bf16 row-major",
                        "b": "bf16 row-major" if not prepacked else "bf16 [N/32,K/32,16,32,2]",
                        "c": out_dtype_name, "seed": 2, "values": "U[-1,1]"}
@@ -204,7 +205,7 @@ class GemmLongK(Workload):
         self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_BF16_TFLOPS
         self.work = 2.0 * m * n * k
         self.dtype = "bf16"
-        self.kernel = "gemm_bf16_dma64_kernel"
+        self.kernel = "gemm_bf16_mi16_kernel"
         self.config = {"workload": self.description, "m": m, "n": n, "k": k, "seed": 2, "values": "U[-1,1]"}
 
     def step(self):
@@ -265,7 +266,7 @@ class Linear(Workload):
         self.work = 2.0 * 8192 * 11008 * 4096
         self.dtype = "bf16"
         # 256x256 tiles over the first 10240 columns (five rounds), then 256x128 tiles over the last 768.
-        self.kernel = "gemm_bf16_dma64_kernel (256x256, then 256x128 tail)"
+        self.kernel = "gemm_bf16_mi16_kernel (256x256), then gemm_bf16_dma64_kernel (256x128 tail)"
         self.config = {"workload": self.description, "m": 8192, "n": 11008, "k": 4096, "seed": 3}
 
     def step(self):

@@ -86,13 +86,20 @@ def traffic(pmc_root: Path) -> dict:
         if not path.is_file() or tag not in ("rd", "wr"):
             continue
         last: dict[tuple[str, str], tuple[int, float]] = {}
+        dispatches: dict[str, set] = collections.defaultdict(set)
         for r in _rows(path):
             key = (kernel_name(r["Kernel_Name"]), r["Counter_Name"])
             disp = int(r.get("Dispatch_Id") or r.get("Correlation_Id") or 0)
+            dispatches[key[0]].add(disp)
             if key not in last or disp >= last[key][0]:
                 last[key] = (disp, float(r["Counter_Value"]))
+        # The step's kernels run on every step; kernels of the workload's
+        # set-up (input copies, a one-time pack) run once or twice.
+        most = max((len(d) for d in dispatches.values()), default=0)
         per_kernel: dict[str, float] = collections.defaultdict(float)
         for (kernel, counter), (_, value) in last.items():
+            if len(dispatches[kernel]) < most / 2:
+                continue
             if tag == "rd":
                 size = {"TCC_EA0_RDREQ_32B_sum": 32, "TCC_EA0_RDREQ_64B_sum": 64,
                         "TCC_EA0_RDREQ_128B_sum": 128}.get(counter)
@@ -104,10 +111,24 @@ def traffic(pmc_root: Path) -> dict:
             result[workload]["kernels"][kernel]["read_bytes" if tag == "rd" else "write_bytes"] = int(value)
     out = {}
     for workload, entry in sorted(result.items()):
-        kernels = {k: dict(v) for k, v in entry["kernels"].items()
-                   if "hmx" in k or "copy" in k.lower() or not k.startswith("void at::")}
+        kernels = {k: dict(v) for k, v in entry["kernels"].items()}
         total = sum(v.get("read_bytes", 0) + v.get("write_bytes", 0) for v in kernels.values())
         out[workload] = {"kernels": kernels, "bytes_per_launch": total}
+    method = {
+        "read_bytes": "32 * TCC_EA0_RDREQ_32B_sum + 64 * TCC_EA0_RDREQ_64B_sum + 128 * TCC_EA0_RDREQ_128B_sum "
+                      "(requests from L2 to the memory fabric, by size: HBM and MALL hits alike)",
+        "write_bytes": "WRITE_SIZE * 1024",
+        "dispatch": "the last dispatch of each kernel that runs on every step (set-up kernels excluded); "
+                    "bytes_per_launch sums the step's kernels",
+    }
+    copy = out.get("copy")
+    if copy:
+        moved = 32768 * 8192 * 2  # the copy workload reads and writes 512 MiB
+        rd = sum(v.get("read_bytes", 0) for v in copy["kernels"].values())
+        wr = sum(v.get("write_bytes", 0) for v in copy["kernels"].values())
+        method["calibration"] = (f"copy workload (torch copy of 512 MiB): read {rd / moved:.4f}, write "
+                                 f"{wr / moved:.4f} of the bytes moved")
+    out["_method"] = method
     return out
 
 
