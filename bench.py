@@ -430,8 +430,8 @@ class MemOp(Workload):
             self.work = {"layernorm": 2 * rw + 8 * n, "groupnorm": 2 * rw + 8 * n, "row_sum": rw + 2 * m,
                          "column_sum": rw + 4 * n, "row_dot": rw + 4 * n + 2 * m, "matvec": rw + 2 * n + 2 * m,
                          "relu": 2 * rw}[op]
-            self.kernel = {"layernorm": "group_norm_cached", "groupnorm": "group_norm_cached",
-                           "row_sum": "row_reduce", "column_sum": "column_sum_kernel", "row_dot": "row_reduce",
+            self.kernel = {"layernorm": "group_norm_rows", "groupnorm": "group_norm_rows",
+                           "row_sum": "row_reduce", "column_sum": "column_partial_kernel + column_final_kernel", "row_dot": "row_reduce",
                            "matvec": "row_reduce", "relu": "elementwise_kernel"}[op]
             self.description = f"{op} [{m}, {n}] bf16 (config 2's X)"
             self.config = {"workload": self.description, "m": m, "n": n, "seed": 1, "values": "N(0, std 2)"}

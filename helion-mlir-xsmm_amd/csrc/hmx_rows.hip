@@ -14,6 +14,7 @@
 // values per lane, 5 waves per SIMD). Rows longer than the register cache
 // (16 waves x 64 values per lane) stream through the same math in chunks, one
 // wave per row.
+#include <atomic>
 #include <type_traits>
 #include <utility>
 
@@ -461,6 +462,160 @@ __global__ __launch_bounds__(kMaxBlock) void group_norm_cached(const T* x, T* y,
   store_row<T, EPV, VPL, WHOLE>(y + unit * n, n, p.li, p.tpr, v);
 }
 
+// Sums of VPL per-lane values, value j over the gv lanes that hold vector j
+// of one group (gv a power of two dividing the row's thread count, lanes
+// aligned to it). gv > 64: the waves' partials meet in `slot` (VPL x
+// kMaxWavesPerRow floats, one array per call site) and each thread adds its
+// group's waves in wave order.
+template <int VPL>
+__device__ __forceinline__ void group_sums(float (&s)[VPL], int gv, float* slot) {
+  for (int off = (gv < kWave ? gv : kWave) >> 1; off > 0; off >>= 1) {
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) s[j] += __shfl_xor(s[j], off, kWave);
+  }
+  if (gv > kWave) {
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) slot[j * kMaxWavesPerRow + wave] = s[j];
+    }
+    __syncthreads();
+    const int wpg = gv / kWave;
+    const int w0 = wave - wave % wpg;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      float t = slot[j * kMaxWavesPerRow + w0];
+      for (int q = 1; q < wpg; ++q) t += slot[j * kMaxWavesPerRow + w0 + q];
+      s[j] = t;
+    }
+  }
+}
+
+// Raw 16-byte vectors of one row, as load_row reads them (whole rows only).
+template <typename T, int EPV, int VPL>
+__device__ __forceinline__ void load_row_raw(const T* __restrict__ p, int li, int tpr, uint4 (&raw)[VPL]) {
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const T* q = p + ((int64_t)j * tpr + li) * EPV;
+    if constexpr (std::is_same_v<T, float>) {
+      const u32x4_t nt = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(q));
+      raw[j] = make_uint4(nt[0], nt[1], nt[2], nt[3]);
+    } else {
+      raw[j] = *reinterpret_cast<const uint4*>(q);
+    }
+  }
+}
+
+// GroupNorm / LayerNorm over whole rows of G groups, each workgroup walking
+// many rows with w, b (and the extra operand's per-channel vector) of its
+// lanes' columns held in registers: they are read once per workgroup instead
+// of once per row. Re-read per row, f32 w and b move 4x a bf16 row's bytes
+// through L2, which then bounds the kernel rather than HBM. The next row's x
+// is loaded before the current row is reduced. The row (n = G * gs channels)
+// is whole: n == tpr * VPL * EPV; a group is gv = gs / EPV vectors, either
+// the whole row (ONE) or a power of two dividing tpr, so vector j of a lane
+// belongs to the group of the gv aligned lanes around it. Statistics are
+// f32: mean, then the centered variance, per group.
+template <typename T, int EPV, int VPL, bool ONE, bool EXTRA>
+__global__ __launch_bounds__(kMaxBlock) void group_norm_rows(const T* x, T* y, GroupNormArgs a,
+                                                             int64_t rows, int tpr, int gv) {
+  __shared__ float red_mean[VPL * kMaxWavesPerRow], red_var[VPL * kMaxWavesPerRow];
+  const int rpb = tpr <= kWave ? (int)blockDim.x / tpr : 1;
+  const int li = (int)threadIdx.x % tpr;
+  int64_t row = (int64_t)blockIdx.x * rpb + threadIdx.x / tpr;
+  const int64_t step = (int64_t)gridDim.x * rpb;
+  // Threads of one row share `row` (tpr > 64: the whole workgroup), so an
+  // early return never skips a barrier another thread of the row waits at.
+  if (row >= rows) return;
+  const int64_t n = a.gs * a.groups;
+  float wv[VPL * EPV], bv[VPL * EPV], ev[EXTRA ? VPL * EPV : 1];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int64_t col0 = col_of<EPV>(j, li, tpr, 0);
+    float t[EPV];
+    load_vec_any<EPV>(a.w, a.vec_dtype, col0, t, 1.f);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) wv[j * EPV + e] = t[e];
+    load_vec_any<EPV>(a.b, a.vec_dtype, col0, t, 0.f);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) bv[j * EPV + e] = t[e];
+    if constexpr (EXTRA) {
+      load_vec_any<EPV>(a.extra, a.vec_dtype, col0, t, 0.f);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) ev[j * EPV + e] = t[e];
+    }
+  }
+  const float inv_n = 1.f / (float)(ONE ? n : a.gs);
+  uint4 cur[VPL];
+  load_row_raw<T, EPV, VPL>(x + row * n, li, tpr, cur);
+  for (;;) {
+    const int64_t next = row + step;
+    uint4 nxt[VPL];
+    if (next < rows) load_row_raw<T, EPV, VPL>(x + next * n, li, tpr, nxt);
+    float v[VPL * EPV];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) Elem<T>::unpack(cur[j], &v[j * EPV]);
+    float mean[VPL], r[VPL];
+    if constexpr (ONE) {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < VPL * EPV; ++i) s += v[i];
+      const float m0 = row_sum_all(s, red_mean, tpr) / (float)n;
+      float q = 0.f;
+#pragma unroll
+      for (int i = 0; i < VPL * EPV; ++i) q += (v[i] - m0) * (v[i] - m0);
+      const float r0 = rsqrtf(row_sum_all(q, red_var, tpr) / (float)n + a.eps);
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        mean[j] = m0;
+        r[j] = r0;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) s += v[j * EPV + e];
+        mean[j] = s;
+      }
+      group_sums<VPL>(mean, gv, red_mean);
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        mean[j] *= inv_n;
+        float q = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) q += (v[j * EPV + e] - mean[j]) * (v[j * EPV + e] - mean[j]);
+        r[j] = q;
+      }
+      group_sums<VPL>(r, gv, red_var);
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) r[j] = rsqrtf(r[j] * inv_n + a.eps);
+    }
+    float ex[VPL * EPV];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) {
+        const int i = j * EPV + e;
+        float yv = (v[i] - mean[j]) * r[j] * wv[i];
+        yv += bv[i];
+        if constexpr (EXTRA) {
+          if (a.extra_op == HMX_EXTRA_ADD) yv += ev[i];
+          if (a.extra_op == HMX_EXTRA_MUL) yv *= ev[i];
+        }
+        v[i] = yv;
+        ex[i] = 0.f;
+      }
+    }
+    group_norm_finish<VPL * EPV, false>(a, v, ex);
+    store_row<T, EPV, VPL, true>(y + row * n, n, li, tpr, v);
+    if (next >= rows) break;
+    row = next;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) cur[j] = nxt[j];
+  }
+}
+
 template <typename T, int EPV, bool PROG>
 __global__ __launch_bounds__(kBlock) void group_norm_stream(const T* x,
                                                             T* y,
@@ -546,26 +701,23 @@ __global__ __launch_bounds__(kBlock) void row_reduce(const T* x,
   if (lane == 0) Elem<T>::store(y + row, s);
 }
 
-// Column sums: one thread per column walks all rows (each row read by a wave
-// as one contiguous run); f32 accumulation in row order.
 // Column sums in two passes, so that every CU streams rows and the result
 // does not depend on scheduling. Pass 1: workgroup (b, c) sums the rows of
-// chunk c for the 64 columns of block b: 64 / EPV threads across the columns
-// (one 16-byte vector each, a whole 128- or 256-byte line per row) times
-// 256 / (64 / EPV) threads down the rows, which are then added in thread
-// order through LDS; the chunk's sums go to `part` ([chunks, n] f32), or
-// straight to y (+ 0.0) when there is one chunk. Pass 2 adds the chunks in
-// chunk order.
-constexpr int kColBlock = 64;
-
-template <typename T, int EPV>
+// chunk c for the TC * EPV columns of block b: TC threads across the columns
+// (one 16-byte vector each; TC = 64 reads a contiguous 1 KiB piece of every
+// row, where 128-byte pieces streamed ~20% slower) times 256 / TC threads
+// down the rows, eight rows in flight per thread; the threads' sums are then
+// added in thread order through LDS. The chunk's sums go to `part`
+// ([chunks, n] f32), or straight to y (+ 0.0) when there is one chunk.
+// Pass 2 adds the chunks in chunk order.
+template <typename T, int EPV, int TC>
 __global__ __launch_bounds__(256) void column_partial_kernel(const T* x, float* __restrict__ part,
                                                              int64_t m, int64_t n, int64_t rows_per_chunk,
                                                              bool final) {
-  constexpr int TC = kColBlock / EPV, TR = 256 / TC;
-  __shared__ float sums[TR][kColBlock];
+  constexpr int CB = TC * EPV, TR = 256 / TC, U = 8;
+  __shared__ float sums[TR][CB];
   const int tc = threadIdx.x % TC, tr = threadIdx.x / TC;
-  const int64_t col = (int64_t)blockIdx.x * kColBlock + tc * EPV;
+  const int64_t col = (int64_t)blockIdx.x * CB + tc * EPV;
   const int64_t r0 = (int64_t)blockIdx.y * rows_per_chunk;
   const int64_t r1 = min(m, r0 + rows_per_chunk);
   float acc[EPV];
@@ -573,13 +725,12 @@ __global__ __launch_bounds__(256) void column_partial_kernel(const T* x, float* 
   for (int e = 0; e < EPV; ++e) acc[e] = 0.f;
   if (col < n) {
     int64_t r = r0 + tr;
-    // Four rows in flight per thread.
-    for (; r + 3 * TR < r1; r += 4 * TR) {
-      float v[4][EPV];
+    for (; r + (U - 1) * TR < r1; r += U * TR) {
+      float v[U][EPV];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) load_chunk<T, EPV>(x + (r + u * TR) * n, n, col, v[u], 0.f);
+      for (int u = 0; u < U; ++u) load_chunk<T, EPV>(x + (r + u * TR) * n, n, col, v[u], 0.f);
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < U; ++u)
 #pragma unroll
         for (int e = 0; e < EPV; ++e) acc[e] += v[u][e];
     }
@@ -593,34 +744,51 @@ __global__ __launch_bounds__(256) void column_partial_kernel(const T* x, float* 
 #pragma unroll
   for (int e = 0; e < EPV; ++e) sums[tr][tc * EPV + e] = acc[e];
   __syncthreads();
-  if (threadIdx.x < kColBlock) {
-    const int64_t c = (int64_t)blockIdx.x * kColBlock + threadIdx.x;
-    float s = sums[0][threadIdx.x];
-    for (int q = 1; q < TR; ++q) s += sums[q][threadIdx.x];
+  for (int k = threadIdx.x; k < CB; k += 256) {
+    const int64_t c = (int64_t)blockIdx.x * CB + k;
+    float t = sums[0][k];
+    for (int q = 1; q < TR; ++q) t += sums[q][k];
     if (c < n) {
-      if (final) part[c] = s + 0.f;
-      else part[blockIdx.y * n + c] = s;
+      if (final) part[c] = t + 0.f;
+      else part[blockIdx.y * n + c] = t;
     }
   }
 }
 
+// Pass 2: each column's chunk sums in chunk order, split over kFinalSplit
+// threads per column (thread t adds its run of consecutive chunks in order,
+// eight loads in flight) whose sums are added in t order through LDS: a
+// fixed order, so the result is the same on every run.
+constexpr int kFinalCols = 32, kFinalSplit = 8;
+
 __global__ __launch_bounds__(256) void column_final_kernel(const float* __restrict__ part,
                                                            float* __restrict__ y, int64_t chunks,
                                                            int64_t n) {
-  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= n) return;
-  // Loads in batches of 8 (independent, in flight together), added in order.
+  __shared__ float red[kFinalSplit][kFinalCols];
+  const int lc = threadIdx.x % kFinalCols, t = threadIdx.x / kFinalCols;
+  const int64_t c = (int64_t)blockIdx.x * kFinalCols + lc;
+  const int64_t per = (chunks + kFinalSplit - 1) / kFinalSplit;
+  const int64_t q1 = min(chunks, (t + 1) * per);
   float s = 0.f;
-  int64_t q = 0;
-  for (; q + 8 <= chunks; q += 8) {
-    float v[8];
+  if (c < n) {
+    int64_t q = t * per;
+    for (; q + 8 <= q1; q += 8) {
+      float v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = part[(q + u) * n + c];
+      for (int u = 0; u < 8; ++u) v[u] = part[(q + u) * n + c];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) s += v[u];
+      for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; q < q1; ++q) s += part[q * n + c];
   }
-  for (; q < chunks; ++q) s += part[q * n + c];
-  y[c] = s + 0.f;
+  red[t][lc] = s;
+  __syncthreads();
+  if (t == 0 && c < n) {
+    float v = red[0][lc];
+#pragma unroll
+    for (int u = 1; u < kFinalSplit; ++u) v += red[u][lc];
+    y[c] = v + 0.f;
+  }
 }
 
 // Elementwise ops over 16-byte vectors (EPV elements), scalar tail.
@@ -740,6 +908,25 @@ bool rows_vectorizable(const void* p, const void* q, int64_t n, int dtype) {
 
 dim3 unit_grid(int64_t units) { return dim3((unsigned)ceil_div(units, kRowsPerBlock)); }
 
+// How many workgroups of `block` threads of `kernel` one CU holds at once,
+// read from the runtime once per kernel and block size (1 if it cannot say).
+// A kernel whose workgroups walk many rows launches no more than fit, so
+// that none waits for another to finish.
+template <auto Kernel>
+int resident_blocks(int block) {
+  static std::atomic<int> known[5];  // block = 64 << i
+  int i = 0;
+  while (i < 4 && (kWave << i) < block) ++i;
+  int b = known[i].load(std::memory_order_relaxed);
+  if (b > 0) return b;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, Kernel, block, 0) != hipSuccess || b < 1) {
+    (void)hipGetLastError();
+    b = 1;
+  }
+  known[i].store(b, std::memory_order_relaxed);
+  return b;
+}
+
 // The largest workgroup count of a one-dimensional launch.
 constexpr int64_t kMaxGrid = 0x7fffffff;
 
@@ -856,6 +1043,38 @@ int hmx_group_norm_rows(int dtype, const void* x, const void* w, const void* b,
       launch(group_norm_stream<T, EPV, true>, unit_grid(units), kBlock, s, (const T*)x, (T*)y, a);
       return;
     }
+    if constexpr (EPV > 1) {
+      // Whole rows in registers when the row fits and each group is one run
+      // of aligned lanes (or the whole row): w, b and extra stay resident.
+      const int64_t row_n = groups * group_size;
+      const RowShape rr = row_shape(row_n, EPV);
+      const int64_t gv = group_size / EPV;
+      const bool one = groups == 1;
+      if (a.vec_ok && rr.vpl > 0 && rr.whole && (one || ((gv & (gv - 1)) == 0 && gv <= rr.tpr))) {
+        const int rpb = rr.tpr <= kWave ? (int)(kBlock / rr.tpr) : 1;
+        const unsigned block = row_block(rr);
+        with_vpl<EPV>(rr.vpl, [&](auto vpl_c) {
+          constexpr int VPL = decltype(vpl_c)::value;
+          auto go = [&](auto one_c, auto extra_c) {
+            constexpr auto kernel = &group_norm_rows<T, EPV, VPL, decltype(one_c)::value, decltype(extra_c)::value>;
+            // As many workgroups as the GPU holds at once, each walking rows
+            // blockIdx, blockIdx + grid, ...
+            const int64_t resident = (int64_t)resident_blocks<kernel>((int)block) * current_device_shape().cus;
+            launch(kernel, dim3((unsigned)std::min(ceil_div(m, rpb), resident)), block, s, (const T*)x, (T*)y, a,
+                   m, rr.tpr, (int)gv);
+          };
+          const bool extra = extra_op != HMX_EXTRA_NONE;
+          if (one) {
+            if (extra) go(std::true_type{}, std::true_type{});
+            else go(std::true_type{}, std::false_type{});
+          } else {
+            if (extra) go(std::false_type{}, std::true_type{});
+            else go(std::false_type{}, std::false_type{});
+          }
+        });
+        return;
+      }
+    }
     if (r.vpl == 0) {
       launch(group_norm_stream<T, EPV, false>, unit_grid(units), kBlock, s, (const T*)x, (T*)y, a);
       return;
@@ -915,9 +1134,11 @@ int hmx_matvec(int dtype, const void* a, const void* x, void* y, int64_t m, int6
 }
 
 // Row chunks of a column sum: about 2048 workgroups, at least 256 rows each.
+// Row chunks of pass 1: about 1024 workgroups over the column blocks of
+// 512 columns, at least 256 rows per chunk.
 static void column_chunks(int64_t m, int64_t n, int64_t& chunks, int64_t& rows_per_chunk) {
-  const int64_t blocks = std::max<int64_t>(1, ceil_div(n, kColBlock));
-  chunks = std::max<int64_t>(1, std::min(ceil_div(2048, blocks), ceil_div(m, 256)));
+  const int64_t blocks = std::max<int64_t>(1, ceil_div(n, 512));
+  chunks = std::max<int64_t>(1, std::min(ceil_div(1024, blocks), ceil_div(m, 256)));
   rows_per_chunk = ceil_div(m, chunks);
   chunks = rows_per_chunk > 0 ? ceil_div(m, rows_per_chunk) : 1;
 }
@@ -938,21 +1159,31 @@ int hmx_column_sum(int dtype, const void* x, float* y, int64_t m, int64_t n, voi
   if (n == 0) return HMX_OK;
   int64_t chunks, rows;
   column_chunks(m, n, chunks, rows);
-  HMX_REQUIRE(chunks <= 65535 && ceil_div(n, kColBlock) <= kMaxGrid, "column_sum: too many columns");
+  HMX_REQUIRE(chunks <= 65535 && ceil_div(n, 8) <= kMaxGrid, "column_sum: too many columns");
   const int64_t need = chunks > 1 ? chunks * n * (int64_t)sizeof(float) : 0;
   HMX_REQUIRE(need == 0 || (workspace && workspace_bytes >= need),
               "column_sum: workspace of %lld bytes needed (hmx_column_sum_plan), %lld given",
               (long long)need, (long long)workspace_bytes);
   auto s = (hipStream_t)stream;
   float* part = chunks > 1 ? (float*)workspace : y;
-  const dim3 grid((unsigned)ceil_div(n, kColBlock), (unsigned)chunks);
   with_type(dtype, rows_vectorizable(x, x, n, dtype), [&](auto tp, auto epv_c) {
     using T = std::remove_pointer_t<decltype(tp)>;
     constexpr int EPV = decltype(epv_c)::value;
-    launch(column_partial_kernel<T, EPV>, grid, 256, s, (const T*)x, part, m, n, rows, chunks == 1);
+    // The fewest threads across (8 to 64) whose vectors span the row.
+    const int64_t vecs = ceil_div(n, EPV);
+    auto go = [&](auto tc_c) {
+      constexpr int TC = decltype(tc_c)::value;
+      const dim3 grid((unsigned)ceil_div(n, TC * EPV), (unsigned)chunks);
+      launch(column_partial_kernel<T, EPV, TC>, grid, 256, s, (const T*)x, part, m, n, rows, chunks == 1);
+    };
+    if (vecs <= 8) go(IntC<8>{});
+    else if (vecs <= 16) go(IntC<16>{});
+    else if (vecs <= 32) go(IntC<32>{});
+    else go(IntC<64>{});
   });
   if (chunks > 1)
-    launch(column_final_kernel, dim3((unsigned)ceil_div(n, 256)), 256, s, (const float*)part, y, chunks, n);
+    launch(column_final_kernel, dim3((unsigned)ceil_div(n, kFinalCols)), 256, s, (const float*)part, y, chunks,
+           n);
   return check_launch("column_sum");
 }
 

@@ -212,8 +212,8 @@ def test_column_sum_plan_and_workspace_check(lib: ctypes.CDLL) -> None:
         assert lib.hmx_column_sum_plan(m, n, ctypes.byref(ws)) == 0
         return ws.value
 
-    # 64 column blocks x 32 chunks of 1024 rows: [32, 4096] f32 partials.
-    assert plan(32768, 4096) == 32 * 4096 * 4
+    # 8 blocks of 512 columns x 128 chunks of 256 rows: [128, 4096] f32 partials.
+    assert plan(32768, 4096) == 128 * 4096 * 4
     # Enough column blocks (or too few rows) for one pass: no workspace.
     assert plan(16, 100000) == 0
     assert plan(0, 10) == 0

@@ -168,6 +168,34 @@ def test_group_norm_lane_groups(gpu_device, groups: int, dtype: str) -> None:
     assert_close(got, ref, rtol, atol * 10)
 
 
+@pytest.mark.parametrize(
+    ("m", "c", "groups", "extra"),
+    [(20000, 4096, 1, False), (20000, 4096, 32, True), (100003, 256, 16, False), (5001, 2048, 2, True),
+     (3001, 16384, 4, False)],
+)
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_group_norm_walks_many_rows(gpu_device, m: int, c: int, groups: int, extra: bool, dtype: str) -> None:
+    # More rows than the GPU holds workgroups at once: each workgroup of the
+    # whole-row kernel normalizes many rows, loading the next row while it
+    # reduces the current one, with w, b and extra held across rows (f32
+    # vectors, as the benchmark passes them). Rows sampled from the start,
+    # the end and between are checked against the oracle.
+    gen = torch.Generator(device=gpu_device).manual_seed(m + c + groups)
+    x = (torch.randn(m, c, device=gpu_device, generator=gen) * 3 + 1.5).to(torch.bfloat16 if dtype == "bf16" else torch.float32)
+    w, b, e = (torch.randn(c, device=gpu_device, generator=gen) for _ in range(3))
+    y = U.group_norm(x, groups, w, b, 1e-5, torch.add, e) if extra else U.group_norm(x, groups, w, b, 1e-5)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([np.arange(8), m - 8 + np.arange(8), RNG.choice(m, 240, replace=False)]))
+    idx = torch.from_numpy(rows).to(gpu_device)
+    xs, ws, bs, es = to_np(x[idx]), to_np(w), to_np(b), to_np(e)
+    if extra:
+        ref = R.group_norm(xs, groups, ws, bs, 1e-5, es, "add", out=dtype)
+    else:
+        ref = R.group_norm(xs, groups, ws, bs, 1e-5, out=dtype)
+    rtol, atol = _tol(dtype)
+    assert_close(to_np(y[idx]), ref, rtol, atol * 10)
+
+
 @pytest.mark.parametrize(("dtype", "c"), [("bf16", 4096), ("f32", 4096), ("bf16", 1000)])
 def test_group_norm_bf16_vectors_through_the_abi(gpu_device, dtype: str, c: int) -> None:
     # bf16 weight, bias and extra operand (the C ABI takes either vector
@@ -228,6 +256,18 @@ def test_column_sum_row_chunks(gpu_device, m: int, n: int, dtype: str) -> None:
     xs = to_np(x)
     assert_close(to_np(got), R.column_sum(xs), 1e-4, 1e-4 * np.sqrt(m))
     assert_close(to_np(U.column_sum(x[1:])), R.column_sum(xs[1:]), 1e-4, 1e-4 * np.sqrt(m))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_column_sum_benchmark_shape(gpu_device, dtype: str) -> None:
+    # The benchmark's [32768, 4096]: 128 row chunks of 256 rows over column
+    # blocks of 1 KiB row pieces, chunk sums added in order by 8 threads per
+    # column. Against the oracle on the whole tensor, and stable run to run.
+    gen = torch.Generator(device=gpu_device).manual_seed(7)
+    x = torch.randn(32768, 4096, device=gpu_device, generator=gen).to(torch.bfloat16 if dtype == "bf16" else torch.float32)
+    got = U.column_sum(x)
+    assert torch.equal(got, U.column_sum(x))
+    assert_close(to_np(got), R.column_sum(to_np(x)), 1e-4, 1e-4 * np.sqrt(32768))
 
 
 @pytest.mark.parametrize("numel", [1, 7, 4096, 1000003])
