@@ -152,7 +152,7 @@ class Gemm(Workload):
         self.work = 2.0 * m * n * k
         self.dtype = "bf16"
         # Blocked VNNI B runs the 32x32x16 direct-to-LDS kernel; row-major B the 16x16x32 one.
-        self.kernel = "gemm_bf16_dma64_kernel" if prepacked else "gemm_bf16_mi16_kernel"
+        self.kernel = "gemm_bf16_mi16_kernel"
         self.config = {"workload": self.description, "m": m, "n": n, "k": k, "a": "bf16 row-major",
                        "b": "bf16 row-major" if not prepacked else "bf16 [N/32,K/32,16,32,2]",
                        "c": out_dtype_name, "seed": 2, "values": "U[-1,1]"}

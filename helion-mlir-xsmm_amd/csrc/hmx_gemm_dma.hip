@@ -544,8 +544,8 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
 
 // ---------------------------------------------------------------------------
 // The eight-wave 64-wide kernel with v_mfma_f32_16x16x32_bf16 in place of
-// 32x32x16: whole 256 x 256 tiles, B [N, K] or [K, N], K chunks of whole
-// 64-element stages, the register epilogue (identity, ReLU, SiLU). The tiles,
+// 32x32x16: whole 256 x 256 tiles, B [N, K], [K, N] or packed (VNNI panels,
+// K-major panels, 32 x 32 blocks), K chunks of whole 64-element stages, the register epilogue (identity, ReLU, SiLU). The tiles,
 // their swizzles, the loads and the waves' 128 x 64 outputs are those of
 // gemm_bf16_dma64_kernel; each wave's outputs are 8 x 4 fragments of 16 x 16.
 // A stage is two k-steps of 32 (32 MFMAs each). The GEMM runs at the power
@@ -569,10 +569,16 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
 // k-step 0 fragments.
 template <int LB, int ACT, bool BF16>
 __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
-  static_assert(LB == L_KCONTIG || LB == L_RCONTIG, "B [N, K] or [K, N]");
+  static_assert(LB == L_KCONTIG || LB == L_RCONTIG || LB == L_VNNI_PANELS || LB == L_PANELS || LB == L_BLOCKED,
+                "B [N, K], [K, N], VNNI panels, K-major panels or 32 x 32 blocks");
   static_assert(ACT == ACT_ID || ACT == ACT_RELU || ACT == ACT_SILU, "register epilogue");
   typedef float f32x4_t __attribute__((ext_vector_type(4)));
-  constexpr bool BT = LB == L_RCONTIG;
+  // Packed B as in gemm_bf16_dma64_kernel: K-major panels and 32 x 32 blocks
+  // land in LDS as the row-major [64 k][256 n] tile (BT), VNNI panels as
+  // copied.
+  constexpr bool BPK = LB == L_PANELS || LB == L_BLOCKED;
+  constexpr bool BT = LB == L_RCONTIG || BPK;
+  constexpr bool VN = LB == L_VNNI_PANELS;
   constexpr int NW = 8, BM = 256, BN = 256, BK = 64;
   constexpr int ROWB = BK * 2, NROWB = BN * 2;
   constexpr int A_BYTES = BM * ROWB;            // 32 KiB
@@ -608,7 +614,40 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
   const int32_t soff_a = (int32_t)((m0 + wave * (BM / NW)) * g.a.ld * 2);
   const int32_t blk_a = (int32_t)(8 * g.a.ld * 2);
   int32_t voff_b0, voff_b1, soff_b, blk_b;
-  if constexpr (BT) {
+  int32_t vn_off[VN ? LBN : 1];
+  const int64_t P = g.b.panel;
+  const int PL = (int)min<int64_t>(P, 256);
+  if constexpr (VN) {
+    // 1 KiB pieces of the stage's 32 K pairs x 256 columns, in the order of
+    // gemm_bf16_dma64_kernel (runs of 128 P bytes for P <= 256, else 1 KiB
+    // pair rows 4 P bytes apart), copied to LDS unchanged.
+    voff_b0 = voff_b1 = lane * 16;
+    soff_b = blk_b = 0;
+#pragma unroll
+    for (int q = 0; q < LBN; ++q) {
+      const int64_t idx = wave * LBN + q;
+      int64_t off;
+      if (P <= 256) {
+        const int64_t b = idx * 1024, run = 128 * P;
+        off = ((n0 / P + b / run) * (g.b.kpad / 2)) * 4 * P + b % run;
+      } else {
+        off = ((n0 / P) * (g.b.kpad / 2) + idx) * 4 * P + (n0 % P) * 4;
+      }
+      vn_off[q] = (int32_t)off;
+    }
+  } else if constexpr (BPK) {
+    // Element (k, n) at col(n) + row(k); a lane's 8 columns stay in one panel
+    // or block, the lane offset holds col(n) and the row within the K pair.
+    const int r = lane >> 5, c = lane & 31;
+    auto col = [&](int64_t n) -> int64_t {
+      if constexpr (LB == L_PANELS) return (n / P) * g.b.kpad * P + n % P;
+      else return (n >> 5) * (g.b.kpad >> 5) * 1024 + (n & 31);
+    };
+    const int64_t rs = LB == L_PANELS ? P : 32;
+    voff_b0 = (int32_t)((col(n0 + (c ^ swz_n(r)) * 8) + r * rs) * 2);
+    voff_b1 = (int32_t)((col(n0 + (c ^ swz_n(r + 2)) * 8) + r * rs) * 2);
+    soff_b = blk_b = 0;
+  } else if constexpr (BT) {
     const int r = lane >> 5, c = lane & 31;
     voff_b0 = (int32_t)((r * g.b.ld + (c ^ swz_n(r)) * 8) * 2);
     voff_b1 = (int32_t)((r * g.b.ld + (c ^ swz_n(r + 2)) * 8) * 2);
@@ -628,6 +667,14 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
     const uint32_t sb = lds_wb + (uint32_t)((t & 1) * STAGE);
     if (q < LA) {
       lds_dma16(srd_a, (q & 1) ? voff_a1 : voff_a0, soff_a + q * blk_a + (int32_t)(k0 * 2), st + q * 1024);
+    } else if constexpr (VN) {
+      const int qb = q - LA;
+      lds_dma16(srd_b, voff_b0, vn_off[qb] + (int32_t)((k0 / 2) * 4 * P), sb + qb * 1024);
+    } else if constexpr (BPK) {
+      const int qb = q - LA;
+      const int64_t kr = k0 + wave * (64 / NW) + 2 * qb;  // even
+      const int64_t row = LB == L_PANELS ? kr * P : (kr >> 5) * 1024 + (kr & 31) * 32;
+      lds_dma16(srd_b, (qb & 1) ? voff_b1 : voff_b0, (int32_t)(row * 2), sb + qb * 1024);
     } else {
       const int qb = q - LA;
       const int32_t kb = BT ? (int32_t)(k0 * g.b.ld * 2) : (int32_t)(k0 * 2);
@@ -655,8 +702,26 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
   auto a_read = [&](int stage, int ks, int i) -> bf16x8_t {
     return *(const bf16x8_t*)(a_frag + stage * STAGE + i * 16 * ROWB + ((4 * ks + fg) ^ fswz) * 16);
   };
+  // VNNI B: column n = wn * 64 + 16 j + lane % 16 needs K pairs
+  // 16 ks + 4 (lane / 16) .. + 3 (4 PL bytes apart), i.e. K values
+  // 32 ks + 8 (lane / 16) .. + 7 -- the MFMA's operand.
+  int b_vn[VN ? FN : 1];
+  const int pair_pitch = 4 * PL;
+  if constexpr (VN) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = wn * WN + 16 * j + frow;
+      b_vn[j] = A_BYTES + (n / PL) * 32 * pair_pitch + (n % PL) * 4 + 4 * fg * pair_pitch;
+    }
+  }
   auto b_read = [&](int stage, int ks, int j) -> bf16x8_t {
-    if constexpr (BT) {
+    if constexpr (VN) {
+      const uint8_t* p = lds + stage * STAGE + b_vn[j] + 16 * ks * pair_pitch;
+      const uint4 v = make_uint4(*(const uint32_t*)p, *(const uint32_t*)(p + pair_pitch),
+                                 *(const uint32_t*)(p + 2 * pair_pitch),
+                                 *(const uint32_t*)(p + 3 * pair_pitch));
+      return __builtin_bit_cast(bf16x8_t, v);
+    } else if constexpr (BT) {
       const uint8_t* p = lds + stage * STAGE + b_tr[j] + 32 * ks * NROWB;
       return __builtin_shufflevector(lds_read_tr(p), lds_read_tr(p + 4 * NROWB), 0, 1, 2, 3, 4, 5, 6, 7);
     } else {
@@ -1135,7 +1200,8 @@ bool mfma16_enabled() {
 
 template <int LB, bool BF16, bool K64, int NW = 4>
 void launch_bf16_dma_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
-  if constexpr (K64 && NW == 8 && (LB == L_KCONTIG || LB == L_RCONTIG)) {
+  if constexpr (K64 && NW == 8 &&
+                (LB == L_KCONTIG || LB == L_RCONTIG || LB == L_VNNI_PANELS || LB == L_PANELS || LB == L_BLOCKED)) {
     // bf16 C leaves the 16x16x32 kernel in 16-byte row pieces.
     const bool rows16 = !BF16 || ((((uintptr_t)g.c) & 15) == 0 && g.ldc % 8 == 0 && g.stride_c % 8 == 0 &&
                                   g.stride_split % 8 == 0);
