@@ -151,7 +151,7 @@ class Gemm(Workload):
         self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_BF16_TFLOPS
         self.work = 2.0 * m * n * k
         self.dtype = "bf16"
-        # Blocked VNNI B runs the 32x32x16 direct-to-LDS kernel; row-major B the 16x16x32 one.
+        # Row-major and blocked VNNI B both run the 16x16x32 direct-to-LDS kernel.
         self.kernel = "gemm_bf16_mi16_kernel"
         self.config = {"workload": self.description, "m": m, "n": n, "k": k, "a": "bf16 row-major",
                        "b": "bf16 row-major" if not prepacked else "bf16 [N/32,K/32,16,32,2]",
