@@ -858,7 +858,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
 // and frees t; step 3 then reads t + 1's first fragments and issues the
 // wave's 16 (8) loads of stage t + 2 into t's buffer from slot 8 on, three
 // steps ahead of their use.
-template <int LB, int NW = 4>
+template <int LB, int NW = 4, int ACT = ACT_ID, bool BF16 = false>
 __global__ __launch_bounds__(NW * 64, 1) void gemm_f32_dma_kernel(GemmArgs g) {
   static_assert(NW == 4 || NW == 8, "f32 waves");
   constexpr bool BT = LB == L_RCONTIG;             // B row-major [K, N]
@@ -1011,7 +1011,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_f32_dma_kernel(GemmArgs g) {
     __builtin_amdgcn_sched_barrier(0);
   }
   wait_vmem<0>();  // no load into LDS outlives the loop
-  epilogue_direct<FM, FN, WM, WN, false, ACT_ID, false>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
+  epilogue_direct<FM, FN, WM, WN, false, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
 }
 
 // Skinny products: at most 64 rows of row-major A against B [N, K] (a
@@ -1447,10 +1447,28 @@ void launch_gemm_f32_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {
     return e && e[0] == '4' ? 4 : 8;
   }();
   if (waves == 8) {
-    if (lb == L_RCONTIG)
-      launch(gemm_f32_dma_kernel<L_RCONTIG, 8>, grid, 512, s, g);
-    else
-      launch(gemm_f32_dma_kernel<L_KCONTIG, 8>, grid, 512, s, g);
+    // Unsplit products finish C in the kernel (f32 or bf16, a register
+    // activation); split-K partials are f32 with the identity epilogue.
+    auto go = [&](auto lb_c) {
+      constexpr int LBc = decltype(lb_c)::value;
+      const bool bf16 = g.c_dtype == HMX_DTYPE_BF16;
+      switch (g.act) {
+        case HMX_EPI_RELU:
+          if (bf16) launch(gemm_f32_dma_kernel<LBc, 8, ACT_RELU, true>, grid, 512, s, g);
+          else launch(gemm_f32_dma_kernel<LBc, 8, ACT_RELU, false>, grid, 512, s, g);
+          break;
+        case HMX_EPI_SILU:
+          if (bf16) launch(gemm_f32_dma_kernel<LBc, 8, ACT_SILU, true>, grid, 512, s, g);
+          else launch(gemm_f32_dma_kernel<LBc, 8, ACT_SILU, false>, grid, 512, s, g);
+          break;
+        default:
+          if (bf16) launch(gemm_f32_dma_kernel<LBc, 8, ACT_ID, true>, grid, 512, s, g);
+          else launch(gemm_f32_dma_kernel<LBc, 8, ACT_ID, false>, grid, 512, s, g);
+          break;
+      }
+    };
+    if (lb == L_RCONTIG) go(std::integral_constant<int, L_RCONTIG>{});
+    else go(std::integral_constant<int, L_KCONTIG>{});
     return;
   }
   if (lb == L_RCONTIG)

@@ -226,6 +226,25 @@ def test_column_sum_plan_and_workspace_check(lib: ctypes.CDLL) -> None:
     assert st == native.ERR_INVALID and "workspace" in native.last_error()
 
 
+
+def test_f32_big_tile_unsplit_plans(lib: ctypes.CDLL) -> None:
+    f32 = native.DTYPE_F32
+    # Whole 256 x 256 f32 tiles that fill the CUs unsplit, with an epilogue
+    # the direct-to-LDS kernel finishes in registers: the big tile, one pass.
+    for epi in (native.EPI_IDENTITY, native.EPI_RELU, native.EPI_SILU):
+        assert _plan(lib, f32, 4096, 4096, 4096, epi=epi) == (1, 256, 256, 32, 0)
+        assert _plan(lib, f32, 8192, 4096, 1024, b_layout=native.B_TRANS, epi=epi) == (1, 256, 256, 32, 0)
+    # Other epilogues, K below 8 tiles, fewer tiles than CUs, ragged shapes,
+    # transposed A or a caller's tile keep the 128 x 128 tile.
+    assert _plan(lib, f32, 4096, 4096, 4096, epi=native.EPI_GELU)[:3] == (1, 128, 128)
+    assert _plan(lib, f32, 4096, 4096, 224)[1] == 128
+    assert _plan(lib, f32, 4096, 4096, 4096, cus=304)[1] == 128
+    assert _plan(lib, f32, 4000, 4096, 4096)[1] == 128
+    assert _plan(lib, f32, 4096, 4096, 4096, trans_a=1)[1] == 128
+    assert _plan(lib, f32, 4096, 4096, 4096, tiles=(128, 128, 32)) == (1, 128, 128, 32, 0)
+    # A plan passed back reproduces itself.
+    assert _plan(lib, f32, 4096, 4096, 4096, splits=1, tiles=(256, 256, 32)) == (1, 256, 256, 32, 0)
+
 def test_plan_honours_requests_and_limits(lib: ctypes.CDLL) -> None:
     bf16 = native.DTYPE_BF16
     assert _plan(lib, bf16, 4096, 4096, 4096, tiles=(128, 128, 64))[1:4] == (128, 128, 64)

@@ -295,6 +295,40 @@ def test_matmul_whole_rounds_split(gpu_device, out, trans_b) -> None:
     _check(got, ref, k, to_np(a), to_np(w), "bf16")
 
 
+@pytest.mark.parametrize(("trans_b", "epilogue", "out"),
+                         [(False, "identity", "f32"), (True, "relu", "f32"), (False, "silu", "bf16"),
+                          (True, "identity", "bf16")])
+def test_f32_big_tile_unsplit(gpu_device, trans_b: bool, epilogue: str, out: str) -> None:
+    # 4096 x 4096 x 1024 f32: 256 whole 256 x 256 tiles fill the CUs, so the
+    # direct-to-LDS f32 kernel runs unsplit and finishes C itself (bias, the
+    # activation, f32 or bf16 C). A with a row pitch that loses 16-byte
+    # alignment takes the 128 x 128 register-staged tile instead. Sampled rows
+    # of both against the oracle.
+    m, n, k = 4096, 4096, 1024
+    if torch.cuda.get_device_properties(gpu_device).multi_processor_count == 256:
+        plan = U.gemm_plan(torch.float32, m, n, k, trans_b=trans_b)
+        assert (plan["splits"], plan["tile_m"], plan["tile_n"], plan["tile_k"]) == (1, 256, 256, 32)
+    gen = torch.Generator(device=gpu_device).manual_seed(17)
+    a = torch.randn(m, k, device=gpu_device, generator=gen)
+    w = torch.randn((n, k) if trans_b else (k, n), device=gpu_device, generator=gen)
+    bias = torch.randn(n, device=gpu_device, generator=gen)
+    fn = {"silu": F.silu, "relu": torch.relu, "identity": None}[epilogue]
+    kw = dict(trans_b=trans_b, out_dtype=torch.bfloat16 if out == "bf16" else None)
+    if fn is not None:
+        kw.update(bias=bias, epilogue=fn)
+    a_pitch = torch.empty(m, k + 1, device=gpu_device)[:, :k]
+    a_pitch.copy_(a)
+    rows = torch.from_numpy(np.sort(RNG.choice(m, 48, replace=False))).to(gpu_device)
+    an, wn = to_np(a[rows]), to_np(w)
+    ref = R.matmul(an, wn, False, trans_b, to_np(bias) if fn is not None else None, act=epilogue, out=out)
+    for x in (a, a_pitch):
+        got = to_np(U.matmul(x, w, **kw)[rows])
+        if out == "f32":
+            _check(got, ref, k, an, wn, "f32")
+        else:
+            assert_close(got, ref, 1e-2, 1e-2)
+
+
 def test_linear_config4_silu(gpu_device) -> None:
     cfg = W.config4()
     x, w, b = (cfg[k].to(gpu_device) for k in ("x", "w", "b"))
