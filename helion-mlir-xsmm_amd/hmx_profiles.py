@@ -30,9 +30,11 @@ import sys
 _NS = re.compile(r"hmx::(\(anonymous namespace\)::)?")
 
 
-def kernel_name(name: str) -> str:
-    """A kernel's demangled name without the library's namespaces."""
-    return _NS.sub("", name)
+def kernel_name(name: str, limit: int = 160) -> str:
+    """A kernel's demangled name without the library's namespaces, cut to
+    ``limit`` characters (torch's own kernels have names of several KB)."""
+    name = _NS.sub("", name)
+    return name if len(name) <= limit else name[: limit - 3] + "..."
 
 
 def _rows(path: Path) -> list[dict]:
