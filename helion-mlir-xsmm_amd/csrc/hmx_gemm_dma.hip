@@ -567,11 +567,12 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
 // reads of stage t, and the barrier publishes t + 1 and frees t; slots 32-51
 // issue the 8 loads of stage t + 2 into it and slots 52-63 read stage t + 1's
 // k-step 0 fragments.
-template <int LB, int ACT, bool BF16>
+template <int LB, int ACT, bool BF16, bool RAGGED = false>
 __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
   static_assert(LB == L_KCONTIG || LB == L_RCONTIG || LB == L_VNNI_PANELS || LB == L_PANELS || LB == L_BLOCKED,
                 "B [N, K], [K, N], VNNI panels, K-major panels or 32 x 32 blocks");
   static_assert(ACT == ACT_ID || ACT == ACT_RELU || ACT == ACT_SILU, "register epilogue");
+  static_assert(!RAGGED || LB == L_KCONTIG || LB == L_RCONTIG, "ragged tiles: B [N, K] or [K, N]");
   typedef float f32x4_t __attribute__((ext_vector_type(4)));
   // Packed B as in gemm_bf16_dma64_kernel: K-major panels and 32 x 32 blocks
   // land in LDS as the row-major [64 k][256 n] tile (BT), VNNI panels as
@@ -611,6 +612,25 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
     return (int32_t)((rr * ld + (slot ^ ((rr >> 1) | (par << 2))) * 8) * 2);
   };
   const int32_t voff_a0 = kc_voff(g.a.ld, 0), voff_a1 = kc_voff(g.a.ld, 1);
+  // RAGGED (M or N not whole tiles), as gemm_bf16_dma64_kernel: a buffer
+  // load's scalar offset is not range-checked, so each lane's whole row of A
+  // (of K-contiguous B) sits in its vector offset, clamped to the last row,
+  // row-major B's columns clamped to the last 8-column chunk, and the scalar
+  // offset holds only the K position. The duplicated rows and columns reach
+  // only outputs that are never stored.
+  auto kc_voff_clamped = [&](int64_t ld, int64_t row, int64_t rows, int par) {
+    return (int32_t)((min(row, rows - 1) * ld + (slot ^ ((rr >> 1) | (par << 2))) * 8) * 2);
+  };
+  int32_t va[RAGGED ? LA : 1], vb[RAGGED && !BT ? LBN : 1];
+  if constexpr (RAGGED) {
+#pragma unroll
+    for (int q = 0; q < LA; ++q) va[q] = kc_voff_clamped(g.a.ld, m0 + wave * (BM / NW) + q * 8 + rr, g.m, q & 1);
+    if constexpr (!BT) {
+#pragma unroll
+      for (int q = 0; q < LBN; ++q)
+        vb[q] = kc_voff_clamped(g.b.ld, n0 + wave * (BN / NW) + q * 8 + rr, g.n, q & 1);
+    }
+  }
   const int32_t soff_a = (int32_t)((m0 + wave * (BM / NW)) * g.a.ld * 2);
   const int32_t blk_a = (int32_t)(8 * g.a.ld * 2);
   int32_t voff_b0, voff_b1, soff_b, blk_b;
@@ -649,9 +669,16 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
     soff_b = blk_b = 0;
   } else if constexpr (BT) {
     const int r = lane >> 5, c = lane & 31;
-    voff_b0 = (int32_t)((r * g.b.ld + (c ^ swz_n(r)) * 8) * 2);
-    voff_b1 = (int32_t)((r * g.b.ld + (c ^ swz_n(r + 2)) * 8) * 2);
-    soff_b = (int32_t)((wave * (64 / NW) * g.b.ld + n0) * 2);
+    if constexpr (RAGGED) {
+      const int64_t last = ((g.n - 1) >> 3) << 3;  // the last 8-column chunk
+      voff_b0 = (int32_t)((r * g.b.ld + min(n0 + (c ^ swz_n(r)) * 8, last)) * 2);
+      voff_b1 = (int32_t)((r * g.b.ld + min(n0 + (c ^ swz_n(r + 2)) * 8, last)) * 2);
+      soff_b = (int32_t)(wave * (64 / NW) * g.b.ld * 2);
+    } else {
+      voff_b0 = (int32_t)((r * g.b.ld + (c ^ swz_n(r)) * 8) * 2);
+      voff_b1 = (int32_t)((r * g.b.ld + (c ^ swz_n(r + 2)) * 8) * 2);
+      soff_b = (int32_t)((wave * (64 / NW) * g.b.ld + n0) * 2);
+    }
     blk_b = (int32_t)(2 * g.b.ld * 2);
   } else {
     voff_b0 = kc_voff(g.b.ld, 0);
@@ -666,7 +693,10 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
     const uint32_t st = lds_w + (uint32_t)((t & 1) * STAGE);
     const uint32_t sb = lds_wb + (uint32_t)((t & 1) * STAGE);
     if (q < LA) {
-      lds_dma16(srd_a, (q & 1) ? voff_a1 : voff_a0, soff_a + q * blk_a + (int32_t)(k0 * 2), st + q * 1024);
+      if constexpr (RAGGED)
+        lds_dma16(srd_a, va[q], (int32_t)(k0 * 2), st + q * 1024);
+      else
+        lds_dma16(srd_a, (q & 1) ? voff_a1 : voff_a0, soff_a + q * blk_a + (int32_t)(k0 * 2), st + q * 1024);
     } else if constexpr (VN) {
       const int qb = q - LA;
       lds_dma16(srd_b, voff_b0, vn_off[qb] + (int32_t)((k0 / 2) * 4 * P), sb + qb * 1024);
@@ -675,6 +705,9 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
       const int64_t kr = k0 + wave * (64 / NW) + 2 * qb;  // even
       const int64_t row = LB == L_PANELS ? kr * P : (kr >> 5) * 1024 + (kr & 31) * 32;
       lds_dma16(srd_b, (qb & 1) ? voff_b1 : voff_b0, (int32_t)(row * 2), sb + qb * 1024);
+    } else if constexpr (RAGGED && !BT) {
+      const int qb = q - LA;
+      lds_dma16(srd_b, vb[qb], (int32_t)(k0 * 2), sb + qb * 1024);
     } else {
       const int qb = q - LA;
       const int32_t kb = BT ? (int32_t)(k0 * g.b.ld * 2) : (int32_t)(k0 * 2);
@@ -788,7 +821,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
     for (int j = 0; j < FN; ++j) {
       const int cl = wn * WN + j * 16 + (lane & 15);  // tile column
       float bias, scale, shift;
-      column_vectors(g, n0 + cl, true, bias, scale, shift);
+      column_vectors(g, n0 + cl, !RAGGED || n0 + cl < g.n, bias, scale, shift);
       const int pc = cl & ~1;
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
@@ -811,7 +844,22 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
     for (int p = 0; p < 16; ++p) {
       const int r = wave * 32 + 2 * p + (lane >> 5), ch = lane & 31;
       const uint4 v = *(const uint4*)(lds + r * 512 + ((ch ^ cswz(r)) << 4));
-      store16_stream(c + (m0 + r) * g.ldc + n0 + ch * 8, v);
+      if constexpr (RAGGED) {
+        // Rows past M are not stored; the chunk across N is stored element
+        // by element.
+        const int64_t row = m0 + r, col = n0 + ch * 8;
+        if (row < g.m) {
+          if (col + 8 <= g.n) {
+            store16_stream(c + row * g.ldc + col, v);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (col + e < g.n) c[row * g.ldc + col + e] = (uint16_t)(dw(v, e >> 1) >> (16 * (e & 1)));
+          }
+        }
+      } else {
+        store16_stream(c + (m0 + r) * g.ldc + n0 + ch * 8, v);
+      }
     }
   } else {
     float* c = (float*)g.c + off;
@@ -819,14 +867,15 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
     for (int j = 0; j < FN; ++j) {
       const int64_t col = n0 + wn * WN + j * 16 + (lane & 15);
       float bias, scale, shift;
-      column_vectors(g, col, true, bias, scale, shift);
+      column_vectors(g, col, !RAGGED || col < g.n, bias, scale, shift);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const int64_t row0 = m0 + wm * WM + i * 16 + 4 * fg;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          store_c32(c + (row0 + e) * g.ldc + col,
-                    __float_as_uint(activate<ACT>((acc[i][j][e] + bias) * scale + shift)));
+          if (!RAGGED || (row0 + e < g.m && col < g.n))
+            store_c32(c + (row0 + e) * g.ldc + col,
+                      __float_as_uint(activate<ACT>((acc[i][j][e] + bias) * scale + shift)));
       }
     }
   }
@@ -1198,14 +1247,30 @@ bool mfma16_enabled() {
   return on;
 }
 
+// The 16x16x32 kernel's conditions beyond its template's: no stagger, and
+// bf16 C in 16-byte row pieces.
+bool mi16_args_ok(const GemmArgs& g) {
+  const bool rows16 = g.c_dtype != HMX_DTYPE_BF16 || ((((uintptr_t)g.c) & 15) == 0 && g.ldc % 8 == 0 &&
+                                                      g.stride_c % 8 == 0 && g.stride_split % 8 == 0);
+  return !g.k_stagger && rows16 && mfma16_enabled();
+}
+
+// Eight waves (two per SIMD) unless the environment sets HMX_GEMM_WAVES=4:
+// the second wave of a SIMD issues MFMAs while the first waits at the stage
+// barrier or on an LDS read (measured: 2-5 % faster on configs 3-5).
+bool eight_waves() {
+  static const bool eight = [] {
+    const char* e = getenv("HMX_GEMM_WAVES");
+    return !(e && e[0] == '4');
+  }();
+  return eight;
+}
+
 template <int LB, bool BF16, bool K64, int NW = 4>
 void launch_bf16_dma_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
   if constexpr (K64 && NW == 8 &&
                 (LB == L_KCONTIG || LB == L_RCONTIG || LB == L_VNNI_PANELS || LB == L_PANELS || LB == L_BLOCKED)) {
-    // bf16 C leaves the 16x16x32 kernel in 16-byte row pieces.
-    const bool rows16 = !BF16 || ((((uintptr_t)g.c) & 15) == 0 && g.ldc % 8 == 0 && g.stride_c % 8 == 0 &&
-                                  g.stride_split % 8 == 0);
-    if (!g.k_stagger && rows16 && mfma16_enabled()) {
+    if (mi16_args_ok(g)) {
       switch (g.act) {
         case HMX_EPI_IDENTITY: launch(gemm_bf16_mi16_kernel<LB, ACT_ID, BF16>, grid, 512, s, g); return;
         case HMX_EPI_RELU: launch(gemm_bf16_mi16_kernel<LB, ACT_RELU, BF16>, grid, 512, s, g); return;
@@ -1241,14 +1306,7 @@ void launch_bf16_dma_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
 
 template <int LB, bool K64>
 void launch_bf16_dma_b(const GemmArgs& g, dim3 grid, hipStream_t s) {
-  // Eight waves (two per SIMD) unless the environment sets HMX_GEMM_WAVES=4:
-  // the second wave of a SIMD issues MFMAs while the first waits at the
-  // stage barrier or on an LDS read (measured: 2-5 % faster on configs 3-5).
-  static const bool eight = [] {
-    const char* e = getenv("HMX_GEMM_WAVES");
-    return !(e && e[0] == '4');
-  }();
-  if (eight && K64) {
+  if (eight_waves() && K64) {
     if (g.c_dtype == HMX_DTYPE_BF16)
       launch_bf16_dma_c<LB, true, K64, 8>(g, grid, s);
     else
@@ -1309,6 +1367,14 @@ void launch_gemm_bf16_dma_narrow(const GemmArgs& g, int lb, dim3 grid, hipStream
 // edge rows and columns and the guarded edge epilogue.
 template <int LB, bool BF16>
 void launch_bf16_dma_ragged(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  if (eight_waves() && mi16_args_ok(g)) {
+    switch (g.act) {
+      case HMX_EPI_IDENTITY: launch(gemm_bf16_mi16_kernel<LB, ACT_ID, BF16, true>, grid, 512, s, g); return;
+      case HMX_EPI_RELU: launch(gemm_bf16_mi16_kernel<LB, ACT_RELU, BF16, true>, grid, 512, s, g); return;
+      case HMX_EPI_SILU: launch(gemm_bf16_mi16_kernel<LB, ACT_SILU, BF16, true>, grid, 512, s, g); return;
+      default: break;
+    }
+  }
   switch (g.act) {
     case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 8, 256, true>, grid, 512, s, g); break;
     case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 8, 256, true>, grid, 512, s, g); break;
