@@ -567,12 +567,18 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
 // reads of stage t, and the barrier publishes t + 1 and frees t; slots 32-51
 // issue the 8 loads of stage t + 2 into it and slots 52-63 read stage t + 1's
 // k-step 0 fragments.
-template <int LB, int ACT, bool BF16, bool RAGGED = false>
-__global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
+template <int LB, int ACT, bool BF16, bool RAGGED = false, int BM = 256, int BN = 256, int NW = 8>
+__global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
   static_assert(LB == L_KCONTIG || LB == L_RCONTIG || LB == L_VNNI_PANELS || LB == L_PANELS || LB == L_BLOCKED,
                 "B [N, K], [K, N], VNNI panels, K-major panels or 32 x 32 blocks");
   static_assert(ACT == ACT_ID || ACT == ACT_RELU || ACT == ACT_SILU, "register epilogue");
   static_assert(!RAGGED || LB == L_KCONTIG || LB == L_RCONTIG, "ragged tiles: B [N, K] or [K, N]");
+  // Tiles: 256 x 256 with eight waves of 128 x 64; 128 x 128 with four of
+  // 64 x 64; 256 x 128 with four of 128 x 64 (one wave per SIMD).
+  static_assert((BM == 256 && BN == 256 && NW == 8) || (BM == 128 && BN == 128 && NW == 4) ||
+                    (BM == 256 && BN == 128 && NW == 4),
+                "256 x 256 (8 waves), 128 x 128 or 256 x 128 (4 waves)");
+  static_assert(BN == 256 || LB == L_KCONTIG || LB == L_RCONTIG, "packed B: 256-column tiles");
   typedef float f32x4_t __attribute__((ext_vector_type(4)));
   // Packed B as in gemm_bf16_dma64_kernel: K-major panels and 32 x 32 blocks
   // land in LDS as the row-major [64 k][256 n] tile (BT), VNNI panels as
@@ -580,14 +586,14 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
   constexpr bool BPK = LB == L_PANELS || LB == L_BLOCKED;
   constexpr bool BT = LB == L_RCONTIG || BPK;
   constexpr bool VN = LB == L_VNNI_PANELS;
-  constexpr int NW = 8, BM = 256, BN = 256, BK = 64;
+  constexpr int BK = 64;
   constexpr int ROWB = BK * 2, NROWB = BN * 2;
-  constexpr int A_BYTES = BM * ROWB;            // 32 KiB
-  constexpr int STAGE = A_BYTES + BN * BK * 2;  // 64 KiB
-  constexpr int WM = 128, WN = 64, FM = 8, FN = 4;
-  constexpr int LA = BM / 8 / NW, LBN = BN / 8 / NW, LOADS = LA + LBN;  // 4 + 4
-  constexpr int NS = FM * FN, SLOTS = 2 * NS, NF = FM + FN;            // 32, 64, 12
-  constexpr int BAR = NS, LOAD_END = SLOTS - NF;                         // 32, 52
+  constexpr int A_BYTES = BM * ROWB;            // 32 KiB (16 KiB for 128-row tiles)
+  constexpr int STAGE = A_BYTES + BN * BK * 2;  // 64 KiB (32 or 48 KiB)
+  constexpr int WM = BM / 2, WN = BN / (NW / 2), FM = WM / 16, FN = WN / 16;
+  constexpr int LA = BM / 8 / NW, LBN = BN / 8 / NW, LOADS = LA + LBN;  // 4 + 4 (8 + 4 for 256 x 128)
+  constexpr int NS = FM * FN, SLOTS = 2 * NS, NF = FM + FN;            // 32, 64, 12 (16, 32, 8)
+  constexpr int BAR = NS, LOAD_END = SLOTS - NF;                         // 32, 52 (16, 24)
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
 
   int tm, tn;
@@ -600,7 +606,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / 4, wn = wave % 4;
+  const int wm = wave / (NW / 2), wn = wave % (NW / 2);
 
   const i32x4_t srd_a = make_srd((const uint16_t*)g.a.p + batch * g.stride_a, g.a.bytes);
   const i32x4_t srd_b = make_srd((const uint16_t*)g.b.p + batch * g.stride_b, g.b.bytes);
@@ -667,6 +673,19 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
     voff_b0 = (int32_t)((col(n0 + (c ^ swz_n(r)) * 8) + r * rs) * 2);
     voff_b1 = (int32_t)((col(n0 + (c ^ swz_n(r + 2)) * 8) + r * rs) * 2);
     soff_b = blk_b = 0;
+  } else if constexpr (BT && BN == 128) {
+    // 256-byte rows: a 1 KiB load is 4 K rows, lane l filling slot l % 16 of
+    // row l / 16; row k % 4 == l / 16 for every load, so one lane offset.
+    const int r = lane >> 4, c = lane & 15;
+    if constexpr (RAGGED) {
+      const int64_t last = ((g.n - 1) >> 3) << 3;  // the last 8-column chunk
+      voff_b0 = voff_b1 = (int32_t)((r * g.b.ld + min(n0 + (c ^ swz_n(r)) * 8, last)) * 2);
+      soff_b = (int32_t)(wave * (64 / NW) * g.b.ld * 2);
+    } else {
+      voff_b0 = voff_b1 = (int32_t)((r * g.b.ld + (c ^ swz_n(r)) * 8) * 2);
+      soff_b = (int32_t)((wave * (64 / NW) * g.b.ld + n0) * 2);
+    }
+    blk_b = (int32_t)(4 * g.b.ld * 2);
   } else if constexpr (BT) {
     const int r = lane >> 5, c = lane & 31;
     if constexpr (RAGGED) {
@@ -832,18 +851,19 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
           const float recv = swap_pair(odd ? v0 : v1);
           const int r = wm * WM + i * 16 + 4 * fg + 2 * q + (odd ? 1 : 0);
           const uint32_t word = odd ? pack_bf16x2(recv, v1) : pack_bf16x2(v0, recv);
-          *(uint32_t*)(lds + r * 512 + (((pc >> 3) ^ cswz(r)) << 4) + (pc & 7) * 2) = word;
+          *(uint32_t*)(lds + r * NROWB + (((pc >> 3) ^ cswz(r)) << 4) + (pc & 7) * 2) = word;
         }
       }
     }
     __syncthreads();
-    // Wave w stores tile rows 32 w .. 32 w + 31, two rows per instruction
-    // (lanes 0-31 and 32-63, 16 bytes each).
+    // Wave w stores tile rows RW w .. RW w + RW - 1, RPI whole rows per
+    // instruction (16 bytes per lane: two 512-byte or four 256-byte rows).
+    constexpr int RW = BM / NW, CPR = NROWB / 16, RPI = 64 / CPR;
     uint16_t* c = (uint16_t*)g.c + off;
 #pragma unroll
-    for (int p = 0; p < 16; ++p) {
-      const int r = wave * 32 + 2 * p + (lane >> 5), ch = lane & 31;
-      const uint4 v = *(const uint4*)(lds + r * 512 + ((ch ^ cswz(r)) << 4));
+    for (int p = 0; p < RW / RPI; ++p) {
+      const int r = wave * RW + RPI * p + lane / CPR, ch = lane % CPR;
+      const uint4 v = *(const uint4*)(lds + r * NROWB + ((ch ^ cswz(r)) << 4));
       if constexpr (RAGGED) {
         // Rows past M are not stored; the chunk across N is stored element
         // by element.
@@ -1343,6 +1363,20 @@ bool gemm_bf16_dma_packed_ok(const GemmArgs& g, int lb) {
 
 template <int LB, bool BF16>
 void launch_bf16_dma_narrow(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  if (mi16_args_ok(g)) {
+    switch (g.act) {
+      case HMX_EPI_IDENTITY:
+        launch(gemm_bf16_mi16_kernel<LB, ACT_ID, BF16, false, 256, 128, 4>, grid, 256, s, g);
+        return;
+      case HMX_EPI_RELU:
+        launch(gemm_bf16_mi16_kernel<LB, ACT_RELU, BF16, false, 256, 128, 4>, grid, 256, s, g);
+        return;
+      case HMX_EPI_SILU:
+        launch(gemm_bf16_mi16_kernel<LB, ACT_SILU, BF16, false, 256, 128, 4>, grid, 256, s, g);
+        return;
+      default: break;
+    }
+  }
   switch (g.act) {
     case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 4, 128>, grid, 256, s, g); break;
     case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 4, 128>, grid, 256, s, g); break;
@@ -1387,6 +1421,23 @@ void launch_bf16_dma_ragged(const GemmArgs& g, dim3 grid, hipStream_t s) {
 // or ragged.
 template <int LB, bool BF16, bool RAGGED>
 void launch_bf16_dma128_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  // The 16x16x32 kernel from 16 stages per split on (1000 x 4096 x 4096:
+  // 51 -> 44 us); short chunks (1024^3 split four ways: 16 -> 17.5 us) keep
+  // the 32x32x16 kernel.
+  if (mi16_args_ok(g) && g.k_chunk >= 16 * 64) {
+    switch (g.act) {
+      case HMX_EPI_IDENTITY:
+        launch(gemm_bf16_mi16_kernel<LB, ACT_ID, BF16, RAGGED, 128, 128, 4>, grid, 256, s, g);
+        return;
+      case HMX_EPI_RELU:
+        launch(gemm_bf16_mi16_kernel<LB, ACT_RELU, BF16, RAGGED, 128, 128, 4>, grid, 256, s, g);
+        return;
+      case HMX_EPI_SILU:
+        launch(gemm_bf16_mi16_kernel<LB, ACT_SILU, BF16, RAGGED, 128, 128, 4>, grid, 256, s, g);
+        return;
+      default: break;
+    }
+  }
   switch (g.act) {
     case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
     case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
