@@ -214,6 +214,35 @@ def test_matmul_random_shapes(gpu_device, m, n, k, trans_a, trans_b, tiles, act,
     _check(to_np(got), ref, k, to_np(a), to_np(b), "bf16")
 
 
+def _long_k_cases(count: int, seed: int) -> list[tuple]:
+    # K chunks of 16 or more 64-element stages: the 16x16x32 kernel's 128 x 128
+    # tiles (whole and ragged) next to its 256 x 256 ones.
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(count):
+        # At least 16 x 16 tiles of 128 x 128 (and too few of 256 x 256 to fill
+        # the CUs): 128 x 128 tiles with whole K chunks.
+        m = int(rng.choice([int(rng.integers(1921, 2400)), 128 * int(rng.integers(16, 19))]))
+        n = int(rng.choice([8 * int(rng.integers(241, 300)), 128 * int(rng.integers(16, 19))]))
+        k = 64 * int(rng.integers(16, 40))
+        cases.append((m, n, k, bool(rng.random() < 0.5), [None, (128, 128, 64)][int(rng.integers(0, 2))],
+                      ["identity", "relu", "silu"][int(rng.integers(0, 3))], bool(rng.random() < 0.5)))
+    return cases
+
+
+@pytest.mark.parametrize(("m", "n", "k", "trans_b", "tiles", "act", "f32_out"), _long_k_cases(16, 23))
+def test_matmul_long_k_tiles(gpu_device, m, n, k, trans_b, tiles, act, f32_out) -> None:
+    if torch.cuda.get_device_properties(gpu_device).multi_processor_count == 256:
+        plan = U.gemm_plan(torch.bfloat16, m, n, k, trans_b=trans_b, block_sizes=tiles)
+        assert (plan["splits"], plan["tile_m"]) == (1, 128)
+    a, b = _operands(m, n, k, False, trans_b, "bf16", gpu_device, 0.3)
+    bias = tensor(RNG.normal(0, 1, n).astype(np.float32), "bf16", gpu_device)
+    out_dtype = torch.float32 if f32_out else torch.bfloat16
+    got = U.matmul(a, b, trans_b=trans_b, bias=bias, epilogue=ACTS[act], out_dtype=out_dtype, block_sizes=tiles)
+    ref = R.matmul(to_np(a), to_np(b), False, trans_b, to_np(bias), act=act, out="f32" if f32_out else "bf16")
+    _check(to_np(got), ref, k, to_np(a), to_np(b), "bf16")
+
+
 @pytest.mark.parametrize(("m", "n", "k", "lda"), [
     (1, 11008, 4096, 0), (32, 11008, 4096, 0), (12, 9000, 512, 0), (31, 17000, 256, 0),  # 2 waves
     (8, 4096, 4096, 0), (16, 203, 192, 0), (17, 1000, 64, 0), (32, 300, 128, 0), (5, 33, 640, 0),  # 4 waves
