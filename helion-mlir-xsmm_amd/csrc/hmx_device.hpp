@@ -147,58 +147,86 @@ __device__ __forceinline__ float min_nan(float a, float b) {
   return (a != a || b != b) ? a + b : fminf(a, b);
 }
 
-// One instruction of an epilogue program (hmx_program): the f32 result of
-// op on registers a, b and the constants. The formulas are the ones torch
-// evaluates for the same operation on f32 tensors.
+// The operations of an epilogue program (hmx_program): X(opcode, f32 result of
+// a, b and the constants c0, c1). The formulas are the ones torch evaluates
+// for the same operation on f32 tensors.
+#define HMX_PROGRAM_OPS(X)                                                       \
+  X(HMX_OP_COPY, a)                                                              \
+  X(HMX_OP_NEG, -a)                                                              \
+  X(HMX_OP_ABS, fabsf(a))                                                        \
+  X(HMX_OP_RELU, a > 0.f ? a : (a != a ? a : 0.f))                               \
+  X(HMX_OP_SIGMOID, 1.f / (1.f + expf(-a)))                                      \
+  X(HMX_OP_TANH, tanhf(a))                                                       \
+  X(HMX_OP_SILU, a / (1.f + expf(-a)))                                           \
+  X(HMX_OP_GELU, a * 0.5f * (1.f + erff(a * 0.7071067811865476f)))               \
+  X(HMX_OP_GELU_TANH,                                                            \
+    0.5f * a * (1.f + tanhf(0.7978845608028654f * (a + 0.044715f * a * a * a)))) \
+  X(HMX_OP_EXP, expf(a))                                                         \
+  X(HMX_OP_LOG, logf(a))                                                         \
+  X(HMX_OP_SQRT, sqrtf(a))                                                       \
+  X(HMX_OP_RSQRT, 1.f / sqrtf(a))                                                \
+  X(HMX_OP_RECIP, 1.f / a)                                                       \
+  X(HMX_OP_ERF, erff(a))                                                         \
+  X(HMX_OP_SIN, sinf(a))                                                         \
+  X(HMX_OP_COS, cosf(a))                                                         \
+  X(HMX_OP_LOG1P, log1pf(a))                                                     \
+  X(HMX_OP_EXPM1, expm1f(a))                                                     \
+  X(HMX_OP_FLOOR, floorf(a))                                                     \
+  X(HMX_OP_CEIL, ceilf(a))                                                       \
+  X(HMX_OP_TRUNC, truncf(a))                                                     \
+  X(HMX_OP_ROUND, rintf(a))                                                      \
+  X(HMX_OP_SOFTPLUS, a * c0 > c1 ? a : log1pf(expf(a * c0)) / c0)                \
+  X(HMX_OP_MISH, a * tanhf(log1pf(expf(a))))                                     \
+  X(HMX_OP_HARDSWISH, a * min_nan(max_nan(a + 3.f, 0.f), 6.f) / 6.f)             \
+  X(HMX_OP_HARDSIGMOID, min_nan(max_nan(a + 3.f, 0.f), 6.f) / 6.f)               \
+  X(HMX_OP_ELU, a <= 0.f ? expm1f(a) * (c0 * c1) : a * c1)                       \
+  X(HMX_OP_LEAKY_RELU, a > 0.f ? a : a * c0)                                     \
+  X(HMX_OP_CLAMP, min_nan(max_nan(a, c0), c1))                                   \
+  X(HMX_OP_ADD_C, a + c0)                                                        \
+  X(HMX_OP_MUL_C, a * c0)                                                        \
+  X(HMX_OP_DIV_C, a / c0)                                                        \
+  X(HMX_OP_RSUB_C, c0 - a)                                                       \
+  X(HMX_OP_RDIV_C, c0 / a)                                                       \
+  X(HMX_OP_POW_C, powf(a, c0))                                                   \
+  X(HMX_OP_ADD, a + b)                                                           \
+  X(HMX_OP_SUB, a - b)                                                           \
+  X(HMX_OP_MUL, a * b)                                                           \
+  X(HMX_OP_DIV, a / b)                                                           \
+  X(HMX_OP_MAX, max_nan(a, b))                                                   \
+  X(HMX_OP_MIN, min_nan(a, b))                                                   \
+  X(HMX_OP_POW, powf(a, b))
+
+// One instruction on one value.
 __device__ __forceinline__ float program_op(int op, float a, float b, float c0, float c1) {
   switch (op) {
-    case HMX_OP_COPY: return a;
-    case HMX_OP_NEG: return -a;
-    case HMX_OP_ABS: return fabsf(a);
-    case HMX_OP_RELU: return a > 0.f ? a : (a != a ? a : 0.f);
-    case HMX_OP_SIGMOID: return 1.f / (1.f + expf(-a));
-    case HMX_OP_TANH: return tanhf(a);
-    case HMX_OP_SILU: return a / (1.f + expf(-a));
-    case HMX_OP_GELU: return a * 0.5f * (1.f + erff(a * 0.7071067811865476f));
-    case HMX_OP_GELU_TANH: {
-      const float inner = 0.7978845608028654f * (a + 0.044715f * a * a * a);
-      return 0.5f * a * (1.f + tanhf(inner));
-    }
-    case HMX_OP_EXP: return expf(a);
-    case HMX_OP_LOG: return logf(a);
-    case HMX_OP_SQRT: return sqrtf(a);
-    case HMX_OP_RSQRT: return 1.f / sqrtf(a);
-    case HMX_OP_RECIP: return 1.f / a;
-    case HMX_OP_ERF: return erff(a);
-    case HMX_OP_SIN: return sinf(a);
-    case HMX_OP_COS: return cosf(a);
-    case HMX_OP_LOG1P: return log1pf(a);
-    case HMX_OP_EXPM1: return expm1f(a);
-    case HMX_OP_FLOOR: return floorf(a);
-    case HMX_OP_CEIL: return ceilf(a);
-    case HMX_OP_TRUNC: return truncf(a);
-    case HMX_OP_ROUND: return rintf(a);
-    case HMX_OP_SOFTPLUS: return a * c0 > c1 ? a : log1pf(expf(a * c0)) / c0;
-    case HMX_OP_MISH: return a * tanhf(log1pf(expf(a)));
-    case HMX_OP_HARDSWISH: return a * min_nan(max_nan(a + 3.f, 0.f), 6.f) / 6.f;
-    case HMX_OP_HARDSIGMOID: return min_nan(max_nan(a + 3.f, 0.f), 6.f) / 6.f;
-    case HMX_OP_ELU: return a <= 0.f ? expm1f(a) * (c0 * c1) : a * c1;
-    case HMX_OP_LEAKY_RELU: return a > 0.f ? a : a * c0;
-    case HMX_OP_CLAMP: return min_nan(max_nan(a, c0), c1);
-    case HMX_OP_ADD_C: return a + c0;
-    case HMX_OP_MUL_C: return a * c0;
-    case HMX_OP_DIV_C: return a / c0;
-    case HMX_OP_RSUB_C: return c0 - a;
-    case HMX_OP_RDIV_C: return c0 / a;
-    case HMX_OP_POW_C: return powf(a, c0);
-    case HMX_OP_ADD: return a + b;
-    case HMX_OP_SUB: return a - b;
-    case HMX_OP_MUL: return a * b;
-    case HMX_OP_DIV: return a / b;
-    case HMX_OP_MAX: return max_nan(a, b);
-    case HMX_OP_MIN: return min_nan(a, b);
-    case HMX_OP_POW: return powf(a, b);
+#define HMX_OP_CASE(OP, EXPR) \
+  case OP:                    \
+    return (EXPR);
+    HMX_PROGRAM_OPS(HMX_OP_CASE)
+#undef HMX_OP_CASE
     default: return a;
+  }
+}
+
+// One instruction on n values: the opcode (uniform across the wave) is
+// dispatched once for all of them.
+template <int N>
+__device__ __forceinline__ void program_op_n(int op, const float (&x)[N], const float (&y)[N], float c0,
+                                             float c1, float (&out)[N]) {
+  switch (op) {
+#define HMX_OP_CASE(OP, EXPR)         \
+  case OP:                            \
+    _Pragma("unroll") for (int i = 0; i < N; ++i) { \
+      const float a = x[i], b = y[i]; \
+      (void)b;                        \
+      out[i] = (EXPR);                \
+    }                                 \
+    break;
+    HMX_PROGRAM_OPS(HMX_OP_CASE)
+#undef HMX_OP_CASE
+    default:
+#pragma unroll
+      for (int i = 0; i < N; ++i) out[i] = x[i];
   }
 }
 
@@ -229,25 +257,65 @@ __device__ __forceinline__ float run_program(const hmx_program& p, float x, floa
   return program_reg(r, p.result);
 }
 
-// Applies the epilogue (activation code or program) to n values in place,
-// one value per pass of a loop that is not unrolled: the values rotate
-// through v[0], so the program's code is emitted once however large n is.
+// Register k (uniform) of n values' register files, by a branch on k rather
+// than a select per register and value.
+template <int N>
+__device__ __forceinline__ void program_read_n(const float (&r)[HMX_PROGRAM_REGS][N], int k, float (&out)[N]) {
+  switch (k) {
+#define HMX_REG_CASE(K)                                 \
+  case K:                                               \
+    _Pragma("unroll") for (int i = 0; i < N; ++i) out[i] = r[K][i]; \
+    break;
+    HMX_REG_CASE(0) HMX_REG_CASE(1) HMX_REG_CASE(2) HMX_REG_CASE(3)
+    HMX_REG_CASE(4) HMX_REG_CASE(5) HMX_REG_CASE(6) HMX_REG_CASE(7)
+#undef HMX_REG_CASE
+    default:
+#pragma unroll
+      for (int i = 0; i < N; ++i) out[i] = 0.f;
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void program_write_n(float (&r)[HMX_PROGRAM_REGS][N], int k, const float (&v)[N]) {
+  switch (k) {
+#define HMX_REG_CASE(K)                                 \
+  case K:                                               \
+    _Pragma("unroll") for (int i = 0; i < N; ++i) r[K][i] = v[i]; \
+    break;
+    HMX_REG_CASE(0) HMX_REG_CASE(1) HMX_REG_CASE(2) HMX_REG_CASE(3)
+    HMX_REG_CASE(4) HMX_REG_CASE(5) HMX_REG_CASE(6) HMX_REG_CASE(7)
+#undef HMX_REG_CASE
+    default: break;
+  }
+}
+static_assert(HMX_PROGRAM_REGS == 8, "the register file's cases");
+
+// Runs the program on n values in place (register 0 of value i is v[i],
+// register 1 extra[i]): the instructions in turn, each read, computed and
+// written for all n values at once, so opcodes and register numbers are
+// dispatched once per instruction, not once per value.
 template <int N>
 __device__ __forceinline__ void run_program_n(const hmx_program& p, float (&v)[N], const float (&extra)[N]) {
-  float e[N];
+  float r[HMX_PROGRAM_REGS][N];
 #pragma unroll
-  for (int i = 0; i < N; ++i) e[i] = extra[i];
-#pragma unroll 1
-  for (int t = 0; t < N; ++t) {
-    const float y = run_program(p, v[0], e[0]);
+  for (int i = 0; i < N; ++i) {
+    r[0][i] = v[i];
+    r[1][i] = extra[i];
 #pragma unroll
-    for (int i = 0; i + 1 < N; ++i) {
-      v[i] = v[i + 1];
-      e[i] = e[i + 1];
-    }
-    v[N - 1] = y;
-    e[N - 1] = 0.f;
+    for (int j = 2; j < HMX_PROGRAM_REGS; ++j) r[j][i] = 0.f;
   }
+  const int count = __builtin_amdgcn_readfirstlane(p.count);
+#pragma unroll 1
+  for (int k = 0; k < count; ++k) {
+    const hmx_instr ins = p.code[k];
+    const int op = __builtin_amdgcn_readfirstlane(ins.op);
+    float a[N], b[N], y[N];
+    program_read_n<N>(r, __builtin_amdgcn_readfirstlane(ins.a), a);
+    program_read_n<N>(r, __builtin_amdgcn_readfirstlane(ins.b), b);
+    program_op_n<N>(op, a, b, ins.c0, ins.c1, y);
+    program_write_n<N>(r, __builtin_amdgcn_readfirstlane(ins.dst), y);
+  }
+  program_read_n<N>(r, __builtin_amdgcn_readfirstlane(p.result), v);
 }
 
 }  // namespace hmx

@@ -182,12 +182,13 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_dma_kernel(GemmArgs g) {
     __builtin_amdgcn_sched_barrier(0);
   }
   wait_vmem<0>();  // no load into LDS outlives the loop
-  if constexpr (ACT == ACT_ANY) {
+  if constexpr (staged_act(ACT)) {
     // Any other activation or a program: through LDS, once every wave is
     // done reading its last stage.
     static_assert(4 * 32 * epi_pitch<WN>() * 4 <= S * STAGE, "staged epilogue fits the stages");
     __syncthreads();
-    epilogue_staged<FM, FN, WM, WN, false, true>(g, (float*)lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
+    epilogue_staged<FM, FN, WM, WN, false, ACT == ACT_PROG>(g, (float*)lds, split, batch, m0, n0, wm, wn, wave,
+                                                             lane, acc);
   } else {
     epilogue_direct<FM, FN, WM, WN, false, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
   }
@@ -525,15 +526,16 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
   }
   wait_vmem<0>();  // no load into LDS outlives the loop
   // RAGGED: tiles that cross M or N store element by element, guarded.
-  if constexpr (ACT == ACT_ANY) {
+  if constexpr (staged_act(ACT)) {
     // Any other activation or a program: through LDS, once every wave is
     // done reading its last stage.
     static_assert(NW * 32 * epi_pitch<WN>() * 4 <= 2 * STAGE, "staged epilogue fits the stages");
     __syncthreads();
+    constexpr bool PROG = ACT == ACT_PROG;
     if (!RAGGED || (m0 + BM <= g.m && n0 + BN <= g.n))
-      epilogue_staged<FM, FN, WM, WN, false, true>(g, (float*)lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
+      epilogue_staged<FM, FN, WM, WN, false, PROG>(g, (float*)lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
     else
-      epilogue_staged<FM, FN, WM, WN, true, true>(g, (float*)lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
+      epilogue_staged<FM, FN, WM, WN, true, PROG>(g, (float*)lds, split, batch, m0, n0, wm, wn, wave, lane, acc);
   } else {
     if (!RAGGED || (m0 + BM <= g.m && n0 + BN <= g.n))
       epilogue_direct<FM, FN, WM, WN, false, ACT, BF16>(g, split, batch, m0, n0, wm, wn, lane, true, acc);
@@ -571,7 +573,9 @@ template <int LB, int ACT, bool BF16, bool RAGGED = false, int BM = 256, int BN 
 __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
   static_assert(LB == L_KCONTIG || LB == L_RCONTIG || LB == L_VNNI_PANELS || LB == L_PANELS || LB == L_BLOCKED,
                 "B [N, K], [K, N], VNNI panels, K-major panels or 32 x 32 blocks");
-  static_assert(ACT == ACT_ID || ACT == ACT_RELU || ACT == ACT_SILU, "register epilogue");
+  static_assert(ACT == ACT_ID || ACT == ACT_RELU || ACT == ACT_SILU || staged_act(ACT), "epilogue class");
+  static_assert(!staged_act(ACT) || (BM == 256 && BN == 256 && NW == 8 && !RAGGED),
+                "other epilogues: whole 256 x 256 tiles");
   static_assert(!RAGGED || LB == L_KCONTIG || LB == L_RCONTIG, "ragged tiles: B [N, K] or [K, N]");
   // Tiles: 256 x 256 with eight waves of 128 x 64; 128 x 128 with four of
   // 64 x 64; 256 x 128 with eight of 128 x 32.
@@ -594,7 +598,11 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
   constexpr int LA = BM / 8 / NW, LBN = BN / 8 / NW, LOADS = LA + LBN;  // 4 + 4 (8 + 4 for 256 x 128)
   constexpr int NS = FM * FN, SLOTS = 2 * NS, NF = FM + FN;            // 32, 64, 12 (16, 32, 8)
   constexpr int BAR = NS, LOAD_END = SLOTS - NF;                         // 32, 52 (16, 24)
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
+  // ACT_ANY stages each wave's 64-row halves as f32, rows of WN * 4 + 16
+  // bytes: 8 x 64 x 272 bytes, a little more than the stages.
+  constexpr int EPI_BYTES = NW * (WM / 2) * (WN * 4 + 16);
+  constexpr int LDS_BYTES = staged_act(ACT) && EPI_BYTES > 2 * STAGE ? EPI_BYTES : 2 * STAGE;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
 
   int tm, tn;
   tile_coords(g.tiles_m, g.tiles_n, g.xcds, tm, tn);
@@ -826,7 +834,56 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
   // 4 g .. 4 g + 3 (bias, scale, shift, activation, one rounding).
   const int64_t off = split * g.stride_split + batch * g.stride_c;
   const bool odd = lane & 1;
-  if constexpr (BF16) {
+  if constexpr (staged_act(ACT)) {
+    // Any other named activation, or an epilogue program: each wave stages
+    // its own 128 x 64 outputs as f32 in its own LDS region, 64 rows at a
+    // time (rows padded by 16 bytes, so one fragment write -- 16 columns of
+    // four rows 4 apart -- meets distinct banks), and finishes them in runs of
+    // 8 columns -- bias, scale, shift, the activation or program, one
+    // rounding -- in a loop that is not unrolled, so the interpreter is
+    // emitted once per half, storing each run with a 16-byte write. Half by
+    // half, the accumulators it has stored are no longer live, which leaves
+    // the interpreter its registers.
+    constexpr int PW = WN * 4 + 16;  // f32 row pitch of a wave's region
+    static_assert(NW * (WM / 2) * PW <= LDS_BYTES, "the waves' regions fit");
+    uint8_t* region = lds + wave * (WM / 2) * PW;
+    __syncthreads();  // every wave is done with the stages
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+#pragma unroll
+      for (int i = q * (FM / 2); i < (q + 1) * (FM / 2); ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            *(float*)(region + ((i - q * (FM / 2)) * 16 + 4 * fg + e) * PW + (j * 16 + (lane & 15)) * 4) =
+                acc[i][j][e];
+      constexpr int RUNS = WN / 8;  // runs of 8 columns per row
+#pragma unroll 1
+      for (int it = 0; it < (WM / 2) * RUNS / 64; ++it) {
+        const int idx = it * 64 + lane, r = idx / RUNS, c8 = (idx % RUNS) * 8;
+        const float4 lo = *(const float4*)(region + r * PW + c8 * 4);
+        const float4 hi = *(const float4*)(region + r * PW + c8 * 4 + 16);
+        float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        const int64_t col = n0 + wn * WN + c8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float bias, scale, shift;
+          column_vectors(g, col + e, true, bias, scale, shift);
+          v[e] = (v[e] + bias) * scale + shift;
+        }
+        activate_all<8, ACT == ACT_PROG>(g, v);
+        const int64_t row = m0 + wm * WM + q * (WM / 2) + r;
+        if constexpr (BF16) {
+          store16_stream((uint16_t*)g.c + off + row * g.ldc + col, Elem<uint16_t>::pack(v));
+        } else {
+          float* cp = (float*)g.c + off + row * g.ldc + col;
+          store16_stream(cp, Elem<float>::pack(v));
+          store16_stream(cp + 4, Elem<float>::pack(v + 4));
+        }
+      }
+    }
+  } else if constexpr (BF16) {
     // bf16 C goes through LDS (free once every wave is done with the last
     // stage) as the whole 256 x 256 tile, 512-byte rows whose 16-byte chunk c
     // sits in slot c ^ cswz(row), then leaves in whole rows: written straight
@@ -1295,7 +1352,16 @@ void launch_bf16_dma_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
         case HMX_EPI_IDENTITY: launch(gemm_bf16_mi16_kernel<LB, ACT_ID, BF16>, grid, 512, s, g); return;
         case HMX_EPI_RELU: launch(gemm_bf16_mi16_kernel<LB, ACT_RELU, BF16>, grid, 512, s, g); return;
         case HMX_EPI_SILU: launch(gemm_bf16_mi16_kernel<LB, ACT_SILU, BF16>, grid, 512, s, g); return;
-        default: break;
+        default:
+          // Other epilogues store 16-byte runs of C rows (f32 C: 4-element
+          // aligned rows too).
+          if (BF16 || ((((uintptr_t)g.c) & 15) == 0 && g.ldc % 4 == 0 && g.stride_c % 4 == 0 &&
+                       g.stride_split % 4 == 0)) {
+            if (g.act == HMX_EPI_PROGRAM) launch(gemm_bf16_mi16_kernel<LB, ACT_PROG, BF16>, grid, 512, s, g);
+            else launch(gemm_bf16_mi16_kernel<LB, ACT_ANY, BF16>, grid, 512, s, g);
+            return;
+          }
+          break;
       }
     }
   }
@@ -1312,14 +1378,20 @@ void launch_bf16_dma_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
       case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, NW, 256>, grid, NW * 64, s, g); break;
       case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, NW, 256>, grid, NW * 64, s, g); break;
       case HMX_EPI_IDENTITY: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, NW, 256>, grid, NW * 64, s, g); break;
-      default: launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, NW, 256>, grid, NW * 64, s, g); break;
+      default:
+        if (g.act == HMX_EPI_PROGRAM) launch(gemm_bf16_dma64_kernel<LB, ACT_PROG, BF16, NW, 256>, grid, NW * 64, s, g);
+        else launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, NW, 256>, grid, NW * 64, s, g);
+        break;
     }
   } else if constexpr (LB != L_VNNI_PANELS) {
     switch (g.act) {
       case HMX_EPI_RELU: launch(gemm_bf16_dma_kernel<LB, ACT_RELU, BF16>, grid, 256, s, g); break;
       case HMX_EPI_SILU: launch(gemm_bf16_dma_kernel<LB, ACT_SILU, BF16>, grid, 256, s, g); break;
       case HMX_EPI_IDENTITY: launch(gemm_bf16_dma_kernel<LB, ACT_ID, BF16>, grid, 256, s, g); break;
-      default: launch(gemm_bf16_dma_kernel<LB, ACT_ANY, BF16>, grid, 256, s, g); break;
+      default:
+        if (g.act == HMX_EPI_PROGRAM) launch(gemm_bf16_dma_kernel<LB, ACT_PROG, BF16>, grid, 256, s, g);
+        else launch(gemm_bf16_dma_kernel<LB, ACT_ANY, BF16>, grid, 256, s, g);
+        break;
     }
   }
 }
@@ -1383,7 +1455,10 @@ void launch_bf16_dma_narrow(const GemmArgs& g, dim3 grid, hipStream_t s) {
     case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 4, 128>, grid, 256, s, g); break;
     case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 4, 128>, grid, 256, s, g); break;
     case HMX_EPI_IDENTITY: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 4, 128>, grid, 256, s, g); break;
-    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, 4, 128>, grid, 256, s, g); break;
+    default:
+        if (g.act == HMX_EPI_PROGRAM) launch(gemm_bf16_dma64_kernel<LB, ACT_PROG, BF16, 4, 128>, grid, 256, s, g);
+        else launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, 4, 128>, grid, 256, s, g);
+        break;
   }
 }
 
@@ -1415,7 +1490,10 @@ void launch_bf16_dma_ragged(const GemmArgs& g, dim3 grid, hipStream_t s) {
     case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 8, 256, true>, grid, 512, s, g); break;
     case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 8, 256, true>, grid, 512, s, g); break;
     case HMX_EPI_IDENTITY: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 8, 256, true>, grid, 512, s, g); break;
-    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, 8, 256, true>, grid, 512, s, g); break;
+    default:
+        if (g.act == HMX_EPI_PROGRAM) launch(gemm_bf16_dma64_kernel<LB, ACT_PROG, BF16, 8, 256, true>, grid, 512, s, g);
+        else launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, 8, 256, true>, grid, 512, s, g);
+        break;
   }
 }
 
@@ -1444,7 +1522,10 @@ void launch_bf16_dma128_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
     case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
     case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
     case HMX_EPI_IDENTITY: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
-    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
+    default:
+        if (g.act == HMX_EPI_PROGRAM) launch(gemm_bf16_dma64_kernel<LB, ACT_PROG, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g);
+        else launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g);
+        break;
   }
 }
 
@@ -1476,7 +1557,10 @@ void launch_bf16_dma_ta_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
     case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 8, 256, false, 256, true>, grid, 512, s, g); break;
     case HMX_EPI_SILU: launch(gemm_bf16_dma64_kernel<LB, ACT_SILU, BF16, 8, 256, false, 256, true>, grid, 512, s, g); break;
     case HMX_EPI_IDENTITY: launch(gemm_bf16_dma64_kernel<LB, ACT_ID, BF16, 8, 256, false, 256, true>, grid, 512, s, g); break;
-    default: launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, 8, 256, false, 256, true>, grid, 512, s, g); break;
+    default:
+        if (g.act == HMX_EPI_PROGRAM) launch(gemm_bf16_dma64_kernel<LB, ACT_PROG, BF16, 8, 256, false, 256, true>, grid, 512, s, g);
+        else launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, 8, 256, false, 256, true>, grid, 512, s, g);
+        break;
   }
 }
 

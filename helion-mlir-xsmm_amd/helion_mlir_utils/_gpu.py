@@ -117,7 +117,7 @@ def epilogue_code(epilogue: Callable[[torch.Tensor], torch.Tensor]) -> Epilogue:
 
     Raises ``ValueError`` for a callable they cannot fuse: an epilogue is
     never run as a separate eager pass behind the caller's back."""
-    from ._program import compile_epilogue
+    from ._program import traced_epilogue
 
     if isinstance(epilogue, Activation):
         return epilogue.code, epilogue.arg, None
@@ -132,7 +132,7 @@ def epilogue_code(epilogue: Callable[[torch.Tensor], torch.Tensor]) -> Epilogue:
             return (native.EPI_GELU_TANH if approx == "tanh" else native.EPI_GELU), 0.0, None
     if epilogue is identity_epilogue or getattr(epilogue, "__name__", None) == "identity_epilogue":
         return IDENTITY
-    program = compile_epilogue(epilogue, 1)
+    program = traced_epilogue(epilogue, 1)
     if program is None:
         return IDENTITY
     if len(program.code) == 1 and program.code[0].a == 0 and program.code[0].op in _NAMED_PROGRAMS:

@@ -23,6 +23,7 @@ from __future__ import annotations
 
 import math
 import operator
+import weakref
 from typing import Callable, NamedTuple
 
 import torch
@@ -31,7 +32,7 @@ import torch.nn.functional as F
 
 from helion_mlir_backend._compiler import native
 
-__all__ = ["EpilogueProgram", "compile_epilogue"]
+__all__ = ["EpilogueProgram", "compile_epilogue", "traced_epilogue"]
 
 _OP = native.OP
 
@@ -423,6 +424,38 @@ def _op_name(node: fx.Node) -> str:
     if name is None:
         raise ValueError(f"the gpu target cannot fuse {node.op} {node.target!r} in an epilogue")
     return name
+
+
+# Programs traced so far, by callable object and arity. Tracing (torch.fx)
+# takes hundreds of microseconds, more than many GEMMs; the reference likewise
+# binds an epilogue once and keeps the bound kernel in an LRU keyed by the
+# epilogue object (helion_mlir_utils/matmul.py:487-489). Entries go with the
+# callable; a full table is cleared.
+_TRACED: "weakref.WeakKeyDictionary[Callable[..., torch.Tensor], dict[int, EpilogueProgram | None]]" = (
+    weakref.WeakKeyDictionary()
+)
+_TRACED_MAX = 256
+
+
+def traced_epilogue(fn: Callable[..., torch.Tensor], arity: int = 1) -> EpilogueProgram | None:
+    """:func:`compile_epilogue`, traced once per callable object: later calls
+    with the same object reuse its program (a closure's captured scalars are
+    read when it is first traced; pass a new callable to change them).
+    Callables that cannot be weakly referenced are traced every time."""
+    try:
+        known = _TRACED.get(fn)
+    except TypeError:
+        return compile_epilogue(fn, arity)
+    if known is not None and arity in known:
+        return known[arity]
+    program = compile_epilogue(fn, arity)
+    if len(_TRACED) >= _TRACED_MAX:
+        _TRACED.clear()
+    try:
+        _TRACED.setdefault(fn, {})[arity] = program
+    except TypeError:
+        pass
+    return program
 
 
 def compile_epilogue(fn: Callable[..., torch.Tensor], arity: int = 1) -> EpilogueProgram | None:

@@ -96,13 +96,13 @@ def _extra_op(epilogue: Callable[[Tensor, Tensor], Tensor]) -> tuple[int, int, f
     extra operand, ``GroupNormEpilogue``, or any other elementwise
     ``epilogue(y, extra)`` traced into an epilogue program (extra op none: the
     program reads the extra operand itself)."""
-    from ._program import compile_epilogue
+    from ._program import traced_epilogue
 
     if isinstance(epilogue, GroupNormEpilogue) and epilogue.activation[0] != native.EPI_PROGRAM:
         return epilogue.extra_op, epilogue.activation[0], epilogue.activation[1], None
     if epilogue in _EXTRA_OPS:
         return _EXTRA_OPS[epilogue], native.EPI_IDENTITY, 0.0, None
-    program = compile_epilogue(epilogue, 2)
+    program = traced_epilogue(epilogue, 2)
     if program is None:
         return native.EXTRA_NONE, native.EPI_IDENTITY, 0.0, None
     return native.EXTRA_NONE, native.EPI_PROGRAM, 0.0, program.struct

@@ -167,3 +167,19 @@ def test_programs_pass_through_as_epilogues() -> None:
     # The structure the library reads holds the instructions as traced.
     assert [(struct.code[i].op, struct.code[i].dst) for i in range(2)] == [(i.op, i.dst) for i in program.code]
     assert math.isclose(struct.code[1].c0, 1.0)
+
+
+def test_a_callable_is_traced_once() -> None:
+    # Tracing takes longer than many GEMMs: the program of a callable object
+    # is kept with it (as the reference keeps a bound kernel per epilogue
+    # object), a new callable is traced anew.
+    s = 2.0
+    fn = lambda x: F.silu(x) * s  # noqa: E731
+    first = U._gpu.epilogue_code(fn)
+    s = 3.0
+    again = U._gpu.epilogue_code(fn)
+    assert again[2] is first[2] and first[2].code[1].c0 == 2.0
+    other = U._gpu.epilogue_code(lambda x: F.silu(x) * s)
+    assert other[2] is not first[2] and other[2].code[1].c0 == 3.0
+    # The public compiler traces every time.
+    assert compile_epilogue(fn).code[1].c0 == 3.0
