@@ -208,11 +208,16 @@ __device__ __forceinline__ float program_op(int op, float a, float b, float c0, 
   }
 }
 
+// N f32 values of one program register.
+template <int N>
+using program_vec = float __attribute__((ext_vector_type(N)));
+
 // One instruction on n values: the opcode (uniform across the wave) is
 // dispatched once for all of them.
 template <int N>
-__device__ __forceinline__ void program_op_n(int op, const float (&x)[N], const float (&y)[N], float c0,
-                                             float c1, float (&out)[N]) {
+__device__ __forceinline__ program_vec<N> program_op_n(int op, program_vec<N> x, program_vec<N> y, float c0,
+                                                       float c1) {
+  program_vec<N> out;
   switch (op) {
 #define HMX_OP_CASE(OP, EXPR)         \
   case OP:                            \
@@ -224,10 +229,9 @@ __device__ __forceinline__ void program_op_n(int op, const float (&x)[N], const 
     break;
     HMX_PROGRAM_OPS(HMX_OP_CASE)
 #undef HMX_OP_CASE
-    default:
-#pragma unroll
-      for (int i = 0; i < N; ++i) out[i] = x[i];
+    default: out = x;
   }
+  return out;
 }
 
 // Register i of a program's register file. The index is uniform across the
@@ -257,65 +261,65 @@ __device__ __forceinline__ float run_program(const hmx_program& p, float x, floa
   return program_reg(r, p.result);
 }
 
-// Register k (uniform) of n values' register files, by a branch on k rather
-// than a select per register and value.
-template <int N>
-__device__ __forceinline__ void program_read_n(const float (&r)[HMX_PROGRAM_REGS][N], int k, float (&out)[N]) {
-  switch (k) {
-#define HMX_REG_CASE(K)                                 \
-  case K:                                               \
-    _Pragma("unroll") for (int i = 0; i < N; ++i) out[i] = r[K][i]; \
-    break;
-    HMX_REG_CASE(0) HMX_REG_CASE(1) HMX_REG_CASE(2) HMX_REG_CASE(3)
-    HMX_REG_CASE(4) HMX_REG_CASE(5) HMX_REG_CASE(6) HMX_REG_CASE(7)
-#undef HMX_REG_CASE
-    default:
-#pragma unroll
-      for (int i = 0; i < N; ++i) out[i] = 0.f;
-  }
-}
-
-template <int N>
-__device__ __forceinline__ void program_write_n(float (&r)[HMX_PROGRAM_REGS][N], int k, const float (&v)[N]) {
-  switch (k) {
-#define HMX_REG_CASE(K)                                 \
-  case K:                                               \
-    _Pragma("unroll") for (int i = 0; i < N; ++i) r[K][i] = v[i]; \
-    break;
-    HMX_REG_CASE(0) HMX_REG_CASE(1) HMX_REG_CASE(2) HMX_REG_CASE(3)
-    HMX_REG_CASE(4) HMX_REG_CASE(5) HMX_REG_CASE(6) HMX_REG_CASE(7)
-#undef HMX_REG_CASE
-    default: break;
-  }
-}
-static_assert(HMX_PROGRAM_REGS == 8, "the register file's cases");
-
 // Runs the program on n values in place (register 0 of value i is v[i],
 // register 1 extra[i]): the instructions in turn, each read, computed and
 // written for all n values at once, so opcodes and register numbers are
-// dispatched once per instruction, not once per value.
+// dispatched once per instruction, not once per value. The registers are
+// eight separate vector variables, read and written in the arms of a branch
+// on the (uniform) register number: an array indexed in those arms would be
+// merged by the compiler into one access at a computed index, which puts
+// the register file in scratch memory.
 template <int N>
 __device__ __forceinline__ void run_program_n(const hmx_program& p, float (&v)[N], const float (&extra)[N]) {
-  float r[HMX_PROGRAM_REGS][N];
+  using V = program_vec<N>;
+  V r0, r1, r2 = V(0.f), r3 = V(0.f), r4 = V(0.f), r5 = V(0.f), r6 = V(0.f), r7 = V(0.f);
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    r[0][i] = v[i];
-    r[1][i] = extra[i];
-#pragma unroll
-    for (int j = 2; j < HMX_PROGRAM_REGS; ++j) r[j][i] = 0.f;
+    r0[i] = v[i];
+    r1[i] = extra[i];
+  }
+#define HMX_REG_READ(OUT, K)   \
+  switch (K) {                 \
+    case 0: OUT = r0; break;   \
+    case 1: OUT = r1; break;   \
+    case 2: OUT = r2; break;   \
+    case 3: OUT = r3; break;   \
+    case 4: OUT = r4; break;   \
+    case 5: OUT = r5; break;   \
+    case 6: OUT = r6; break;   \
+    case 7: OUT = r7; break;   \
+    default: OUT = V(0.f);     \
   }
   const int count = __builtin_amdgcn_readfirstlane(p.count);
+  // Each instruction is fetched one step ahead, so that its (scalar) load
+  // is not waited for at the top of every step.
+  hmx_instr next = p.code[0];
 #pragma unroll 1
   for (int k = 0; k < count; ++k) {
-    const hmx_instr ins = p.code[k];
-    const int op = __builtin_amdgcn_readfirstlane(ins.op);
-    float a[N], b[N], y[N];
-    program_read_n<N>(r, __builtin_amdgcn_readfirstlane(ins.a), a);
-    program_read_n<N>(r, __builtin_amdgcn_readfirstlane(ins.b), b);
-    program_op_n<N>(op, a, b, ins.c0, ins.c1, y);
-    program_write_n<N>(r, __builtin_amdgcn_readfirstlane(ins.dst), y);
+    const hmx_instr ins = next;
+    next = p.code[k + 1 < HMX_PROGRAM_MAX ? k + 1 : k];
+    V a, b;
+    HMX_REG_READ(a, __builtin_amdgcn_readfirstlane(ins.a))
+    HMX_REG_READ(b, __builtin_amdgcn_readfirstlane(ins.b))
+    const V y = program_op_n<N>(__builtin_amdgcn_readfirstlane(ins.op), a, b, ins.c0, ins.c1);
+    switch (__builtin_amdgcn_readfirstlane(ins.dst)) {
+      case 0: r0 = y; break;
+      case 1: r1 = y; break;
+      case 2: r2 = y; break;
+      case 3: r3 = y; break;
+      case 4: r4 = y; break;
+      case 5: r5 = y; break;
+      case 6: r6 = y; break;
+      case 7: r7 = y; break;
+      default: break;
+    }
   }
-  program_read_n<N>(r, __builtin_amdgcn_readfirstlane(p.result), v);
+  V out;
+  HMX_REG_READ(out, __builtin_amdgcn_readfirstlane(p.result))
+#undef HMX_REG_READ
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = out[i];
 }
+static_assert(HMX_PROGRAM_REGS == 8, "the register file's variables");
 
 }  // namespace hmx

@@ -130,15 +130,30 @@ __device__ __forceinline__ void column_vectors(const GemmArgs& g, int64_t col, b
 }
 
 
+// f(std::integral_constant<int, I>) for the runtime index i == I (0 <= i <
+// N). A loop the compiler leaves rolled (one around an epilogue program's
+// interpreter is too large to unroll) reads the accumulators through it, by a
+// constant index in each branch: indexed by the loop counter they would be
+// moved to scratch memory.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void with_index(int i, F&& f) {
+  if constexpr (I + 1 < N) {
+    if (i == I)
+      f(std::integral_constant<int, I>{});
+    else
+      with_index<N, I + 1>(i, f);
+  } else {
+    f(std::integral_constant<int, I>{});
+  }
+}
+
 // The epilogue's activation on N values in place: a named code, or with
 // PROG (kernels instantiated for epilogue programs only, so the others do not
 // carry the interpreter's registers) the program.
 template <int N, bool PROG>
 __device__ __forceinline__ void activate_all(const GemmArgs& g, float (&v)[N]) {
   if (PROG && g.act == HMX_EPI_PROGRAM) {
-    float none[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i) none[i] = 0.f;
+    const float none[N] = {};
     run_program_n<N>(g.prog, v, none);
   } else {
     // One switch per value: dispatching once for all N values unrolls every
@@ -263,11 +278,14 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& g, float* lds, i
   const int64_t col0 = n0 + wn * WN;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
+    with_index<FM>(i, [&](auto i_c) {
+      constexpr int I = decltype(i_c)::value;
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        ep[(8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * P + j * 32 + (lane & 31)] = acc[i][j][e];
+        for (int e = 0; e < 16; ++e)
+          ep[(8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * P + j * 32 + (lane & 31)] = acc[I][j][e];
+    });
     __syncthreads();
     const int64_t row0 = m0 + wm * WM + i * 32;
     for (int idx = lane; idx < 32 * (WN / 4); idx += 64) {

@@ -850,14 +850,17 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
     __syncthreads();  // every wave is done with the stages
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
+      with_index<2>(q, [&](auto q_c) {
+        constexpr int Q = decltype(q_c)::value;
 #pragma unroll
-      for (int i = q * (FM / 2); i < (q + 1) * (FM / 2); ++i)
+        for (int i = Q * (FM / 2); i < (Q + 1) * (FM / 2); ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
+          for (int j = 0; j < FN; ++j)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            *(float*)(region + ((i - q * (FM / 2)) * 16 + 4 * fg + e) * PW + (j * 16 + (lane & 15)) * 4) =
-                acc[i][j][e];
+            for (int e = 0; e < 4; ++e)
+              *(float*)(region + ((i - Q * (FM / 2)) * 16 + 4 * fg + e) * PW + (j * 16 + (lane & 15)) * 4) =
+                  acc[i][j][e];
+      });
       constexpr int RUNS = WN / 8;  // runs of 8 columns per row
 #pragma unroll 1
       for (int it = 0; it < (WM / 2) * RUNS / 64; ++it) {

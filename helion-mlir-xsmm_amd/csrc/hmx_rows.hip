@@ -515,9 +515,11 @@ __device__ __forceinline__ void load_row_raw(const T* __restrict__ p, int li, in
 // is whole: n == tpr * VPL * EPV; a group is gv = gs / EPV vectors, either
 // the whole row (ONE) or a power of two dividing tpr, so vector j of a lane
 // belongs to the group of the gv aligned lanes around it. Statistics are
-// f32: mean, then the centered variance, per group.
-template <typename T, int EPV, int VPL, bool ONE, bool EXTRA>
-__global__ __launch_bounds__(kMaxBlock) void group_norm_rows(const T* x, T* y, GroupNormArgs a,
+// f32: mean, then the centered variance, per group. PROG: the epilogue is a
+// program on (normalized value, extra), EXTRA then meaning that an extra
+// operand is given (else register 1 reads 0).
+template <typename T, int EPV, int VPL, bool ONE, bool EXTRA, bool PROG = false>
+__global__ __launch_bounds__(PROG ? kBlock : kMaxBlock) void group_norm_rows(const T* x, T* y, GroupNormArgs a,
                                                              int64_t rows, int tpr, int gv) {
   __shared__ float red_mean[VPL * kMaxWavesPerRow], red_var[VPL * kMaxWavesPerRow];
   const int rpb = tpr <= kWave ? (int)blockDim.x / tpr : 1;
@@ -599,15 +601,27 @@ __global__ __launch_bounds__(kMaxBlock) void group_norm_rows(const T* x, T* y, G
         const int i = j * EPV + e;
         float yv = (v[i] - mean[j]) * r[j] * wv[i];
         yv += bv[i];
-        if constexpr (EXTRA) {
+        if constexpr (EXTRA && !PROG) {
           if (a.extra_op == HMX_EXTRA_ADD) yv += ev[i];
           if (a.extra_op == HMX_EXTRA_MUL) yv *= ev[i];
         }
         v[i] = yv;
-        ex[i] = 0.f;
+        if constexpr (EXTRA && PROG) ex[i] = ev[i];
+        else ex[i] = 0.f;
       }
     }
-    group_norm_finish<VPL * EPV, false>(a, v, ex);
+    if constexpr (PROG) {
+      // The program on one row vector (EPV values) at a time: its register
+      // file for EPV values, not the lane's whole row.
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        float (&vj)[EPV] = *reinterpret_cast<float (*)[EPV]>(&v[j * EPV]);
+        const float (&ej)[EPV] = *reinterpret_cast<const float (*)[EPV]>(&ex[j * EPV]);
+        run_program_n<EPV>(a.prog, vj, ej);
+      }
+    } else {
+      group_norm_finish<VPL * EPV, false>(a, v, ex);
+    }
     store_row<T, EPV, VPL, true>(y + row * n, n, li, tpr, v);
     if (next >= rows) break;
     row = next;
@@ -1037,12 +1051,6 @@ int hmx_group_norm_rows(int dtype, const void* x, const void* w, const void* b,
     using T = std::remove_pointer_t<decltype(tp)>;
     constexpr int EPV = decltype(epv_c)::value;
     const RowShape r = row_shape(group_size, EPV);
-    if (activation == HMX_EPI_PROGRAM) {
-      // Epilogue programs run in the streaming kernel only: the cached
-      // kernels stay free of the interpreter's registers.
-      launch(group_norm_stream<T, EPV, true>, unit_grid(units), kBlock, s, (const T*)x, (T*)y, a);
-      return;
-    }
     if constexpr (EPV > 1) {
       // Whole rows in registers when the row fits and each group is one run
       // of aligned lanes (or the whole row): w, b and extra stay resident.
@@ -1050,30 +1058,49 @@ int hmx_group_norm_rows(int dtype, const void* x, const void* w, const void* b,
       const RowShape rr = row_shape(row_n, EPV);
       const int64_t gv = group_size / EPV;
       const bool one = groups == 1;
-      if (a.vec_ok && rr.vpl > 0 && rr.whole && (one || ((gv & (gv - 1)) == 0 && gv <= rr.tpr))) {
+      // A program's interpreter needs more than the 128 VGPRs of a
+      // 1024-thread workgroup: its kernels are built for rows of at most
+      // kBlock threads.
+      const bool fits = activation != HMX_EPI_PROGRAM || row_block(rr) <= (unsigned)kBlock;
+      if (a.vec_ok && rr.vpl > 0 && rr.whole && fits && (one || ((gv & (gv - 1)) == 0 && gv <= rr.tpr))) {
         const int rpb = rr.tpr <= kWave ? (int)(kBlock / rr.tpr) : 1;
         const unsigned block = row_block(rr);
         with_vpl<EPV>(rr.vpl, [&](auto vpl_c) {
           constexpr int VPL = decltype(vpl_c)::value;
-          auto go = [&](auto one_c, auto extra_c) {
-            constexpr auto kernel = &group_norm_rows<T, EPV, VPL, decltype(one_c)::value, decltype(extra_c)::value>;
+          auto go = [&](auto one_c, auto extra_c, auto prog_c) {
+            constexpr auto kernel = &group_norm_rows<T, EPV, VPL, decltype(one_c)::value, decltype(extra_c)::value,
+                                                     decltype(prog_c)::value>;
             // As many workgroups as the GPU holds at once, each walking rows
             // blockIdx, blockIdx + grid, ...
             const int64_t resident = (int64_t)resident_blocks<kernel>((int)block) * current_device_shape().cus;
             launch(kernel, dim3((unsigned)std::min(ceil_div(m, rpb), resident)), block, s, (const T*)x, (T*)y, a,
                    m, rr.tpr, (int)gv);
           };
-          const bool extra = extra_op != HMX_EXTRA_NONE;
-          if (one) {
-            if (extra) go(std::true_type{}, std::true_type{});
-            else go(std::true_type{}, std::false_type{});
-          } else {
-            if (extra) go(std::false_type{}, std::true_type{});
-            else go(std::false_type{}, std::false_type{});
-          }
+          // With a program, EXTRA: an extra operand is given (the program
+          // reads it); else: an extra op applies.
+          const bool program = activation == HMX_EPI_PROGRAM;
+          const bool has_extra = program ? extra != nullptr : extra_op != HMX_EXTRA_NONE;
+          auto go2 = [&](auto one_c) {
+            if (program) {
+              if (has_extra) go(one_c, std::true_type{}, std::true_type{});
+              else go(one_c, std::false_type{}, std::true_type{});
+            } else {
+              if (has_extra) go(one_c, std::true_type{}, std::false_type{});
+              else go(one_c, std::false_type{}, std::false_type{});
+            }
+          };
+          if (one) go2(std::true_type{});
+          else go2(std::false_type{});
         });
         return;
       }
+    }
+    if (activation == HMX_EPI_PROGRAM) {
+      // Programs on rows the whole-row kernel does not take run in the
+      // streaming kernel: the cached kernels stay free of the interpreter's
+      // registers.
+      launch(group_norm_stream<T, EPV, true>, unit_grid(units), kBlock, s, (const T*)x, (T*)y, a);
+      return;
     }
     if (r.vpl == 0) {
       launch(group_norm_stream<T, EPV, false>, unit_grid(units), kBlock, s, (const T*)x, (T*)y, a);
