@@ -32,6 +32,9 @@ constexpr int kMaxPerLane = 16;
 // Waves of a workgroup that share one row.
 constexpr int kMaxWavesPerRow = 16;
 constexpr int kMaxBlock = kMaxWavesPerRow * kWave;
+// Workgroups of kernels that run an epilogue program: two waves per SIMD at
+// most, 256 VGPRs each.
+constexpr int kProgBlock = 8 * kWave;
 
 // ---------------------------------------------------------------------------
 // Row access. `tpr` threads share a row; thread `li` of them holds, as its
@@ -519,7 +522,7 @@ __device__ __forceinline__ void load_row_raw(const T* __restrict__ p, int li, in
 // program on (normalized value, extra), EXTRA then meaning that an extra
 // operand is given (else register 1 reads 0).
 template <typename T, int EPV, int VPL, bool ONE, bool EXTRA, bool PROG = false>
-__global__ __launch_bounds__(PROG ? kBlock : kMaxBlock) void group_norm_rows(const T* x, T* y, GroupNormArgs a,
+__global__ __launch_bounds__(PROG ? kProgBlock : kMaxBlock) void group_norm_rows(const T* x, T* y, GroupNormArgs a,
                                                              int64_t rows, int tpr, int gv) {
   __shared__ float red_mean[VPL * kMaxWavesPerRow], red_var[VPL * kMaxWavesPerRow];
   const int rpb = tpr <= kWave ? (int)blockDim.x / tpr : 1;
@@ -1060,8 +1063,8 @@ int hmx_group_norm_rows(int dtype, const void* x, const void* w, const void* b,
       const bool one = groups == 1;
       // A program's interpreter needs more than the 128 VGPRs of a
       // 1024-thread workgroup: its kernels are built for rows of at most
-      // kBlock threads.
-      const bool fits = activation != HMX_EPI_PROGRAM || row_block(rr) <= (unsigned)kBlock;
+      // kProgBlock threads.
+      const bool fits = activation != HMX_EPI_PROGRAM || row_block(rr) <= (unsigned)kProgBlock;
       if (a.vec_ok && rr.vpl > 0 && rr.whole && fits && (one || ((gv & (gv - 1)) == 0 && gv <= rr.tpr))) {
         const int rpb = rr.tpr <= kWave ? (int)(kBlock / rr.tpr) : 1;
         const unsigned block = row_block(rr);

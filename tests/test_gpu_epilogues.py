@@ -146,10 +146,11 @@ def test_prepacked_and_linear_take_programs(gpu_device) -> None:
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 @pytest.mark.parametrize("groups", [1, 32])
-@pytest.mark.parametrize("m,c", [(256, 4096), (3000, 2048), (700, 320)])
+@pytest.mark.parametrize("m,c", [(256, 4096), (3000, 2048), (64, 8192), (700, 320)])
 def test_group_norm_programs(gpu_device, dtype: str, groups: int, m: int, c: int) -> None:
-    # 3000 rows make the whole-row kernel walk several rows per block; 320
-    # channels in 32 groups (10 per group) take the streaming kernel.
+    # 3000 rows make the whole-row kernel walk several rows per block; 8192
+    # channels take 512-thread workgroups (bf16) or the streaming kernel
+    # (f32); 320 channels in 32 groups (10 per group) take the streaming kernel.
     x = tensor(RNG.normal(0, 2, (m, c)).astype(np.float32), dtype, gpu_device)
     w = torch.from_numpy(RNG.uniform(0.5, 1.5, c).astype(np.float32)).to(gpu_device)
     b = torch.from_numpy(RNG.normal(0, 0.5, c).astype(np.float32)).to(gpu_device)
