@@ -569,7 +569,11 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_dma64_kernel(GemmArgs g)
 // reads of stage t, and the barrier publishes t + 1 and frees t; slots 32-51
 // issue the 8 loads of stage t + 2 into it and slots 52-63 read stage t + 1's
 // k-step 0 fragments.
-template <int LB, int ACT, bool BF16, bool RAGGED = false, int BM = 256, int BN = 256, int NW = 8>
+//
+// S stages in LDS (4 for 128 x 128 tiles that run one workgroup per CU):
+// the loads issued in stage t are stage t + S's, so S - 1 stages are in
+// flight while one is read; the barrier waits only for stage t + 1.
+template <int LB, int ACT, bool BF16, bool RAGGED = false, int BM = 256, int BN = 256, int NW = 8, int S = 2>
 __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) {
   static_assert(LB == L_KCONTIG || LB == L_RCONTIG || LB == L_VNNI_PANELS || LB == L_PANELS || LB == L_BLOCKED,
                 "B [N, K], [K, N], VNNI panels, K-major panels or 32 x 32 blocks");
@@ -583,6 +587,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
                     (BM == 256 && BN == 128 && NW == 8),
                 "256 x 256 (8 waves), 128 x 128 (4 waves) or 256 x 128 (8 waves)");
   static_assert(BN == 256 || LB == L_KCONTIG || LB == L_RCONTIG, "packed B: 256-column tiles");
+  static_assert(S == 2 || (S == 4 && BM == 128 && BN == 128 && !staged_act(ACT)), "stages: 2, or 4 of 128 x 128");
   typedef float f32x4_t __attribute__((ext_vector_type(4)));
   // Packed B as in gemm_bf16_dma64_kernel: K-major panels and 32 x 32 blocks
   // land in LDS as the row-major [64 k][256 n] tile (BT), VNNI panels as
@@ -601,7 +606,8 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
   // ACT_ANY stages each wave's 64-row halves as f32, rows of WN * 4 + 16
   // bytes: 8 x 64 x 272 bytes, a little more than the stages.
   constexpr int EPI_BYTES = NW * (WM / 2) * (WN * 4 + 16);
-  constexpr int LDS_BYTES = staged_act(ACT) && EPI_BYTES > 2 * STAGE ? EPI_BYTES : 2 * STAGE;
+  constexpr int LDS_BYTES = staged_act(ACT) && EPI_BYTES > S * STAGE ? EPI_BYTES : S * STAGE;
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
 
   int tm, tn;
@@ -717,8 +723,8 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
   const uint32_t lds_wb = __builtin_amdgcn_readfirstlane(lds_addr(lds)) + A_BYTES + wave * LBN * 1024;
   auto dma = [&](int t, int q) {
     const int64_t k0 = k_begin + (int64_t)min(t, ktiles - 1) * BK;
-    const uint32_t st = lds_w + (uint32_t)((t & 1) * STAGE);
-    const uint32_t sb = lds_wb + (uint32_t)((t & 1) * STAGE);
+    const uint32_t st = lds_w + (uint32_t)((t & (S - 1)) * STAGE);
+    const uint32_t sb = lds_wb + (uint32_t)((t & (S - 1)) * STAGE);
     if (q < LA) {
       if constexpr (RAGGED)
         lds_dma16(srd_a, va[q], (int32_t)(k0 * 2), st + q * 1024);
@@ -792,10 +798,10 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
   // The host launches this kernel only with at least one K stage per split.
   bf16x8_t fa[2][FM], fb[2][FN];
 #pragma unroll
-  for (int q = 0; q < LOADS; ++q) dma(0, q);
+  for (int u = 0; u < S; ++u)
 #pragma unroll
-  for (int q = 0; q < LOADS; ++q) dma(1, q);
-  wait_vmem<LOADS>();  // stage 0 landed
+    for (int q = 0; q < LOADS; ++q) dma(u, q);
+  wait_vmem<LOADS * (S - 1)>();  // stage 0 landed
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < FM; ++i) fa[0][i] = a_read(0, 0, i);
@@ -803,12 +809,13 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
   for (int j = 0; j < FN; ++j) fb[0][j] = b_read(0, 0, j);
 
   for (int t = 0; t < ktiles; ++t) {
-    const int cur = t & 1, nxt = cur ^ 1;
+    const int cur = t & (S - 1), nxt = (t + 1) & (S - 1);
 #pragma unroll
     for (int x = 0; x < SLOTS; ++x) {
       __builtin_amdgcn_sched_barrier(0);
       const int ks = x / NS, sub = x % NS;
-      if (x == BAR) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (x == BAR)
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(LOADS * (S - 2)) : "memory");
       if (ks == 0 && sub < NF) {
         if (sub < FM) fa[1][sub] = a_read(cur, 1, sub);
         else fb[1][sub - FM] = b_read(cur, 1, sub - FM);
@@ -817,7 +824,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
       // next stage's fragment reads.
 #pragma unroll
       for (int q = (x - BAR) * LOADS / (LOAD_END - BAR); q < (x + 1 - BAR) * LOADS / (LOAD_END - BAR); ++q)
-        if (x >= BAR && x < LOAD_END) dma(t + 2, q);
+        if (x >= BAR && x < LOAD_END) dma(t + S, q);
       if (x >= SLOTS - NF) {
         const int f = x - (SLOTS - NF);
         if (f < FM) fa[0][f] = a_read(nxt, 0, f);
@@ -1502,24 +1509,37 @@ void launch_bf16_dma_ragged(const GemmArgs& g, dim3 grid, hipStream_t s) {
 
 // 128 x 128 tiles (four waves of 64 x 64), B K-contiguous or row-major, whole
 // or ragged.
+// Stages in LDS of the 16x16x32 kernel's 128 x 128 tiles: 4 (one workgroup
+// per CU, three stages in flight) or 2 (two workgroups per CU);
+// HMX_MI16_STAGES=2 or 4 overrides the choice, for comparison.
+int mi16_stages128(const GemmArgs& g, dim3 grid) {
+  static const int forced = [] {
+    const char* e = getenv("HMX_MI16_STAGES");
+    return e ? atoi(e) : 0;
+  }();
+  if (forced == 2 || forced == 4) return forced;
+  return (int64_t)grid.x * grid.y * grid.z <= g.cus ? 4 : 2;
+}
+
+template <int LB, bool BF16, bool RAGGED, int S>
+bool launch_mi16_128(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  switch (g.act) {
+    case HMX_EPI_IDENTITY: launch(gemm_bf16_mi16_kernel<LB, ACT_ID, BF16, RAGGED, 128, 128, 4, S>, grid, 256, s, g); return true;
+    case HMX_EPI_RELU: launch(gemm_bf16_mi16_kernel<LB, ACT_RELU, BF16, RAGGED, 128, 128, 4, S>, grid, 256, s, g); return true;
+    case HMX_EPI_SILU: launch(gemm_bf16_mi16_kernel<LB, ACT_SILU, BF16, RAGGED, 128, 128, 4, S>, grid, 256, s, g); return true;
+    default: return false;
+  }
+}
+
 template <int LB, bool BF16, bool RAGGED>
 void launch_bf16_dma128_c(const GemmArgs& g, dim3 grid, hipStream_t s) {
   // The 16x16x32 kernel from 16 stages per split on (1000 x 4096 x 4096:
   // 51 -> 44 us); short chunks (1024^3 split four ways: 16 -> 17.5 us) keep
   // the 32x32x16 kernel.
   if (mi16_args_ok(g) && g.k_chunk >= 16 * 64) {
-    switch (g.act) {
-      case HMX_EPI_IDENTITY:
-        launch(gemm_bf16_mi16_kernel<LB, ACT_ID, BF16, RAGGED, 128, 128, 4>, grid, 256, s, g);
-        return;
-      case HMX_EPI_RELU:
-        launch(gemm_bf16_mi16_kernel<LB, ACT_RELU, BF16, RAGGED, 128, 128, 4>, grid, 256, s, g);
-        return;
-      case HMX_EPI_SILU:
-        launch(gemm_bf16_mi16_kernel<LB, ACT_SILU, BF16, RAGGED, 128, 128, 4>, grid, 256, s, g);
-        return;
-      default: break;
-    }
+    const bool done = mi16_stages128(g, grid) == 4 ? launch_mi16_128<LB, BF16, RAGGED, 4>(g, grid, s)
+                                                   : launch_mi16_128<LB, BF16, RAGGED, 2>(g, grid, s);
+    if (done) return;
   }
   switch (g.act) {
     case HMX_EPI_RELU: launch(gemm_bf16_dma64_kernel<LB, ACT_RELU, BF16, 4, 128, RAGGED, 128>, grid, 256, s, g); break;
