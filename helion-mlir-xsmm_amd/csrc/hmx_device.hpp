@@ -264,13 +264,74 @@ __device__ __forceinline__ float run_program(const hmx_program& p, float x, floa
 // Runs the program on n values in place (register 0 of value i is v[i],
 // register 1 extra[i]): the instructions in turn, each read, computed and
 // written for all n values at once, so opcodes and register numbers are
-// dispatched once per instruction, not once per value. The registers are
-// eight separate vector variables, read and written in the arms of a branch
-// on the (uniform) register number: an array indexed in those arms would be
-// merged by the compiler into one access at a computed index, which puts
-// the register file in scratch memory.
+// dispatched once per instruction, not once per value. The register file is
+// held as arrays of 8 registers x at most 4 values indexed by the (uniform)
+// register number: the compiler keeps arrays of that size in VGPRs and reads
+// and writes register k with indexed moves (s_set_gpr_idx), with no branch
+// per register (8 x 8 values in one array would go to scratch memory).
 template <int N>
 __device__ __forceinline__ void run_program_n(const hmx_program& p, float (&v)[N], const float (&extra)[N]) {
+  constexpr int H = N > 4 ? 4 : N;  // values per array
+  static_assert(N == H || N == 2 * H, "at most two arrays of four values");
+  constexpr int R = HMX_PROGRAM_REGS * H;
+  float r0[R], r1[N > H ? R : 1];
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    r0[i] = v[i];
+    r0[H + i] = extra[i];
+    if constexpr (N > H) {
+      r1[i] = v[H + i];
+      r1[H + i] = extra[H + i];
+    }
+  }
+#pragma unroll
+  for (int i = 2 * H; i < R; ++i) {
+    r0[i] = 0.f;
+    if constexpr (N > H) r1[i] = 0.f;
+  }
+  const int count = __builtin_amdgcn_readfirstlane(p.count);
+  // Each instruction is fetched one step ahead, so that its (scalar) load
+  // is not waited for at the top of every step.
+  hmx_instr next = p.code[0];
+#pragma unroll 1
+  for (int k = 0; k < count; ++k) {
+    const hmx_instr ins = next;
+    next = p.code[k + 1 < HMX_PROGRAM_MAX ? k + 1 : k];
+    const int a = __builtin_amdgcn_readfirstlane(ins.a) * H, b = __builtin_amdgcn_readfirstlane(ins.b) * H;
+    const int d = __builtin_amdgcn_readfirstlane(ins.dst) * H;
+    program_vec<N> x, y;
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      x[i] = r0[a + i];
+      y[i] = r0[b + i];
+      if constexpr (N > H) {
+        x[H + i] = r1[a + i];
+        y[H + i] = r1[b + i];
+      }
+    }
+    const program_vec<N> out = program_op_n<N>(__builtin_amdgcn_readfirstlane(ins.op), x, y, ins.c0, ins.c1);
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      r0[d + i] = out[i];
+      if constexpr (N > H) r1[d + i] = out[H + i];
+    }
+  }
+  const int res = __builtin_amdgcn_readfirstlane(p.result) * H;
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    v[i] = r0[res + i];
+    if constexpr (N > H) v[H + i] = r1[res + i];
+  }
+}
+
+// run_program_n for kernels whose VGPRs are mostly taken (the GEMM
+// epilogues): the same instructions in turn, each for all n values at once,
+// with the registers in eight separate vector variables read and written in
+// the arms of a branch on the (uniform) register number. (One array indexed
+// in those arms would be merged by the compiler into a single access at a
+// computed index, which puts the register file in scratch memory.)
+template <int N>
+__device__ __forceinline__ void run_program_branches_n(const hmx_program& p, float (&v)[N], const float (&extra)[N]) {
   using V = program_vec<N>;
   V r0, r1, r2 = V(0.f), r3 = V(0.f), r4 = V(0.f), r5 = V(0.f), r6 = V(0.f), r7 = V(0.f);
 #pragma unroll

@@ -153,8 +153,11 @@ __device__ __forceinline__ void with_index(int i, F&& f) {
 template <int N, bool PROG>
 __device__ __forceinline__ void activate_all(const GemmArgs& g, float (&v)[N]) {
   if (PROG && g.act == HMX_EPI_PROGRAM) {
+    // The branch-per-register interpreter: the indexed register file of the
+    // row kernels spills in the 256-VGPR GEMM kernels (config 4 with a
+    // 4-instruction program: 1000 -> 1405 us).
     const float none[N] = {};
-    run_program_n<N>(g.prog, v, none);
+    run_program_branches_n<N>(g.prog, v, none);
   } else {
     // One switch per value: dispatching once for all N values unrolls every
     // activation N times, and the registers that takes spilled (GELU-tanh

@@ -398,9 +398,13 @@ __device__ __forceinline__ float group_norm_pre(const GroupNormArgs& a, float ce
 template <int N, bool PROG>
 __device__ __forceinline__ void group_norm_finish(const GroupNormArgs& a, float (&v)[N],
                                                   const float (&extra)[N]) {
-  if (PROG && a.act == HMX_EPI_PROGRAM) {
-    run_program_n<N>(a.prog, v, extra);
-  } else if (a.act != HMX_EPI_IDENTITY) {
+  if constexpr (PROG) {
+    if (a.act == HMX_EPI_PROGRAM) {
+      run_program_n<N>(a.prog, v, extra);
+      return;
+    }
+  }
+  if (a.act != HMX_EPI_IDENTITY) {
 #pragma unroll
     for (int i = 0; i < N; ++i) v[i] = apply_activation(a.act, v[i], a.act_arg);
   }
