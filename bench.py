@@ -733,7 +733,7 @@ def main() -> int:
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (every box here has one GPU; "
-              "the sharded design is described in DESIGN.md)", file=sys.stderr)
+              "the path is measured on one GPU's share at its real shape)", file=sys.stderr)
         return 2
 
     import torch
