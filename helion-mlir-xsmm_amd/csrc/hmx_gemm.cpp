@@ -113,7 +113,7 @@ constexpr int64_t kTransposeMinRows = 512;
 // tiles count one per CU: on a skinny 32 x 11008 x 4096 product four splits
 // (344 workgroups) measure 26 us, eight 36 us.
 int auto_splits(TileChoice tile, int64_t tiles, int64_t m, int64_t n, int64_t k, int64_t batch,
-                int64_t esz, int64_t max_ws, int cus) {
+                int64_t esz, int64_t max_ws, int cus, bool fill = false) {
   const int64_t kt = ceil_div(k, tile.bk);
   const int64_t operand_bytes = batch * (m + n) * k * esz;
   const int64_t resident = (tile.bm == 256 || esz == 2 ? 1 : 4) * (int64_t)cus;
@@ -122,7 +122,20 @@ int auto_splits(TileChoice tile, int64_t tiles, int64_t m, int64_t n, int64_t k,
     const int s2 = splits * 2;
     if (tiles * splits >= resident || kt / s2 < 8) break;
     const int64_t need = (int64_t)s2 * batch * m * n * 4;
-    if ((max_ws >= 0 && need > max_ws) || 2 * need > operand_bytes / 4) break;
+    // The f32 partials' traffic (written once, read once) at most an eighth
+    // of the operands'. With `fill`, bf16 128 x 128 tiles of products of at
+    // least 2^30 multiply-adds, K in whole stages, also split while the grid
+    // stays within one workgroup per CU, each chunk keeps 16 or more stages
+    // and the partials move at most the operands' bytes: a grid of one such
+    // workgroup per CU on a few CUs is latency-bound, and filling the CUs
+    // pays for the partials (same box, unsplit -> split: 1024 x 1024 x 4096
+    // 31.5 -> 21.5 us, 512 x 2048 x 8192 57 -> 28.5 us, 256 x 4000 x 4096
+    // 33.7 -> 27.9 us, 768 x 768 x 3072 24.5 -> 20.5 us; a grid past one
+    // workgroup per CU loses the four-stage ring: 256 x 11008 x 4096
+    // 36 -> 44.5 us in two).
+    const bool fills = fill && esz == 2 && tile.bm == 128 && k % tile.bk == 0 && kt / s2 >= 16 && tiles * s2 <= cus &&
+                       (double)batch * m * n * k >= 1073741824.0 && need <= operand_bytes;
+    if ((max_ws >= 0 && need > max_ws) || (2 * need > operand_bytes / 4 && !fills)) break;
     splits = s2;
   }
   return splits;
@@ -225,7 +238,7 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
   const int64_t tiles = ceil_div(m, plan.tile.bm) * ceil_div(n, plan.tile.bn) * batch;
   const int64_t kt = ceil_div(k, plan.tile.bk);
   if (splits == 0) {
-    splits = auto_splits(plan.tile, tiles, m, n, k, batch, bf16 ? 2 : 4, max_ws, cus);
+    splits = auto_splits(plan.tile, tiles, m, n, k, batch, bf16 ? 2 : 4, max_ws, cus, true);
     if (!bf16 && plan.tile.bm < 256 && tiles * 4 <= cus)
       splits = std::max(splits, small_f32_splits(tiles, kt, batch * m * n, max_ws, cus));
   }

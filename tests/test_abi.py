@@ -160,7 +160,17 @@ def test_plans_of_the_baseline_configs(lib: ctypes.CDLL) -> None:
     assert _plan(lib, bf16, 4000, 4096, 4100) == (1, 256, 256, 64, 4096 * 4100 * 2)
     assert _plan(lib, bf16, 4000, 4096, 4100, max_ws=0) == (1, 256, 256, 64, 0)
     # Few output rows do not amortize the transpose.
-    assert _plan(lib, bf16, 256, 4000, 4096)[4] == 0
+    assert _plan(lib, bf16, 256, 4000, 4100)[4] == 0
+    # Few 128 x 128 tiles with K in whole stages split K until the grid holds
+    # one workgroup per CU (the workspace holds the f32 partials only).
+    assert _plan(lib, bf16, 256, 4000, 4096) == (4, 128, 128, 64, 4 * 256 * 4000 * 4)
+    assert _plan(lib, bf16, 1024, 1024, 4096) == (4, 128, 128, 64, 4 * 1024 * 1024 * 4)
+    assert _plan(lib, bf16, 1024, 2048, 4096)[:4] == (2, 128, 128, 64)
+    # Not past one workgroup per CU, not below 16 stages per chunk, not for
+    # small products.
+    assert _plan(lib, bf16, 256, 11008, 4096)[0] == 1
+    assert _plan(lib, bf16, 384, 384, 2048)[0] == 1
+    assert _plan(lib, bf16, 2048, 1024, 2048)[0] == 1
     # Fused linear, 8192 x 11008 x 4096 (B row-major here): 1376 tiles, no split.
     assert _plan(lib, bf16, 8192, 11008, 4096)[:4] == (1, 256, 256, 64)
     # Split-K bmm [16, 256, 65536] @ [16, 65536, 256]: one 256 x 256 tile per
