@@ -128,11 +128,27 @@ __device__ __forceinline__ float apply_activation(int code, float x, float arg) 
       return x * __builtin_amdgcn_rcpf(1.f + __expf(-x));
     case HMX_EPI_SIGMOID:
       return __builtin_amdgcn_rcpf(1.f + __expf(-x));
-    case HMX_EPI_GELU:
-      return 0.5f * x * (1.f + erff(x * 0.7071067811865476f));
+    case HMX_EPI_GELU: {
+      // 0.5 x (1 + erf(x / sqrt 2)) with erfc(z), z = |x| / sqrt 2, by
+      // Abramowitz & Stegun 7.1.26 (|error of erf| <= 1.5e-7): one
+      // reciprocal, a degree-5 polynomial and one exponential, the same
+      // instructions for every lane (the library erff branches on |z| < 1,
+      // and a GEMM epilogue of it cost a third of config 4's time).
+      // 1 + erf(x / sqrt 2) is 2 - erfc(z) for x >= 0, erfc(z) below, so
+      // the negative side keeps its relative accuracy.
+      const float z = fabsf(x) * 0.7071067811865476f;
+      const float t = __builtin_amdgcn_rcpf(1.f + 0.3275911f * z);
+      const float poly =
+          t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
+      const float erfc_z = poly * __expf(-z * z);
+      return 0.5f * x * (x >= 0.f ? 2.f - erfc_z : erfc_z);
+    }
     case HMX_EPI_GELU_TANH: {
+      // 0.5 x (1 + tanh(u)) = x / (1 + e^(-2u)) exactly: one exponential and
+      // a reciprocal instead of tanhf, with the same limits (x for u -> inf,
+      // -0 for u -> -inf, NaN for NaN).
       const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-      return 0.5f * x * (1.f + tanhf(u));
+      return x * __builtin_amdgcn_rcpf(1.f + __expf(-2.f * u));
     }
     case HMX_EPI_TANH:
       return tanhf(x);

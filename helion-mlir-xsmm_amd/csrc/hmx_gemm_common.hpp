@@ -279,6 +279,14 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& g, float* lds, i
   const bool vec_ok = (g.ldc % 4 == 0) &&
                       ((((uintptr_t)g.c) & (bf16 ? 7 : 15)) == 0) && (off % 4 == 0);
   const int64_t col0 = n0 + wn * WN;
+  // A lane's 4 columns are the same in every step below (64 is a multiple of
+  // WN / 4): their bias, scale and shift are loaded once (inside the loop the
+  // stores to C keep the compiler from hoisting the loads).
+  static_assert(64 % (WN / 4) == 0, "a lane's columns are the same in every step");
+  const int cq = (lane % (WN / 4)) * 4;
+  float cb[4], cs[4], ch[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) column_vectors(g, col0 + cq + t, !GUARD || col0 + cq + t < g.n, cb[t], cs[t], ch[t]);
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     with_index<FM>(i, [&](auto i_c) {
@@ -292,18 +300,13 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& g, float* lds, i
     __syncthreads();
     const int64_t row0 = m0 + wm * WM + i * 32;
     for (int idx = lane; idx < 32 * (WN / 4); idx += 64) {
-      const int r = idx / (WN / 4), cq = (idx % (WN / 4)) * 4;
+      const int r = idx / (WN / 4);
       const int64_t row = row0 + r, col = col0 + cq;
       if (GUARD && row >= g.m) continue;
       const float4 q = *(const float4*)(ep + r * P + cq);
       float v[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const bool in = !GUARD || col + t < g.n;
-        float bias, scale, shift;
-        column_vectors(g, col + t, in, bias, scale, shift);
-        v[t] = (v[t] + bias) * scale + shift;
-      }
+      for (int t = 0; t < 4; ++t) v[t] = (v[t] + cb[t]) * cs[t] + ch[t];
       activate_all<4, PROG>(g, v);
       const int64_t o = off + row * g.ldc + col;
       if ((!GUARD || col + 4 <= g.n) && vec_ok) {

@@ -854,6 +854,16 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
     constexpr int PW = WN * 4 + 16;  // f32 row pitch of a wave's region
     static_assert(NW * (WM / 2) * PW <= LDS_BYTES, "the waves' regions fit");
     uint8_t* region = lds + wave * (WM / 2) * PW;
+    constexpr int RUNS = WN / 8;  // runs of 8 columns per row
+    static_assert(64 % RUNS == 0, "a lane's run is the same in every step");
+    // The lane's 8 columns are the same in every step below: their bias,
+    // scale and shift are loaded once (inside the loop the stores to C keep
+    // the compiler from hoisting the loads).
+    const int c8 = (lane % RUNS) * 8;
+    const int64_t col = n0 + wn * WN + c8;
+    float cb[8], cs[8], ch[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) column_vectors(g, col + e, true, cb[e], cs[e], ch[e]);
     __syncthreads();  // every wave is done with the stages
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -868,20 +878,14 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
               *(float*)(region + ((i - Q * (FM / 2)) * 16 + 4 * fg + e) * PW + (j * 16 + (lane & 15)) * 4) =
                   acc[i][j][e];
       });
-      constexpr int RUNS = WN / 8;  // runs of 8 columns per row
 #pragma unroll 1
       for (int it = 0; it < (WM / 2) * RUNS / 64; ++it) {
-        const int idx = it * 64 + lane, r = idx / RUNS, c8 = (idx % RUNS) * 8;
+        const int r = (it * 64 + lane) / RUNS;
         const float4 lo = *(const float4*)(region + r * PW + c8 * 4);
         const float4 hi = *(const float4*)(region + r * PW + c8 * 4 + 16);
         float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-        const int64_t col = n0 + wn * WN + c8;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float bias, scale, shift;
-          column_vectors(g, col + e, true, bias, scale, shift);
-          v[e] = (v[e] + bias) * scale + shift;
-        }
+        for (int e = 0; e < 8; ++e) v[e] = (v[e] + cb[e]) * cs[e] + ch[e];
         activate_all<8, ACT == ACT_PROG>(g, v);
         const int64_t row = m0 + wm * WM + q * (WM / 2) + r;
         if constexpr (BF16) {
