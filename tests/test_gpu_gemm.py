@@ -243,6 +243,26 @@ def test_matmul_long_k_tiles(gpu_device, m, n, k, trans_b, tiles, act, f32_out) 
     _check(to_np(got), ref, k, to_np(a), to_np(b), "bf16")
 
 
+@pytest.mark.parametrize(("m", "n", "k", "trans_b", "splits"), [
+    (1024, 1024, 4096, False, 4), (256, 4000, 4096, True, 4), (768, 768, 3072, False, 2),
+    (128, 4096, 4096, True, 4), (512, 2048, 8192, False, 4),
+])
+@pytest.mark.parametrize(("act", "f32_out"), [("identity", False), ("gelu", True), ("silu", False)])
+def test_matmul_fill_splits(gpu_device, m, n, k, trans_b, splits, act, f32_out) -> None:
+    # Few 128 x 128 tiles with K in whole stages: split K until the grid holds
+    # one workgroup per CU; the partials are summed in split order.
+    if torch.cuda.get_device_properties(gpu_device).multi_processor_count == 256:
+        plan = U.gemm_plan(torch.bfloat16, m, n, k, trans_b=trans_b)
+        assert (plan["splits"], plan["tile_m"]) == (splits, 128)
+    a, b = _operands(m, n, k, False, trans_b, "bf16", gpu_device, 0.3)
+    bias = tensor(RNG.normal(0, 1, n).astype(np.float32), "bf16", gpu_device)
+    out_dtype = torch.float32 if f32_out else torch.bfloat16
+    got = U.matmul(a, b, trans_b=trans_b, bias=bias, epilogue=ACTS[act], out_dtype=out_dtype)
+    ref = R.matmul(to_np(a), to_np(b), False, trans_b, to_np(bias), act=act, out="f32" if f32_out else "bf16")
+    _check(to_np(got), ref, k, to_np(a), to_np(b), "bf16")
+    assert torch.equal(got, U.matmul(a, b, trans_b=trans_b, bias=bias, epilogue=ACTS[act], out_dtype=out_dtype))
+
+
 @pytest.mark.parametrize(("m", "n", "k", "lda"), [
     (1, 11008, 4096, 0), (32, 11008, 4096, 0), (12, 9000, 512, 0), (31, 17000, 256, 0),  # 2 waves
     (8, 4096, 4096, 0), (16, 203, 192, 0), (17, 1000, 64, 0), (32, 300, 128, 0), (5, 33, 640, 0),  # 4 waves
