@@ -199,3 +199,52 @@ def test_noalloc_runs_programs(gpu_device) -> None:
     torch.cuda.synchronize()
     ref = R.matmul(to_np(a), to_np(b), act=fn, out="bf16")
     _check(to_np(c), ref, k, to_np(a), to_np(b), "bf16")
+
+
+def _exact_activation(name: str, x: np.ndarray) -> np.ndarray:
+    """The named activations in float64 from their definitions (math.erf,
+    tanh, exp): the accuracy bound the kernels' fast forms are held to."""
+    import math
+
+    x = x.astype(np.float64)
+    if name == "silu":
+        return x / (1.0 + np.exp(-x))
+    if name == "sigmoid":
+        return 1.0 / (1.0 + np.exp(-x))
+    if name == "gelu":
+        return 0.5 * x * (1.0 + np.vectorize(math.erf)(x / math.sqrt(2.0)))
+    u = math.sqrt(2.0 / math.pi) * (x + 0.044715 * x ** 3)
+    # 1 + tanh(u) cancels in float64 too once u < -5; there it is
+    # 2 / (1 + e^-2u), the same number without the cancellation.
+    return np.where(u > -5.0, 0.5 * x * (1.0 + np.tanh(u)), x / (1.0 + np.exp(-2.0 * u)))
+
+
+@pytest.mark.parametrize("name", ["silu", "sigmoid", "gelu", "gelu_tanh"])
+def test_fast_activations_accuracy(gpu_device, name: str) -> None:
+    import math
+
+    # C = I @ X passes X through the f32 GEMM exactly, so the epilogue sees
+    # the values themselves. SiLU and sigmoid (hardware reciprocal) and
+    # tanh-GELU (x / (1 + e^-2u)) stay within 2e-6 relative over [-12, 12]
+    # (e^x as v_exp_f32 of x log2 e loses up to ~1e-6 at |x| = 12); GELU's
+    # erf by Abramowitz & Stegun 7.1.26 within its 1.5e-7 absolute bound on
+    # erf, 0.5 |x| 1.5e-7 on GELU, plus the same relative rounding. A wrong
+    # coefficient or branch fails these by orders of magnitude.
+    x = np.linspace(-12.0, 12.0, 128 * 512, dtype=np.float32).reshape(128, 512)
+    eye = torch.eye(128, device=gpu_device)
+    fn = {"silu": F.silu, "sigmoid": torch.sigmoid, "gelu": F.gelu, "gelu_tanh": U.Activation("gelu_tanh")}[name]
+    got = to_np(U.matmul(eye, torch.from_numpy(x).to(gpu_device), epilogue=fn)).astype(np.float64)
+    exact = _exact_activation(name, x)
+    err = np.abs(got - exact)
+    if name == "gelu":
+        assert (err <= 0.5 * np.abs(x) * 2e-7 + 2e-6 * np.abs(exact) + 1e-30).all(), float(err.max())
+    elif name == "gelu_tanh":
+        # u = sqrt(2/pi) (x + 0.044715 x^3) itself is an f32 value: its
+        # rounding (~|u| 2^-24) moves e^(-2u) by a relative 2|u| 2^-24, which
+        # far out on the negative side outweighs the rest. (torch, adding
+        # tanh(u) to 1 in f32, returns 0 there.)
+        u = np.abs(math.sqrt(2.0 / math.pi) * (x.astype(np.float64) + 0.044715 * x.astype(np.float64) ** 3))
+        assert (err <= (2e-6 + 4e-7 * u) * np.abs(exact) + 1e-30).all(), float(err.max())
+    else:
+        # (Values below 1e-30, where f32 has underflowed as torch's does, are exempt.)
+        assert (err <= 2e-6 * np.abs(exact) + 1e-30).all(), float((err / np.maximum(np.abs(exact), 1e-30)).max())
