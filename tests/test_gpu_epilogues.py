@@ -211,6 +211,8 @@ def _exact_activation(name: str, x: np.ndarray) -> np.ndarray:
         return x / (1.0 + np.exp(-x))
     if name == "sigmoid":
         return 1.0 / (1.0 + np.exp(-x))
+    if name == "tanh":
+        return np.tanh(x)
     if name == "gelu":
         return 0.5 * x * (1.0 + np.vectorize(math.erf)(x / math.sqrt(2.0)))
     u = math.sqrt(2.0 / math.pi) * (x + 0.044715 * x ** 3)
@@ -219,20 +221,22 @@ def _exact_activation(name: str, x: np.ndarray) -> np.ndarray:
     return np.where(u > -5.0, 0.5 * x * (1.0 + np.tanh(u)), x / (1.0 + np.exp(-2.0 * u)))
 
 
-@pytest.mark.parametrize("name", ["silu", "sigmoid", "gelu", "gelu_tanh"])
+@pytest.mark.parametrize("name", ["silu", "sigmoid", "gelu", "gelu_tanh", "tanh"])
 def test_fast_activations_accuracy(gpu_device, name: str) -> None:
     import math
 
     # C = I @ X passes X through the f32 GEMM exactly, so the epilogue sees
-    # the values themselves. SiLU and sigmoid (hardware reciprocal) and
-    # tanh-GELU (x / (1 + e^-2u)) stay within 2e-6 relative over [-12, 12]
+    # the values themselves. SiLU and sigmoid (hardware reciprocal), tanh
+    # (series below 0.25, 1 - 2 / (1 + e^2|x|) above) and tanh-GELU
+    # (x / (1 + e^-2u)) stay within 2e-6 relative over [-12, 12]
     # (e^x as v_exp_f32 of x log2 e loses up to ~1e-6 at |x| = 12); GELU's
     # erf by Abramowitz & Stegun 7.1.26 within its 1.5e-7 absolute bound on
     # erf, 0.5 |x| 1.5e-7 on GELU, plus the same relative rounding. A wrong
     # coefficient or branch fails these by orders of magnitude.
     x = np.linspace(-12.0, 12.0, 128 * 512, dtype=np.float32).reshape(128, 512)
     eye = torch.eye(128, device=gpu_device)
-    fn = {"silu": F.silu, "sigmoid": torch.sigmoid, "gelu": F.gelu, "gelu_tanh": U.Activation("gelu_tanh")}[name]
+    fn = {"silu": F.silu, "sigmoid": torch.sigmoid, "gelu": F.gelu, "gelu_tanh": U.Activation("gelu_tanh"),
+          "tanh": torch.tanh}[name]
     got = to_np(U.matmul(eye, torch.from_numpy(x).to(gpu_device), epilogue=fn)).astype(np.float64)
     exact = _exact_activation(name, x)
     err = np.abs(got - exact)
