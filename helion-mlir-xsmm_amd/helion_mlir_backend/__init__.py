@@ -14,6 +14,7 @@ from ._compiler import native as _native
 from ._compiler import output_pool as output_pool
 from ._compiler.native import set_native_call as set_native_call
 from ._compiler.output_pool import set_output_pool as set_output_pool
+from ._compiler.prepared import GpuLaunch as GpuLaunch
 from ._compiler.prepared import PreparedCall as PreparedCall
 from ._compiler.prepared import prepared_call as prepared_call
 from ._compiler.support.errors import UnsupportedTargetError as UnsupportedTargetError
@@ -40,6 +41,7 @@ def explain() -> dict[str, object]:
 
 
 __all__ = [
+    "GpuLaunch",
     "InlineMLIRHint",
     "PreparedCall",
     "UnsupportedTargetError",

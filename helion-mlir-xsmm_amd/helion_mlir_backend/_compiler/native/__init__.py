@@ -270,20 +270,26 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
-# Native calls are always on for the gpu target; the switch is kept for the
-# reference's API (set_native_call), which turns the CPU target's native
-# paths on and off.
+# The native call switch (HELION_MLIR_NATIVE_CALL, set_native_call), as in the
+# reference (native/__init__.py:73-95): it governs the prepared-call paths.
 _enabled = os.environ.get(NATIVE_CALL_ENV, "").strip().lower() not in ("0", "false", "no", "off")
 
 
 def enabled() -> bool:
+    """Whether prepared calls launch natively (:func:`set_native_call`)."""
     return _enabled
 
 
 def set_native_call(enabled: bool) -> None:
-    """Kept for the reference's API (``helion_mlir_backend.set_native_call``).
-    The gpu target has a single, native path: turning it off makes its entry
-    points raise rather than run anything else."""
+    """Turn the native call paths on or off for the whole process
+    (``helion_mlir_backend.set_native_call``; ``HELION_MLIR_NATIVE_CALL``
+    gives the initial state, read once at import). Off takes effect at once
+    for every prepared call (each checks it per call): it takes its fallback,
+    the general entry point; and ``prepared_call`` made while off returns
+    ``None``, as the reference's kernels compiled while off have no native
+    run. The ``helion_mlir_utils`` entry points themselves launch their
+    ``libhmx`` kernels either way: on this target there is no other path to
+    take."""
     global _enabled
     _enabled = bool(enabled)
 

@@ -149,7 +149,8 @@ def _launcher(
         bias=vec_bias, scale=vec_scale, shift=vec_shift, vec_dtype=vec_dtype, epilogue=epilogue_code(epilogue),
         tiles=(tile_m, 0, 0) if tile_m else None,
     )
-    return prepared_call(lambda a: launch.run(a, weight), [x], general)
+    prepared = prepared_call(launch, (x, weight), [0], general)
+    return general if prepared is None else prepared
 
 
 def _with_call(cache, epilogue, make: Callable[[], Callable[[Tensor], Tensor]]):

@@ -34,6 +34,7 @@ from torch import Tensor
 
 from helion_mlir_backend import output_pool
 from helion_mlir_backend._compiler import native
+from helion_mlir_backend._compiler.prepared import GpuLaunch
 
 from ._gpu import IDENTITY, SUPPORTED_DTYPES, Epilogue, epilogue_code, identity_epilogue, is_gpu, on_device
 
@@ -187,7 +188,7 @@ def gemm_plan(a_dtype: torch.dtype, m: int, n: int, k: int, batch: int = 1,
     return {"splits": s, "tile_m": tm, "tile_n": tn, "tile_k": tk, "workspace_bytes": ws}
 
 
-class GemmLaunch:
+class GemmLaunch(GpuLaunch):
     """One ``hmx_gemm`` problem with everything but the operand and output
     data pointers bound: the plan (splits, workspace bytes), shapes, strides,
     layout, epilogue and per-column vectors. A call allocates C (and the
@@ -196,7 +197,8 @@ class GemmLaunch:
     reference's ``PreparedRun`` (``native/call.cpp:703-830``). The bound
     vectors are kept alive by the launch."""
 
-    __slots__ = ("_fn", "_args", "_vectors", "_ws_bytes", "_device", "_shape", "_dtype", "splits")
+    __slots__ = ("_fn", "_args", "_vectors", "_ws_bytes", "_staged_ws", "_rows_ok", "_device", "_shape",
+                 "_dtype", "splits")
 
     def __init__(
         self, ab: int, c_dtype: torch.dtype, device: torch.device, c_shape: tuple[int, ...],
@@ -230,10 +232,24 @@ class GemmLaunch:
             None,
         ]
         self._ws_bytes = ws_bytes
+        # The plan assumes operands in 16-byte aligned rows. An epilogue
+        # program on operands that are not runs staged (f32 partials, then
+        # the reduction) and needs the partials too: such calls pass a larger
+        # workspace.
+        partials = batch * m * n * 4
+        program = epilogue[0] == native.EPI_PROGRAM and layout in (native.B_ROW, native.B_TRANS)
+        self._staged_ws = ws_bytes + partials if program and ws_bytes < partials else None
+        vec = 8 if ab == native.DTYPE_BF16 else 4
+        self._rows_ok = all(v % vec == 0 for v in (lda, ldb, stride_a, stride_b))
         self._device = device
         self._shape = c_shape
         self._dtype = c_dtype
         self.splits = s
+
+    def __call__(self, a: Tensor, b: Tensor) -> Tensor:
+        """C = the bound GEMM of ``a`` and ``b`` in a fresh output (the
+        :class:`~helion_mlir_backend.PreparedCall` protocol)."""
+        return self.run(a, b)
 
     def run(self, a: Tensor, b: Tensor, c: Tensor | None = None) -> Tensor:
         """C = the bound GEMM of ``a`` and ``b`` (buffers as planned)."""
@@ -244,8 +260,12 @@ class GemmLaunch:
         args[5] = b.data_ptr()
         args[10] = c.data_ptr()
         ws = None
-        if self._ws_bytes > 0:
-            ws = torch.empty(self._ws_bytes, dtype=torch.uint8, device=self._device)
+        ws_bytes = self._ws_bytes
+        if self._staged_ws is not None and (not self._rows_ok or a.data_ptr() % 16 or b.data_ptr() % 16):
+            ws_bytes = self._staged_ws
+            args[28] = ws_bytes
+        if ws_bytes > 0:
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=self._device)
             args[27] = ws.data_ptr()
         device = self._device
         if device.index is None or device.index == torch.cuda.current_device():
@@ -673,4 +693,5 @@ def prepacked_b_call(
         m, n, k, bias=bias_, scale=scale_, shift=shift_, vec_dtype=vec_dtype, epilogue=code,
         tiles=tiles,
     )
-    return prepared_call(lambda x: launch.run(x, b_buf), [a], general)
+    prepared = prepared_call(launch, (a, b_buf), [0], general)
+    return general if prepared is None else prepared

@@ -70,3 +70,30 @@ def test_row_kernels_replay(gpu_device) -> None:
     w = tensor(RNG.uniform(0.5, 1.5, 4096).astype(np.float32), "bf16", gpu_device)
     graph, out = _capture(lambda: U.rms_norm(U.softmax(x), w, 1e-6))
     _replays_match(graph, out, [x], lambda: U.rms_norm(U.softmax(x), w, 1e-6))
+
+
+def test_native_switch_sends_prepared_calls_to_the_fallback(gpu_device) -> None:
+    # set_native_call(False): a prepared linear takes its fallback (the
+    # general entry point, same kernel and plan: the same bits) and counts no
+    # native call; a linear prepared while off holds no prepared call.
+    import helion_mlir_backend as B
+
+    layer = torch.nn.Linear(512, 768).to(device=gpu_device, dtype=torch.bfloat16)
+    x = tensor(RNG.normal(0, 1, (256, 512)).astype(np.float32), "bf16", gpu_device)
+    with torch.no_grad():
+        y, cache = U.linear(x, layer, F.silu)
+        prepared = cache.call[1]
+        assert isinstance(prepared, B.PreparedCall)
+        before = prepared.native_calls
+        try:
+            B.set_native_call(False)
+            y_off, _ = U.linear(x, layer, F.silu, cache=cache)
+            assert prepared.native_calls == before
+            _, fresh = U.linear(x, layer, F.silu)
+            assert not isinstance(fresh.call[1], B.PreparedCall)
+        finally:
+            B.set_native_call(True)
+        y_on, _ = U.linear(x, layer, F.silu, cache=cache)
+        assert prepared.native_calls == before + 1
+        torch.cuda.synchronize()
+    assert torch.equal(y, y_off) and torch.equal(y, y_on)
