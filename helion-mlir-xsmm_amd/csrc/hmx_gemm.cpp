@@ -159,6 +159,26 @@ bool skinny_shape(int ab_dtype, int64_t m, int64_t k, int64_t batch, int trans_a
          !trans_a && b_layout == HMX_B_TRANS && splits <= 1 && (no_tile || skinny_tile);
 }
 
+bool dma_enabled();
+
+// Whether an unsplit bf16 launch of this shape takes a direct-to-LDS kernel,
+// which runs epilogue programs fused (select_kernel's rules with operands
+// that keep 16-byte rows; B row-major or [N, K]).
+bool program_fused_shape(const Plan& plan, bool bf16, int64_t m, int64_t n, int64_t k, int trans_a,
+                         int b_layout) {
+  const bool plain_b = b_layout == HMX_B_ROW || b_layout == HMX_B_TRANS;
+  if (!bf16 || !plain_b || plan.splits > 1 || k <= 0 || plan.k_chunk % 32 != 0 || !dma_enabled())
+    return false;
+  const TileChoice t = plan.tile;
+  const bool whole = m % t.bm == 0 && n % t.bn == 0 && plan.k_chunk % t.bk == 0 && k % t.bk == 0;
+  const bool k64 = k % 64 == 0 && plan.k_chunk % 64 == 0;
+  // Spans past 2^31 bytes take the register-staged kernel.
+  const bool spans = m * k * 2 < INT32_MAX && n * k * 2 < INT32_MAX;
+  if (!spans) return false;
+  if (t.bm == 256) return trans_a ? whole : (whole || k64);
+  return t.bm == 128 && !trans_a && k64;
+}
+
 // A plan is a pure function of the problem, the request (splits, tile) and
 // the device's CU count. Passing a plan's own splits, tile and workspace
 // back reproduces it exactly: a tile request that names an instantiated tile
@@ -253,9 +273,15 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
   plan.splits = splits;
   // An epilogue program runs fused in the direct-to-LDS kernels; the others
   // write f32 products to the workspace (as one split) for the split-K
-  // reduction to finish, so its plan holds those partials even unsplit.
+  // reduction to finish, so their plan holds those partials even unsplit.
+  // The plan sees no pointers: it assumes operands that keep the 16-byte
+  // alignment of whole rows, and reserves the partials for packed B (whose
+  // panel widths it does not see) and for shapes no fused kernel takes.
+  // hmx_gemm asks for them only when the launch stages the program.
   const int64_t partial_bytes =
-      splits > 1 || program ? (int64_t)std::max(splits, 1) * batch * m * n * 4 : 0;
+      splits > 1 || (program && !program_fused_shape(plan, bf16, m, n, k, trans_a, b_layout))
+          ? (int64_t)std::max(splits, 1) * batch * m * n * 4
+          : 0;
   plan.bt_bytes = ceil_div(n * k * 2, 256) * 256;
   // The direct-to-LDS kernels read row-major B in place (256 x 256 tiles,
   // ragged M and N too, or transposed A on whole tiles; 128 x 128 tiles of
@@ -410,30 +436,18 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
   make_plan(ab_dtype, m, n, k, batch, trans_a, b_layout, splits,
             use_scratch ? kScratchBytes : (workspace ? workspace_bytes : 0), tile_m, tile_n, tile_k, dev.cus,
             epilogue, plan);
-  if (use_scratch) {
-    HMX_REQUIRE(plan.workspace_bytes <= kScratchBytes,
-                "gemm_noalloc: the launch needs %lld bytes of workspace and the library's scratch holds "
-                "%lld: ask for fewer splits (splits = 0 plans within the scratch)",
-                (long long)plan.workspace_bytes, (long long)kScratchBytes);
-    if (plan.workspace_bytes > 0) {
-      const int st = scratch_of_current_device(&workspace);
-      if (st != HMX_OK) return st;
-      workspace_bytes = kScratchBytes;
-    }
+  // Workspace is checked once the launch is known (below): a B transposed up
+  // front (plan.bt_bytes) and f32 partials for split-K or a staged epilogue
+  // program. The transposed B is read K-contiguous from the workspace.
+  if (use_scratch && plan.transpose_b) {
+    const int st = scratch_of_current_device(&workspace);
+    if (st != HMX_OK) return st;
+    workspace_bytes = kScratchBytes;
   }
-  if (plan.splits > 1 || program_epi) {
-    HMX_REQUIRE(workspace != nullptr && workspace_bytes >= plan.workspace_bytes,
-                "gemm: %s needs %lld workspace bytes, got %lld",
-                plan.splits > 1 ? "split-K" : "an epilogue program", (long long)plan.workspace_bytes,
-                (long long)workspace_bytes);
-  }
-  void* partials = workspace ? (char*)workspace + plan.bt_bytes : nullptr;
+  const void* b_given = b;
+  const int64_t ldb_given = ldb;
   int lb_run = lb;
   if (plan.transpose_b) {
-    // B [K, N] -> B^T [N, K] in the workspace; the GEMM then reads it K-contiguous.
-    launch_transpose16(b, workspace, k, n, ldb, (hipStream_t)stream);
-    const int st = check_launch("gemm B transpose");
-    if (st != HMX_OK) return st;
     b = workspace;
     ldb = k;
     lb_run = L_KCONTIG;
@@ -513,6 +527,30 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
   // the GEMM writes f32 partials ([splits, batch, M, N]) with the identity
   // epilogue, and the reduction applies bias, scale, shift and the epilogue.
   const bool staged = plan.splits > 1 || (program_epi && !runs_programs(kind));
+  const int64_t need = plan.bt_bytes + (staged ? (int64_t)std::max(plan.splits, 1) * batch * m * n * 4 : 0);
+  const char* what = plan.splits > 1 ? "split-K" : staged ? "an epilogue program on these operands"
+                                                           : "the B transpose";
+  if (use_scratch && need > 0) {
+    HMX_REQUIRE(need <= kScratchBytes,
+                "gemm_noalloc: %s needs %lld bytes of workspace and the library's scratch holds %lld%s", what,
+                (long long)need, (long long)kScratchBytes,
+                plan.splits > 1 ? ": ask for fewer splits (splits = 0 plans within the scratch)" : "");
+    if (workspace == nullptr) {
+      const int st = scratch_of_current_device(&workspace);
+      if (st != HMX_OK) return st;
+      workspace_bytes = kScratchBytes;
+    }
+  }
+  HMX_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need),
+              "gemm: %s needs %lld workspace bytes, got %lld", what, (long long)need,
+              (long long)(workspace ? workspace_bytes : 0));
+  void* partials = workspace ? (char*)workspace + plan.bt_bytes : nullptr;
+  if (plan.transpose_b) {
+    // B [K, N] -> B^T [N, K] in the workspace; the GEMM then reads it K-contiguous.
+    launch_transpose16(b_given, workspace, k, n, ldb_given, (hipStream_t)stream);
+    const int st = check_launch("gemm B transpose");
+    if (st != HMX_OK) return st;
+  }
   if (staged) {
     // Split-K grids of one tile per batch slice share no operand data between
     // workgroups: each walks its K chunk from a stage of its own, so the

@@ -119,7 +119,9 @@ def _gemm(lib: ctypes.CDLL, **kw: object) -> int:
         ({"epi": native.EPI_PROGRAM, "prog": "empty"}, "0 instructions"),
         ({"epi": native.EPI_PROGRAM, "prog": "bad_op"}, "unknown opcode"),
         ({"epi": native.EPI_PROGRAM, "prog": "bad_reg"}, "register past"),
-        ({"epi": native.EPI_PROGRAM, "prog": "ok"}, "an epilogue program needs"),
+        # An unaligned A takes the register-staged kernel, which leaves the
+        # program to the split-K reduction and needs the partials.
+        ({"epi": native.EPI_PROGRAM, "prog": "ok", "a": 18}, "an epilogue program on these operands needs"),
         ({"lda": 8}, "lda"),
         ({"ldb": 8}, "ldb"),
         ({"ldc": 8}, "ldc"),
@@ -287,9 +289,16 @@ _PLAN_LAYOUTS = [(native.B_ROW, 0), (native.B_TRANS, 0), (native.B_ROW, 1), (nat
 def test_program_epilogues_plan_their_partials(lib: ctypes.CDLL) -> None:
     bf16, f32 = native.DTYPE_BF16, native.DTYPE_F32
     prog = native.EPI_PROGRAM
-    # An unsplit product plans f32 partials of the whole output for kernels
-    # that leave the program to the reduction; split products plan them anyway.
-    assert _plan(lib, bf16, 4096, 4096, 4096, epi=prog) == (1, 256, 256, 64, 4096 * 4096 * 4)
+    # The direct-to-LDS bf16 kernels run programs fused: no partials. Shapes
+    # they do not take, packed B (whose panels the plan does not see) and f32
+    # plan f32 partials of the whole output for the reduction that finishes
+    # the program; split products plan them anyway.
+    assert _plan(lib, bf16, 4096, 4096, 4096, epi=prog) == (1, 256, 256, 64, 0)
+    assert _plan(lib, bf16, 8192, 11008, 4096, epi=prog, b_layout=native.B_TRANS)[4] == 0
+    assert _plan(lib, bf16, 4000, 4096, 4096, epi=prog)[4] == 0  # ragged M, K in whole stages
+    assert _plan(lib, bf16, 4000, 4096, 4100, epi=prog, max_ws=0)[4] == 4000 * 4096 * 4
+    assert _plan(lib, bf16, 4096, 4096, 4096, epi=prog, b_layout=native.B_BLOCKED)[4] == 4096 * 4096 * 4
+    assert _plan(lib, f32, 4096, 4096, 4096, epi=prog)[4] >= 4096 * 4096 * 4
     assert _plan(lib, f32, 512, 512, 512, epi=prog) == (4, 64, 64, 32, 4 * 512 * 512 * 4)
     # Decode-shaped products never take the skinny kernel with a program.
     assert _plan(lib, bf16, 32, 11008, 4096, b_layout=native.B_TRANS)[:4] == (1, 32, 32, 64)

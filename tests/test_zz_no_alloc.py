@@ -38,7 +38,8 @@ def _plan(a: torch.Tensor, m: int, n: int, k: int, batch: int,
 
 
 def _gemm(a: torch.Tensor, b: torch.Tensor, noalloc: bool, bias: torch.Tensor | None = None,
-          act: int = native.EPI_IDENTITY, splits: int = 0) -> tuple[int, torch.Tensor]:
+          act: int = native.EPI_IDENTITY, splits: int = 0,
+          program: "native.Program | None" = None) -> tuple[int, torch.Tensor]:
     """C[i] = act(A[i] @ B[i] + bias) of A [batch, M, K], B [batch, K, N]
     (row-major), through one of the two entry points; (status, C)."""
     batch, m, k = a.shape
@@ -48,7 +49,7 @@ def _gemm(a: torch.Tensor, b: torch.Tensor, noalloc: bool, bias: torch.Tensor | 
     head = (native.dtype_code(a.dtype), native.dtype_code(c.dtype), a.data_ptr(), k, 0,
             b.data_ptr(), n, native.B_ROW, 0, 0, c.data_ptr(), n, m, n, k, batch, m * k, k * n, m * n,
             native.ptr(bias), None, None, native.dtype_code(a.dtype) if bias is not None else native.DTYPE_F32,
-            act, 0.0, None, splits)
+            act, 0.0, native.program_arg(program), splits)
     if noalloc:
         status = native.lib().hmx_gemm_noalloc(*head, 0, 0, 0, stream)
     else:
@@ -131,3 +132,27 @@ def test_noalloc_refuses_splits_beyond_the_scratch(gpu_device) -> None:
     # splits = 0 plans within the scratch and runs.
     st, _ = _gemm(a, b, True)
     assert st == native.OK, native.last_error()
+
+
+def test_noalloc_program_epilogue_past_the_scratch_size(gpu_device) -> None:
+    # An epilogue program that the direct-to-LDS kernel runs fused needs no
+    # workspace: a bf16 [8192, 4096] x [4096, 4096] product (its f32 partials
+    # would be 128 MiB, twice the scratch) runs through hmx_gemm_noalloc, twice,
+    # and equals hmx_gemm; the second call is smaller.
+    prog = native.Program()
+    prog.count = 2
+    prog.code[0] = native.Instr(native.OP["silu"], 1, 0, 0, 0.0, 0.0)
+    prog.code[1] = native.Instr(native.OP["mul_c"], 2, 1, 0, 2.0, 0.0)
+    prog.result = 2
+    for m, n, k in ((8192, 4096, 4096), (4096, 2048, 1024)):
+        a, b = _operands(1, m, n, k, "bf16", gpu_device)
+        assert _plan(a, m, n, k, 1, native.EPI_PROGRAM)[4] == 0
+        st, got = _gemm(a, b, True, act=native.EPI_PROGRAM, program=prog)
+        assert st == native.OK, native.last_error()
+        st, ref = _gemm(a, b, False, act=native.EPI_PROGRAM, program=prog)
+        assert st == native.OK, native.last_error()
+        assert torch.equal(got, ref)
+        rows = np.arange(0, m, 997)
+        exact = R.matmul(to_np(a[0][rows]), to_np(b[0]), act="silu", out="f32") * 2.0
+        assert max_rel_error(to_np(got[0][rows]), exact) < 1e-2
+        del a, b, got, ref
