@@ -134,8 +134,10 @@ __device__ __forceinline__ float apply_activation(int code, float x, float arg) 
       // reciprocal, a degree-5 polynomial and one exponential, the same
       // instructions for every lane (the library erff branches on |z| < 1,
       // and a GEMM epilogue of it cost a third of config 4's time).
-      // 1 + erf(x / sqrt 2) is 2 - erfc(z) for x >= 0, erfc(z) below, so
-      // the negative side keeps its relative accuracy.
+      // 1 + erf(x / sqrt 2) is 2 - erfc(z) for x >= 0, erfc(z) below (no
+      // cancellation), but the formula's error bound is absolute: on the
+      // negative side, where GELU is small, the relative error grows (about
+      // 3e-6 at x = -2, 1.6e-3 at x = -5, 4e-2 at x = -13).
       const float z = fabsf(x) * 0.7071067811865476f;
       const float t = __builtin_amdgcn_rcpf(1.f + 0.3275911f * z);
       const float poly =

@@ -135,7 +135,8 @@ def epilogue_code(epilogue: Callable[[torch.Tensor], torch.Tensor]) -> Epilogue:
     program = traced_epilogue(epilogue, 1)
     if program is None:
         return IDENTITY
-    if len(program.code) == 1 and program.code[0].a == 0 and program.code[0].op in _NAMED_PROGRAMS:
+    if (len(program.code) == 1 and program.code[0].a == 0 and program.result == program.code[0].dst
+            and program.code[0].op in _NAMED_PROGRAMS):
         ins = program.code[0]
         return _NAMED_PROGRAMS[ins.op], ins.c0, None
     return native.EPI_PROGRAM, 0.0, program.struct

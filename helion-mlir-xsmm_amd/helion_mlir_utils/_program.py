@@ -486,6 +486,39 @@ def compile_epilogue(fn: Callable[..., torch.Tensor], arity: int = 1) -> Epilogu
     def source(v: object) -> object:
         return alias.get(v, v) if isinstance(v, fx.Node) else v
 
+    # In-place activations (``F.relu(x, inplace=True)`` and the like) write
+    # their input: every later use of that value, or of an alias of it, reads
+    # the activation's result. Rewrite those uses to the activation's node,
+    # then recompute the aliases.
+    rewritten = False
+    for i, node in enumerate(nodes):
+        if node.op not in ("call_function", "call_method") or node.kwargs.get("inplace") is not True:
+            continue
+        if not node.args or not isinstance(node.args[0], fx.Node):
+            raise ValueError(f"the gpu epilogue cannot fuse in-place {node.target!r} of a constant")
+        written = source(node.args[0])
+        for later in nodes[i + 1:]:
+            for arg in list(later.all_input_nodes):
+                if source(arg) is written:
+                    later.replace_input_with(arg, node)
+        rewritten = True
+    # Operations whose result nothing reads (a discarded activation) are dead:
+    # dropped, so they cost no instruction.
+    changed = True
+    while changed:
+        changed = False
+        for node in reversed(list(graph.nodes)):
+            if node.op in ("call_function", "call_method") and not node.users:
+                graph.erase_node(node)
+                names.pop(node, None)
+                changed = rewritten = True
+    if rewritten:
+        nodes = list(graph.nodes)
+        alias.clear()
+        for node in nodes:
+            if names.get(node) == "identity" and node.args and isinstance(node.args[0], fx.Node):
+                alias[node] = alias.get(node.args[0], node.args[0])
+
     last_use: dict[fx.Node, int] = {}
     for i, node in enumerate(nodes):
         for arg in node.all_input_nodes:

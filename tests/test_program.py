@@ -183,3 +183,51 @@ def test_a_callable_is_traced_once() -> None:
     assert other[2] is not first[2] and other[2].code[1].c0 == 3.0
     # The public compiler traces every time.
     assert compile_epilogue(fn).code[1].c0 == 3.0
+
+
+def _relu_inplace_then_scale(x):
+    F.relu(x, inplace=True)
+    return x * 2
+
+
+def _silu_inplace_plus_input(x):
+    y = F.silu(x, inplace=True)
+    return y + x
+
+
+def _alias_then_leaky_inplace(x):
+    y = x.float()  # an alias of x: the in-place op below writes it too
+    F.leaky_relu(x, 0.1, inplace=True)
+    return y - 1
+
+
+def _hardtanh_inplace(x):
+    F.hardtanh(x, -0.5, 0.5, inplace=True)
+    return x
+
+
+@pytest.mark.parametrize("fn", [_relu_inplace_then_scale, _silu_inplace_plus_input, _alias_then_leaky_inplace,
+                                _hardtanh_inplace])
+def test_inplace_activations_write_their_input(fn) -> None:
+    # An in-place activation changes the value every later use reads; the
+    # program must give what eager torch gives on a fresh copy.
+    x = _values()
+    program = compile_epilogue(fn)
+    assert program is not None
+    torch.testing.assert_close(program(x.clone()), fn(x.clone()), rtol=0, atol=0, equal_nan=True)
+
+
+def test_discarded_results_cost_nothing() -> None:
+    # A result nothing reads is dead code: the identity stays the identity,
+    # and one in-place activation returned as its input is that activation.
+    def discard(x):
+        torch.relu(x)
+        return x
+
+    def relu_inplace(x):
+        F.relu(x, inplace=True)
+        return x
+
+    assert compile_epilogue(discard) is None
+    assert U._gpu.epilogue_code(discard)[0] == native.EPI_IDENTITY
+    assert U._gpu.epilogue_code(relu_inplace)[0] == native.EPI_RELU
