@@ -678,7 +678,8 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
   } else if constexpr (BPK) {
     // Element (k, n) at col(n) + row(k); a lane's 8 columns stay in one panel
     // or block, the lane offset holds col(n) and the row within the K pair.
-    const int r = lane >> 5, c = lane & 31;
+    // Rows 8 w .. 8 w + 7: bit 3 of the row is the wave's parity.
+    const int r = lane >> 5, c = (lane & 31) ^ (((wave * (64 / NW)) >> 2) & 2);
     auto col = [&](int64_t n) -> int64_t {
       if constexpr (LB == L_PANELS) return (n / P) * g.b.kpad * P + n % P;
       else return (n >> 5) * (g.b.kpad >> 5) * 1024 + (n & 31);
@@ -689,19 +690,25 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
     soff_b = blk_b = 0;
   } else if constexpr (BT && BN == 128) {
     // 256-byte rows: a 1 KiB load is 4 K rows, lane l filling slot l % 16 of
-    // row l / 16; row k % 4 == l / 16 for every load, so one lane offset.
+    // row l / 16; row k % 4 == l / 16 for every load. Bit 3 of the row flips
+    // chunk bit 1 (bswz): voff_b0 for rows with it clear, voff_b1 set.
     const int r = lane >> 4, c = lane & 15;
+    const int h = ((wave * (64 / NW)) >> 2) & 2;  // bit 3 of the wave's first row, as chunk bit 1
     if constexpr (RAGGED) {
       const int64_t last = ((g.n - 1) >> 3) << 3;  // the last 8-column chunk
-      voff_b0 = voff_b1 = (int32_t)((r * g.b.ld + min(n0 + (c ^ swz_n(r)) * 8, last)) * 2);
+      voff_b0 = (int32_t)((r * g.b.ld + min(n0 + (c ^ swz_n(r) ^ h) * 8, last)) * 2);
+      voff_b1 = (int32_t)((r * g.b.ld + min(n0 + (c ^ swz_n(r) ^ h ^ 2) * 8, last)) * 2);
       soff_b = (int32_t)(wave * (64 / NW) * g.b.ld * 2);
     } else {
-      voff_b0 = voff_b1 = (int32_t)((r * g.b.ld + (c ^ swz_n(r)) * 8) * 2);
+      voff_b0 = (int32_t)((r * g.b.ld + (c ^ swz_n(r) ^ h) * 8) * 2);
+      voff_b1 = (int32_t)((r * g.b.ld + (c ^ swz_n(r) ^ h ^ 2) * 8) * 2);
       soff_b = (int32_t)((wave * (64 / NW) * g.b.ld + n0) * 2);
     }
     blk_b = (int32_t)(4 * g.b.ld * 2);
   } else if constexpr (BT) {
-    const int r = lane >> 5, c = lane & 31;
+    // Rows 8 w .. 8 w + 7 (eight waves): bit 3 of the row is the wave's
+    // parity, folded into the chunk (bswz).
+    const int r = lane >> 5, c = (lane & 31) ^ (((wave * (64 / NW)) >> 2) & 2);
     if constexpr (RAGGED) {
       const int64_t last = ((g.n - 1) >> 3) << 3;  // the last 8-column chunk
       voff_b0 = (int32_t)((r * g.b.ld + min(n0 + (c ^ swz_n(r)) * 8, last)) * 2);
@@ -744,7 +751,10 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
     } else {
       const int qb = q - LA;
       const int32_t kb = BT ? (int32_t)(k0 * g.b.ld * 2) : (int32_t)(k0 * 2);
-      lds_dma16(srd_b, (qb & 1) ? voff_b1 : voff_b0, soff_b + qb * blk_b + kb, sb + qb * 1024);
+      // 256-byte B rows: load qb covers rows 4 qb .. 4 qb + 3 of the wave's,
+      // bit 3 of which is that of qb >> 1.
+      const bool hi = BT && BN == 128 ? (qb >> 1) & 1 : qb & 1;
+      lds_dma16(srd_b, hi ? voff_b1 : voff_b0, soff_b + qb * blk_b + kb, sb + qb * 1024);
     }
   };
 
@@ -763,7 +773,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
 #pragma unroll
     for (int j = 0; j < FN; ++j)
       b_tr[j] = A_BYTES + (8 * fg + (sl >> 2)) * NROWB +
-                ((wn * (WN / 8) + 2 * j + ((sl & 3) >> 1)) ^ swz_n(sl >> 2)) * 16 + 8 * (sl & 1);
+                ((wn * (WN / 8) + 2 * j + ((sl & 3) >> 1)) ^ bswz(8 * fg + (sl >> 2))) * 16 + 8 * (sl & 1);
   }
   auto a_read = [&](int stage, int ks, int i) -> bf16x8_t {
     return *(const bf16x8_t*)(a_frag + stage * STAGE + i * 16 * ROWB + ((4 * ks + fg) ^ fswz) * 16);
@@ -831,26 +841,41 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
         else fb[0][f - FM] = b_read(nxt, 0, f - FM);
       }
       const int i = sub / FN, j = sub % FN;
-      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+      // B's fragment first: the product is C^T's fragment, so each lane ends
+      // with four adjacent columns of one row of C.
+      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
   wait_vmem<0>();  // no load into LDS outlives the loop
 
-  // Epilogue: lane l finishes column l % 16 of each fragment, rows
-  // 4 g .. 4 g + 3 (bias, scale, shift, activation, one rounding).
+  // Epilogue. Lane l holds row l % 16 of each fragment, columns
+  // 4 (l / 16) .. + 3 (the operands went in B first): bias, scale, shift,
+  // activation, one rounding. Without bias, scale and shift (the common
+  // case) the affine step is skipped; it would only turn -0 into +0.
   const int64_t off = split * g.stride_split + batch * g.stride_c;
-  const bool odd = lane & 1;
+  const bool affine = g.bias || g.scale || g.shift;
+  // The lane's four columns of fragment column j (tile coordinates).
+  auto col4_of = [&](int j) { return wn * WN + j * 16 + 4 * fg; };
+  // Bias, scale and shift of the lane's four columns of fragment column j
+  // (columns past N: identity values, for ragged tiles).
+  auto vectors4 = [&](int j, float (&cb)[4], float (&cs)[4], float (&ch)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t col = n0 + col4_of(j) + e;
+      column_vectors(g, col, !RAGGED || col < g.n, cb[e], cs[e], ch[e]);
+    }
+  };
   if constexpr (staged_act(ACT)) {
     // Any other named activation, or an epilogue program: each wave stages
     // its own 128 x 64 outputs as f32 in its own LDS region, 64 rows at a
-    // time (rows padded by 16 bytes, so one fragment write -- 16 columns of
-    // four rows 4 apart -- meets distinct banks), and finishes them in runs of
-    // 8 columns -- bias, scale, shift, the activation or program, one
-    // rounding -- in a loop that is not unrolled, so the interpreter is
-    // emitted once per half, storing each run with a 16-byte write. Half by
-    // half, the accumulators it has stored are no longer live, which leaves
-    // the interpreter its registers.
+    // time (rows padded by 16 bytes; a lane writes its four columns of a
+    // fragment row as one 16-byte store, and the 16 rows of one write meet
+    // distinct banks), and finishes them in runs of 8 columns -- bias,
+    // scale, shift, the activation or program, one rounding -- in a loop that
+    // is not unrolled, so the interpreter is emitted once per half, storing
+    // each run with a 16-byte write. Half by half, the accumulators it has
+    // stored are no longer live, which leaves the interpreter its registers.
     constexpr int PW = WN * 4 + 16;  // f32 row pitch of a wave's region
     static_assert(NW * (WM / 2) * PW <= LDS_BYTES, "the waves' regions fit");
     uint8_t* region = lds + wave * (WM / 2) * PW;
@@ -873,10 +898,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
         for (int i = Q * (FM / 2); i < (Q + 1) * (FM / 2); ++i)
 #pragma unroll
           for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              *(float*)(region + ((i - Q * (FM / 2)) * 16 + 4 * fg + e) * PW + (j * 16 + (lane & 15)) * 4) =
-                  acc[i][j][e];
+            *(f32x4_t*)(region + ((i - Q * (FM / 2)) * 16 + frow) * PW + (j * 16 + 4 * fg) * 4) = acc[i][j];
       });
 #pragma unroll 1
       for (int it = 0; it < (WM / 2) * RUNS / 64; ++it) {
@@ -899,33 +921,33 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
     }
   } else if constexpr (BF16) {
     // bf16 C goes through LDS (free once every wave is done with the last
-    // stage) as the whole 256 x 256 tile, 512-byte rows whose 16-byte chunk c
-    // sits in slot c ^ cswz(row), then leaves in whole rows: written straight
-    // from the fragments, each store would cover 32-byte pieces of 8 rows,
-    // and the tile's writes would cost ~25 us per launch more. Lanes 2c and
-    // 2c + 1 exchange rows so that each writes one 4-byte word (two columns);
-    // the 8 rows x 32 bytes of one LDS write meet 16 distinct chunk slots.
-    auto cswz = [](int r) { return 2 * ((r & 1) | (((r >> 2) & 3) << 1)); };
+    // stage) as the whole tile, rows of NROWB bytes whose 16-byte chunk c sits
+    // in slot c ^ (row % 16), then leaves in whole rows: written straight
+    // from the fragments, each store would cover 32-byte pieces of 16 rows.
+    // A lane writes its four columns of a fragment row as one 8-byte word;
+    // the 16 rows x 32 bytes of one LDS write meet distinct banks.
     __syncthreads();
+    auto stage_rows = [&](auto&& finish) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int cl = wn * WN + j * 16 + (lane & 15);  // tile column
-      float bias, scale, shift;
-      column_vectors(g, n0 + cl, !RAGGED || n0 + cl < g.n, bias, scale, shift);
-      const int pc = cl & ~1;
+      for (int j = 0; j < FN; ++j) {
+        const int col4 = col4_of(j);
+        float cb[4] = {0.f, 0.f, 0.f, 0.f}, cs[4] = {1.f, 1.f, 1.f, 1.f}, ch[4] = {0.f, 0.f, 0.f, 0.f};
+        if (affine) vectors4(j, cb, cs, ch);
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
+        for (int i = 0; i < FM; ++i) {
+          const int r = wm * WM + i * 16 + frow;
+          float v[4];
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const float v0 = activate<ACT>((acc[i][j][2 * q] + bias) * scale + shift);
-          const float v1 = activate<ACT>((acc[i][j][2 * q + 1] + bias) * scale + shift);
-          const float recv = swap_pair(odd ? v0 : v1);
-          const int r = wm * WM + i * 16 + 4 * fg + 2 * q + (odd ? 1 : 0);
-          const uint32_t word = odd ? pack_bf16x2(recv, v1) : pack_bf16x2(v0, recv);
-          *(uint32_t*)(lds + r * NROWB + (((pc >> 3) ^ cswz(r)) << 4) + (pc & 7) * 2) = word;
+          for (int e = 0; e < 4; ++e) v[e] = finish(acc[i][j][e], cb[e], cs[e], ch[e]);
+          *(uint2*)(lds + r * NROWB + (((col4 >> 3) ^ frow) << 4) + (col4 & 4) * 2) =
+              make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
         }
       }
-    }
+    };
+    if (affine)
+      stage_rows([](float a, float b, float s, float h) { return activate<ACT>((a + b) * s + h); });
+    else
+      stage_rows([](float a, float, float, float) { return activate<ACT>(a); });
     __syncthreads();
     // Wave w stores tile rows RW w .. RW w + RW - 1, RPI whole rows per
     // instruction (16 bytes per lane: two 512-byte or four 256-byte rows).
@@ -934,7 +956,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
 #pragma unroll
     for (int p = 0; p < RW / RPI; ++p) {
       const int r = wave * RW + RPI * p + lane / CPR, ch = lane % CPR;
-      const uint4 v = *(const uint4*)(lds + r * NROWB + ((ch ^ cswz(r)) << 4));
+      const uint4 v = *(const uint4*)(lds + r * NROWB + ((ch ^ (r & 15)) << 4));
       if constexpr (RAGGED) {
         // Rows past M are not stored; the chunk across N is stored element
         // by element.
@@ -953,20 +975,31 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
       }
     }
   } else {
+    // f32 C straight from the fragments: a lane's four columns of a row are
+    // one 16-byte store where C's rows allow it (16-byte aligned, whole), else
+    // four 4-byte stores.
     float* c = (float*)g.c + off;
+    const bool vec = ((((uintptr_t)g.c) & 15) == 0) && g.ldc % 4 == 0 && g.stride_c % 4 == 0 &&
+                     g.stride_split % 4 == 0;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const int64_t col = n0 + wn * WN + j * 16 + (lane & 15);
-      float bias, scale, shift;
-      column_vectors(g, col, !RAGGED || col < g.n, bias, scale, shift);
+      const int64_t col = n0 + col4_of(j);
+      float cb[4], cs[4], ch[4];
+      vectors4(j, cb, cs, ch);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
-        const int64_t row0 = m0 + wm * WM + i * 16 + 4 * fg;
+        const int64_t row = m0 + wm * WM + i * 16 + frow;
+        float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (!RAGGED || (row0 + e < g.m && col < g.n))
-            store_c32(c + (row0 + e) * g.ldc + col,
-                      __float_as_uint(activate<ACT>((acc[i][j][e] + bias) * scale + shift)));
+        for (int e = 0; e < 4; ++e) v[e] = activate<ACT>((acc[i][j][e] + cb[e]) * cs[e] + ch[e]);
+        float* cp = c + row * g.ldc + col;
+        if ((!RAGGED || (row < g.m && col + 4 <= g.n)) && vec) {
+          store16_stream(cp, Elem<float>::pack(v));
+        } else if (!RAGGED || row < g.m) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (!RAGGED || col + e < g.n) store_c32(cp + e, __float_as_uint(v[e]));
+        }
       }
     }
   }

@@ -50,6 +50,11 @@ __device__ __forceinline__ void wait_vmem() {
 __device__ __forceinline__ int swz_k(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
 __device__ __forceinline__ int swz_n(int r) { return ((r & 3) << 1) ^ ((r & 3) << 2); }
 __device__ __forceinline__ int swz64(int r) { return (r >> 1) & 7; }
+// Row-major B tiles of the 16x16x32 kernel: swz_n, with bit 3 of the K row
+// also flipping chunk bit 1. One transposing fragment read covers rows
+// r .. r + 3 and r + 8 .. r + 11 in its two 16-lane halves; with swz_n alone
+// both halves met the same banks (a two-way conflict on every read).
+__device__ __forceinline__ int bswz(int r) { return swz_n(r) ^ ((r >> 2) & 2); }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
