@@ -238,7 +238,13 @@ def device_units(device: torch.device | None) -> int:
     """Compute units of ``device`` (checked as ``ensure_device`` does); 0 --
     the library's default, MI355X's 256 -- for ``None`` or a non-ROCm device,
     where plans are made without a GPU."""
-    if device is None or device.type != "cuda" or not torch.cuda.is_available():
+    if device is None or device.type != "cuda":
+        return 0
+    if device.index is not None:
+        units = _device_units.get(device.index)
+        if units is not None:
+            return units
+    if not torch.cuda.is_available():
         return 0
     ensure_device(device)
     index = device.index if device.index is not None else torch.cuda.current_device()

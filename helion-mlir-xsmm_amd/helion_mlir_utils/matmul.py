@@ -246,19 +246,29 @@ class GemmLaunch(GpuLaunch):
         self._dtype = c_dtype
         self.splits = s
 
+    def unbind_vectors(self) -> None:
+        """Drop the references to the bound bias, scale and shift: every later
+        call passes its own (``run(..., vectors=...)``)."""
+        self._vectors = (None, None, None, self._vectors[3])
+
     def __call__(self, a: Tensor, b: Tensor) -> Tensor:
         """C = the bound GEMM of ``a`` and ``b`` in a fresh output (the
         :class:`~helion_mlir_backend.PreparedCall` protocol)."""
         return self.run(a, b)
 
-    def run(self, a: Tensor, b: Tensor, c: Tensor | None = None) -> Tensor:
-        """C = the bound GEMM of ``a`` and ``b`` (buffers as planned)."""
+    def run(self, a: Tensor, b: Tensor, c: Tensor | None = None,
+            vectors: tuple[Tensor | None, Tensor | None, Tensor | None] | None = None) -> Tensor:
+        """C = the bound GEMM of ``a`` and ``b`` (buffers as planned);
+        ``vectors`` replaces the bound bias, scale and shift by tensors of the
+        same presence and dtype."""
         if c is None:
             c = output_pool.empty(self._shape, dtype=self._dtype, device=self._device)
         args = list(self._args)
         args[2] = a.data_ptr()
         args[5] = b.data_ptr()
         args[10] = c.data_ptr()
+        if vectors is not None:
+            args[19], args[20], args[21] = (None if v is None else v.data_ptr() for v in vectors)
         ws = None
         ws_bytes = self._ws_bytes
         if self._staged_ws is not None and (not self._rows_ok or a.data_ptr() % 16 or b.data_ptr() % 16):
@@ -282,6 +292,15 @@ class GemmLaunch(GpuLaunch):
         return c
 
 
+# Bound GEMM launches of eager calls, by everything a launch binds except the
+# data pointers: a repeated problem is a pointer patch and one native call
+# (the reference likewise keeps bound kernels in an LRU, matmul.py:470-523).
+# Bounded, cleared when full. A launch holds its epilogue program, so the
+# program's id in the key cannot be reused while the entry lives.
+_LAUNCHES: dict[tuple, GemmLaunch] = {}
+_LAUNCHES_MAX = 256
+
+
 def _launch_gemm(
     a: Tensor, lda: int, trans_a: bool,
     b: Tensor, ldb: int, layout: int, panel: int, kpad: int,
@@ -291,12 +310,21 @@ def _launch_gemm(
     vec_dtype: int = native.DTYPE_F32, epilogue: Epilogue = IDENTITY,
     splits: int = 0, tiles: Sequence[int] | None = None,
 ) -> Tensor:
-    launch = GemmLaunch(
-        native.dtype_code(a.dtype), c.dtype, a.device, tuple(c.shape), lda, trans_a, ldb, layout,
-        panel, kpad, m, n, k, batch, stride_a, stride_b, stride_c, bias, scale, shift, vec_dtype,
-        epilogue, splits, tiles,
-    )
-    return launch.run(a, b, c)
+    key = (a.dtype, c.dtype, a.device, tuple(c.shape), lda, trans_a, ldb, layout, panel, kpad, m, n, k, batch,
+           stride_a, stride_b, stride_c, bias is None, scale is None, shift is None, vec_dtype, epilogue[0],
+           epilogue[1], id(epilogue[2]), splits, None if tiles is None else tuple(tiles))
+    launch = _LAUNCHES.get(key)
+    if launch is None:
+        launch = GemmLaunch(
+            native.dtype_code(a.dtype), c.dtype, a.device, tuple(c.shape), lda, trans_a, ldb, layout,
+            panel, kpad, m, n, k, batch, stride_a, stride_b, stride_c, bias, scale, shift, vec_dtype,
+            epilogue, splits, tiles,
+        )
+        launch.unbind_vectors()
+        if len(_LAUNCHES) >= _LAUNCHES_MAX:
+            _LAUNCHES.clear()
+        _LAUNCHES[key] = launch
+    return launch.run(a, b, c, (bias, scale, shift))
 
 
 def matmul(
