@@ -3,10 +3,25 @@
 // epilogue activations.
 #pragma once
 
+#ifdef __HIPCC_RTC__
+// Run-time compilation (hipRTC, hmx_jit.cpp): no host headers; the
+// fixed-width integer types live in __hip_internal.
+using __hip_internal::int16_t;
+using __hip_internal::int32_t;
+using __hip_internal::int64_t;
+using __hip_internal::int8_t;
+using __hip_internal::uint16_t;
+using __hip_internal::uint32_t;
+using __hip_internal::uint64_t;
+using __hip_internal::uint8_t;
+typedef __hip_internal::uint64_t uintptr_t;
+#include "hmx.h"
+#else
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "hmx_internal.hpp"
+#endif
 
 namespace hmx {
 
@@ -183,18 +198,19 @@ __device__ __forceinline__ float min_nan(float a, float b) {
 
 // The operations of an epilogue program (hmx_program): X(opcode, f32 result of
 // a, b and the constants c0, c1). The formulas are the ones torch evaluates
-// for the same operation on f32 tensors.
+// for the same operation on f32 tensors, except the activations that also
+// have a named code (sigmoid, tanh, SiLU, GELU and its tanh form), which take
+// that code's form (apply_activation): a program's SiLU is the named SiLU.
 #define HMX_PROGRAM_OPS(X)                                                       \
   X(HMX_OP_COPY, a)                                                              \
   X(HMX_OP_NEG, -a)                                                              \
   X(HMX_OP_ABS, fabsf(a))                                                        \
   X(HMX_OP_RELU, a > 0.f ? a : (a != a ? a : 0.f))                               \
-  X(HMX_OP_SIGMOID, 1.f / (1.f + expf(-a)))                                      \
-  X(HMX_OP_TANH, tanhf(a))                                                       \
-  X(HMX_OP_SILU, a / (1.f + expf(-a)))                                           \
-  X(HMX_OP_GELU, a * 0.5f * (1.f + erff(a * 0.7071067811865476f)))               \
-  X(HMX_OP_GELU_TANH,                                                            \
-    0.5f * a * (1.f + tanhf(0.7978845608028654f * (a + 0.044715f * a * a * a)))) \
+  X(HMX_OP_SIGMOID, apply_activation(HMX_EPI_SIGMOID, a, 0.f))                   \
+  X(HMX_OP_TANH, apply_activation(HMX_EPI_TANH, a, 0.f))                         \
+  X(HMX_OP_SILU, apply_activation(HMX_EPI_SILU, a, 0.f))                         \
+  X(HMX_OP_GELU, apply_activation(HMX_EPI_GELU, a, 0.f))                         \
+  X(HMX_OP_GELU_TANH, apply_activation(HMX_EPI_GELU_TANH, a, 0.f))               \
   X(HMX_OP_EXP, expf(a))                                                         \
   X(HMX_OP_LOG, logf(a))                                                         \
   X(HMX_OP_SQRT, sqrtf(a))                                                       \

@@ -179,16 +179,23 @@ constexpr int epi_pitch() { return WN + 8; }
 // Activation classes compiled into the register epilogue. ACT_ANY: any
 // other named activation, ACT_PROG: an epilogue program, both finished by the
 // LDS-staged epilogue (separate instantiations: only ACT_PROG carries the
-// interpreter's registers).
-enum : int { ACT_ID = 0, ACT_RELU = 1, ACT_SILU = 2, ACT_ANY = 3, ACT_PROG = 4 };
+// interpreter's registers). ACT_JIT: the epilogue compiled in at run time
+// (hmx_jit.cpp) as hmx_jit_epilogue, finished in registers like ReLU.
+enum : int { ACT_ID = 0, ACT_RELU = 1, ACT_SILU = 2, ACT_ANY = 3, ACT_PROG = 4, ACT_JIT = 5 };
 
 // The staged class for an epilogue code that is not identity, ReLU or SiLU.
 constexpr bool staged_act(int act) { return act == ACT_ANY || act == ACT_PROG; }
+
+// The run-time compiled epilogue of ACT_JIT kernels: f(value, extra). Only
+// the sources that hmx_jit.cpp compiles define it; the library's own
+// kernels never instantiate ACT_JIT.
+__device__ float hmx_jit_epilogue(float x, float extra);
 
 template <int ACT>
 __device__ __forceinline__ float activate(float v) {
   if constexpr (ACT == ACT_RELU) return apply_activation(HMX_EPI_RELU, v, 0.f);
   if constexpr (ACT == ACT_SILU) return apply_activation(HMX_EPI_SILU, v, 0.f);
+  if constexpr (ACT == ACT_JIT) return hmx_jit_epilogue(v, 0.f);
   return v;
 }
 
@@ -361,6 +368,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, float* lds, int spli
 #undef HMX_DIRECT
 }
 
+#ifndef __HIPCC_RTC__
 // Kernel launchers, one translation unit each. `la` / `lb` are L_* layouts
 // of A and B; `guard` selects the kernels that check every edge.
 // hmx_gemm_bf16_*.hip: register-staged bf16 kernel, tiles 256 x 256 or 128 x 128
@@ -399,5 +407,13 @@ void launch_gemm_f32(const GemmArgs& g, int tile_bm, int la, int lb, bool guard,
                      hipStream_t s);
 void launch_splitk_reduce(const float* partials, int splits, int64_t batch, const GemmArgs& r,
                           bool vec4, hipStream_t s);
+// hmx_jit.cpp: the 16x16x32 kernel (layout lb, bf16 or f32 C, ragged or
+// whole tiles of bm x bn, nw waves, `stages` K stages) with g's epilogue --
+// a program or a named activation -- compiled into its register epilogue at
+// run time. HMX_OK, or HMX_ERR_UNSUPPORTED when run-time compilation is off
+// (HMX_JIT=0) or failed: the caller then launches the interpreter.
+int launch_mi16_jit(const GemmArgs& g, int lb, bool bf16, bool ragged, int bm, int bn, int nw, int stages,
+                    dim3 grid, hipStream_t s);
+#endif  // __HIPCC_RTC__
 
 }  // namespace hmx

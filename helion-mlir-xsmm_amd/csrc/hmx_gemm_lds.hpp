@@ -33,6 +33,11 @@ __device__ __forceinline__ i32x4_t make_srd(const void* p, int32_t bytes) {
 #pragma clang diagnostic ignored "-Winline-asm"
 template <bool NT = false>
 __device__ __forceinline__ void lds_dma16(i32x4_t srd, int32_t voff, int32_t soff, uint32_t lds) {
+  // The scalar offset and the LDS address are uniform by construction; saying
+  // so keeps them in SGPRs where the compiler cannot prove it (run-time
+  // compilation of the VNNI-panel loads), and costs nothing where it can.
+  soff = __builtin_amdgcn_readfirstlane(soff);
+  lds = __builtin_amdgcn_readfirstlane(lds);
   if constexpr (NT)
     asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen nt lds"
                  :: "v"(voff), "s"(srd), "s"(soff), "s"(lds) : "memory", "m0");

@@ -36,6 +36,7 @@ def explain() -> dict[str, object]:
         "library": str(_native.library_path()),
         "library_built": _native.available(),
         "native_calls": _native.native_calls(),
+        "jit": _native.jit_info() if _native.available() else None,
         "output_pool": output_pool.output_pool_stats(),
     }
 

@@ -25,7 +25,7 @@ import torch
 from ..support.errors import UnsupportedTargetError
 
 LIBRARY_ENV = "HMX_LIBRARY"
-ABI_VERSION = 4  # HMX_ABI_VERSION of include/hmx.h
+ABI_VERSION = 5  # HMX_ABI_VERSION of include/hmx.h
 NATIVE_CALL_ENV = "HELION_MLIR_NATIVE_CALL"
 _DEFAULT = Path(__file__).resolve().parents[3] / "csrc" / "libhmx.so"
 
@@ -93,6 +93,8 @@ SIGNATURES: dict[str, list[object]] = {
     "hmx_abi_version": [],
     "hmx_device_check": [_IP],
     "hmx_time_launches": [_P, _P],
+    "hmx_jit_info": [_LP, _LP, _LP],
+    "hmx_jit_last_log": [],
     "hmx_gemm": [
         _I, _I,  # ab_dtype, c_dtype
         _P, _L, _I,  # a, lda, trans_a
@@ -134,7 +136,7 @@ SIGNATURES: dict[str, list[object]] = {
     "hmx_elementwise": [_I, _I, _P, _P, _L, _F, _P],
     "hmx_pack": [_I, _I, _P, _L, _L, _L, _P, _L, _L, _L, _P],
 }
-_RESTYPES = {"hmx_last_error": ctypes.c_char_p}
+_RESTYPES = {"hmx_last_error": ctypes.c_char_p, "hmx_jit_last_log": ctypes.c_char_p}
 
 _lock = threading.Lock()
 _lib: list[ctypes.CDLL] = []
@@ -211,6 +213,17 @@ def time_launches(start: "torch.cuda.Event | None", stop: "torch.cuda.Event | No
     if any(h == 0 for h in handles):
         raise ValueError("time_launches: record each event once before arming it")
     check(lib().hmx_time_launches(*handles), "hmx_time_launches")
+
+
+def jit_info() -> dict[str, object]:
+    """Run-time compiled GEMM epilogues so far (``hmx_jit_info``): kernels
+    compiled, compilations that failed (their GEMMs ran the interpreter),
+    launches of compiled kernels, and the last failure's compiler log."""
+    vals = [ctypes.c_int64() for _ in range(3)]
+    check(lib().hmx_jit_info(*[ctypes.byref(v) for v in vals]), "hmx_jit_info")
+    log = lib().hmx_jit_last_log() or b""
+    return {"compiled": vals[0].value, "failed": vals[1].value, "launches": vals[2].value,
+            "last_failure_log": log.decode(errors="replace")}
 
 
 def count_call() -> None:

@@ -27,13 +27,15 @@
 #ifndef HMX_H
 #define HMX_H
 
+#ifndef __HIPCC_RTC__
 #include <stdint.h>
+#endif
 
 #ifdef __cplusplus
 extern "C" {
 #endif
 
-#define HMX_ABI_VERSION 4
+#define HMX_ABI_VERSION 5
 
 /* Status codes. */
 #define HMX_OK 0
@@ -191,6 +193,18 @@ int hmx_device_check(int* compute_units);
  * and belong to the device the calls run on. Per-thread state, like the
  * error message. */
 int hmx_time_launches(void* start_event, void* stop_event);
+
+/* Run-time compiled epilogues, as the reference reports its JIT's work
+ * (helion_mlir_backend.explain(), _compiler/call_trace.py:220): GEMM kernels
+ * compiled with an epilogue program or a named activation in their register
+ * epilogue (hipRTC, on first use of each kernel variant and epilogue), the
+ * compilations that failed (their GEMMs ran the interpreter), and the launches
+ * of compiled kernels. Any pointer may be NULL. HMX_JIT=0 in the environment
+ * turns run-time compilation off (read on every call). */
+int hmx_jit_info(int64_t* compiled, int64_t* failed, int64_t* launches);
+
+/* The compiler log of the last failed run-time compilation ("" if none). */
+const char* hmx_jit_last_log(void);
 
 /*
  * GEMM with fused epilogue:

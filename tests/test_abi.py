@@ -60,7 +60,7 @@ def test_binding_covers_the_header() -> None:
 
 
 def test_abi_version(lib: ctypes.CDLL) -> None:
-    assert lib.hmx_abi_version() == native.ABI_VERSION == 4
+    assert lib.hmx_abi_version() == native.ABI_VERSION == 5
 
 
 @pytest.mark.parametrize(

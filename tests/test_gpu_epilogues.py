@@ -252,3 +252,112 @@ def test_fast_activations_accuracy(gpu_device, name: str) -> None:
     else:
         # (Values below 1e-30, where f32 has underflowed as torch's does, are exempt.)
         assert (err <= 2e-6 * np.abs(exact) + 1e-30).all(), float((err / np.maximum(np.abs(exact), 1e-30)).max())
+
+
+# Run-time compiled epilogues (hmx_jit.cpp): the 16x16x32 kernel with the
+# program or named activation compiled into its register epilogue. Each
+# shape reaches one of its variants: whole 256 x 256 tiles, ragged ones, the
+# 256 x 128 round after whole rounds of 256 x 256, 128 x 128 tiles (K of 16+
+# stages), and f32 C.
+JIT_SHAPES = {
+    "whole": (4096, 4096, 256, False, "bf16"),
+    "ragged": (4000, 4104, 256, True, "bf16"),
+    "round_tail": (4096, 4352, 256, True, "bf16"),
+    "tiles_128": (512, 512, 1024, False, "bf16"),
+    "f32_out": (4096, 4096, 256, True, "f32"),
+}
+
+
+def _jit_launches() -> int:
+    return native.jit_info()["launches"]
+
+
+@pytest.mark.parametrize("shape", list(JIT_SHAPES))
+@pytest.mark.parametrize("epi", ["silu_mix", "hardswish", "gelu_named", "module"])
+def test_jit_epilogues_run_compiled(gpu_device, monkeypatch, shape: str, epi: str) -> None:
+    m, n, k, tb, out = JIT_SHAPES[shape]
+    fn = EPILOGUES[epi]
+    a, b = _operands(m, n, k, False, tb, "bf16", gpu_device)
+    bias = tensor(RNG.normal(0, 1, n).astype(np.float32), "bf16", gpu_device)
+    out_dtype = torch.float32 if out == "f32" else None
+    start = native.jit_info()
+    got = U.matmul(a, b, trans_b=tb, bias=bias, epilogue=fn, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    info = native.jit_info()
+    assert info["failed"] == start["failed"], info["last_failure_log"]
+    assert info["launches"] > start["launches"], "the compiled kernel did not run"
+    ref = R.matmul(to_np(a), to_np(b), False, tb, to_np(bias), act=fn, out=out)
+    if out == "f32":
+        assert_close(to_np(got), ref, 1e-4, 2 * 3 * bf16_gemm_atol(k, to_np(a), to_np(b)))
+    else:
+        _check(to_np(got), ref, k, to_np(a), to_np(b), out)
+    # With run-time compilation off the interpreter runs it; on whole tiles
+    # it is the same 16x16x32 kernel, so the two agree bit for bit (the
+    # compiled code evaluates each instruction with the interpreter's
+    # formula).
+    monkeypatch.setenv("HMX_JIT", "0")
+    before = _jit_launches()
+    again = U.matmul(a, b, trans_b=tb, bias=bias, epilogue=fn, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    assert _jit_launches() == before
+    if shape in ("whole", "f32_out"):
+        assert torch.equal(got, again)
+    else:
+        if out == "f32":
+            assert_close(to_np(again), ref, 1e-4, 2 * 3 * bf16_gemm_atol(k, to_np(a), to_np(b)))
+        else:
+            _check(to_np(again), ref, k, to_np(a), to_np(b), out)
+
+
+@pytest.mark.parametrize("act", [F.gelu, torch.tanh, torch.sigmoid, lambda x: F.leaky_relu(x, 0.2),
+                                 lambda x: F.gelu(x, approximate="tanh")])
+def test_jit_named_activations_match_the_staged_epilogue(gpu_device, monkeypatch, act) -> None:
+    # Named activations the precompiled register epilogue does not carry run
+    # compiled in; the staged epilogue they replace computes the same formula.
+    m, n, k = 4096, 4096, 256
+    a, b = _operands(m, n, k, False, True, "bf16", gpu_device)
+    scale = torch.from_numpy(RNG.uniform(0.5, 1.5, n).astype(np.float32)).to(gpu_device)
+    got = U.matmul(a, b, trans_b=True, epilogue=act, scale=scale)
+    monkeypatch.setenv("HMX_JIT", "0")
+    staged = U.matmul(a, b, trans_b=True, epilogue=act, scale=scale)
+    torch.cuda.synchronize()
+    assert torch.equal(got, staged)
+    ref = R.matmul(to_np(a), to_np(b), False, True, None, to_np(scale), act=act, out="bf16")
+    _check(to_np(got), ref, k, to_np(a), to_np(b), "bf16")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("groups,c", [(32, 4096), (1, 4096), (1, 8192), (32, 2048)])
+def test_jit_group_norm_programs(gpu_device, monkeypatch, dtype: str, groups: int, c: int) -> None:
+    # Whole-row GroupNorm with the program compiled in: every row shape the
+    # whole-row kernel takes (8192 f32 channels need 16 waves, which the
+    # interpreter's kernels cannot hold: they take the streaming kernel).
+    m = 600
+    x = tensor(RNG.normal(0, 2, (m, c)).astype(np.float32), dtype, gpu_device)
+    w = torch.from_numpy(RNG.uniform(0.5, 1.5, c).astype(np.float32)).to(gpu_device)
+    b = torch.from_numpy(RNG.normal(0, 0.5, c).astype(np.float32)).to(gpu_device)
+    extra = torch.from_numpy(RNG.normal(0, 1, c).astype(np.float32)).to(gpu_device)
+    fn = lambda y, e: F.silu(y * e + 1) - e  # noqa: E731
+    start = native.jit_info()
+    got = U.group_norm(x, groups, w, b, 1e-5, epilogue=fn, extra=extra)
+    torch.cuda.synchronize()
+    info = native.jit_info()
+    assert info["failed"] == start["failed"], info["last_failure_log"]
+    assert info["launches"] > start["launches"], "the compiled kernel did not run"
+    ref = R.group_norm(to_np(x), groups, to_np(w), to_np(b), 1e-5, to_np(extra), "callable", fn, out=dtype)
+    assert_close(to_np(got), ref, 1e-2 if dtype == "bf16" else 1e-4, 5e-3 if dtype == "bf16" else 1e-4)
+    monkeypatch.setenv("HMX_JIT", "0")
+    again = U.group_norm(x, groups, w, b, 1e-5, epilogue=fn, extra=extra)
+    torch.cuda.synchronize()
+    if dtype == "bf16" or c <= 4096:
+        # The same whole-row kernel with the interpreter: the same bits.
+        assert torch.equal(got, again)
+    else:
+        assert_close(to_np(again), ref, 1e-4, 1e-4)
+
+
+def test_no_run_time_compilation_failed(gpu_device) -> None:
+    # Every kernel the tests above compiled at run time compiled: a failure
+    # would have sent its GEMM to the interpreter without an error.
+    info = native.jit_info()
+    assert info["failed"] == 0, info["last_failure_log"]
