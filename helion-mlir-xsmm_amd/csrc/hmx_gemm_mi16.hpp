@@ -120,24 +120,29 @@ __device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g) {
   int32_t voff_b0, voff_b1, soff_b, blk_b;
   int32_t vn_off[VN ? LBN : 1];
   const int64_t P = g.b.panel;
-  const int PL = (int)min<int64_t>(P, 256);
   if constexpr (VN) {
-    // 1 KiB pieces of the stage's 32 K pairs x 256 columns, in the order of
-    // gemm_bf16_dma64_kernel (runs of 128 P bytes for P <= 256, else 1 KiB
-    // pair rows 4 P bytes apart), copied to LDS unchanged.
-    voff_b0 = voff_b1 = lane * 16;
+    // The stage lands re-laid in 16-byte pieces (4 columns of one K pair) so
+    // that one fragment read of the 16 x 16 x 32 MFMA is 256 consecutive
+    // bytes: slabs of 4 KiB, one per K pair kp = 16 ks + 4 f + i (i, ks
+    // outer), each holding the tile's 16 groups of 16 columns as 256-byte
+    // lines [f 4][16 columns][K pair]. 1 KiB load b (of the stage's 32) fills
+    // slab (ks, i) = (b / 16, b / 4 % 4), groups 4 (b % 4) .. + 3; lane l
+    // takes group 4 (b % 4) + l / 16, f = l / 4 % 4, columns 4 (l % 4) .. + 3,
+    // i.e. K-pair row 16 ks + 4 f + i of tile columns 64 (b % 4) + lam,
+    // lam = 16 (l / 16) + 4 (l % 4). Every load still reads 8 whole 128-byte
+    // rows. A lane's part of the offset is its K-pair row f and column lam
+    // (a 32-column panel boundary falls inside lam for P = 32); the load's
+    // part is the slab and the 64-column group. P is a multiple of 32 that
+    // divides 256, or a multiple of 256, so (n0 + 64 (b % 4)) % P + lam stays in
+    // one panel for P > 32.
+    const int f = (lane >> 2) & 3, lam = 16 * (lane >> 4) + 4 * (lane & 3);
+    voff_b0 = voff_b1 = (int32_t)(f * 16 * P + (lam / P) * (g.b.kpad / 2) * 4 * P + (lam % P) * 4);
     soff_b = blk_b = 0;
 #pragma unroll
     for (int q = 0; q < LBN; ++q) {
-      const int64_t idx = wave * LBN + q;
-      int64_t off;
-      if (P <= 256) {
-        const int64_t b = idx * 1024, run = 128 * P;
-        off = ((n0 / P + b / run) * (g.b.kpad / 2)) * 4 * P + b % run;
-      } else {
-        off = ((n0 / P) * (g.b.kpad / 2) + idx) * 4 * P + (n0 % P) * 4;
-      }
-      vn_off[q] = (int32_t)off;
+      const int b = wave * LBN + q, ks = b >> 4, i = (b >> 2) & 3;
+      const int64_t col = n0 + 64 * (b & 3);
+      vn_off[q] = (int32_t)((16 * ks + i) * 4 * P + (col / P) * (g.b.kpad / 2) * 4 * P + (col % P) * 4);
     }
   } else if constexpr (BPK) {
     // Element (k, n) at col(n) + row(k); a lane's 8 columns stay in one panel
@@ -243,23 +248,16 @@ __device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g) {
     return *(const bf16x8_t*)(a_frag + stage * STAGE + i * 16 * ROWB + ((4 * ks + fg) ^ fswz) * 16);
   };
   // VNNI B: column n = wn * 64 + 16 j + lane % 16 needs K pairs
-  // 16 ks + 4 (lane / 16) .. + 3 (4 PL bytes apart), i.e. K values
-  // 32 ks + 8 (lane / 16) .. + 7 -- the MFMA's operand.
-  int b_vn[VN ? FN : 1];
-  const int pair_pitch = 4 * PL;
-  if constexpr (VN) {
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int n = wn * WN + 16 * j + frow;
-      b_vn[j] = A_BYTES + (n / PL) * 32 * pair_pitch + (n % PL) * 4 + 4 * fg * pair_pitch;
-    }
-  }
+  // 16 ks + 4 (lane / 16) + i, i = 0 .. 3 (K values 32 ks + 8 (lane / 16)
+  // .. + 7, the MFMA's operand): one 4-byte read per slab, lane l at byte
+  // 4 (l % 16) of f = l / 16's 64 bytes of the column group's line.
+  constexpr int VSLAB = BN * 16;  // 4 KiB: one K pair of each tile column
+  const int b_vn = A_BYTES + (wn * (WN / 16)) * 256 + fg * 64 + frow * 4;
   auto b_read = [&](int stage, int ks, int j) -> bf16x8_t {
     if constexpr (VN) {
-      const uint8_t* p = lds + stage * STAGE + b_vn[j] + 16 * ks * pair_pitch;
-      const uint4 v = make_uint4(*(const uint32_t*)p, *(const uint32_t*)(p + pair_pitch),
-                                 *(const uint32_t*)(p + 2 * pair_pitch),
-                                 *(const uint32_t*)(p + 3 * pair_pitch));
+      const uint8_t* p = lds + stage * STAGE + b_vn + j * 256 + ks * 4 * VSLAB;
+      const uint4 v = make_uint4(*(const uint32_t*)p, *(const uint32_t*)(p + VSLAB),
+                                 *(const uint32_t*)(p + 2 * VSLAB), *(const uint32_t*)(p + 3 * VSLAB));
       return __builtin_bit_cast(bf16x8_t, v);
     } else if constexpr (BT) {
       const uint8_t* p = lds + stage * STAGE + b_tr[j] + 32 * ks * NROWB;
