@@ -129,6 +129,45 @@ __device__ __forceinline__ void column_vectors(const GemmArgs& g, int64_t col, b
   shift = (g.shift && in) ? load_any(g.shift, g.vec_dtype, col) : 0.f;
 }
 
+// Bias, scale and shift of columns col .. col + 3 (columns from n on:
+// identity values): one 8-byte (bf16) or 16-byte (f32) load per vector where
+// all four columns are below n and the load is aligned, else element by
+// element.
+__device__ __forceinline__ void column_vectors4(const GemmArgs& g, int64_t col, int64_t n, float (&cb)[4],
+                                                float (&cs)[4], float (&ch)[4]) {
+  const bool bf = g.vec_dtype == HMX_DTYPE_BF16;
+  auto four = [&](const void* p, float id, float (&out)[4]) {
+    if (!p) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[e] = id;
+      return;
+    }
+    const uint16_t* h = (const uint16_t*)p + col;
+    const float* f = (const float*)p + col;
+    if (col + 4 <= n && (bf ? ((uintptr_t)h & 7) : ((uintptr_t)f & 15)) == 0) {
+      if (bf) {
+        const uint2 v = *(const uint2*)h;
+        out[0] = bf16_bits_to_f32((uint16_t)(v.x & 0xffff));
+        out[1] = bf16_bits_to_f32((uint16_t)(v.x >> 16));
+        out[2] = bf16_bits_to_f32((uint16_t)(v.y & 0xffff));
+        out[3] = bf16_bits_to_f32((uint16_t)(v.y >> 16));
+      } else {
+        const float4 v = *(const float4*)f;
+        out[0] = v.x;
+        out[1] = v.y;
+        out[2] = v.z;
+        out[3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[e] = col + e < n ? load_any(p, g.vec_dtype, col + e) : id;
+    }
+  };
+  four(g.bias, 0.f, cb);
+  four(g.scale, 1.f, cs);
+  four(g.shift, 0.f, ch);
+}
+
 
 // f(std::integral_constant<int, I>) for the runtime index i == I (0 <= i <
 // N). A loop the compiler leaves rolled (one around an epilogue program's

@@ -322,11 +322,7 @@ __device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g) {
   // Bias, scale and shift of the lane's four columns of fragment column j
   // (columns past N: identity values, for ragged tiles).
   auto vectors4 = [&](int j, float (&cb)[4], float (&cs)[4], float (&ch)[4]) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int64_t col = n0 + col4_of(j) + e;
-      column_vectors(g, col, !RAGGED || col < g.n, cb[e], cs[e], ch[e]);
-    }
+    column_vectors4(g, n0 + col4_of(j), g.n, cb, cs, ch);
   };
   if constexpr (staged_act(ACT)) {
     // Any other named activation, or an epilogue program: each wave stages

@@ -396,6 +396,39 @@ def test_linear_config4_silu(gpu_device) -> None:
     _check(got, ref, 4096, xn, wn, "bf16")
 
 
+@pytest.mark.parametrize(
+    ("m", "n", "k", "trans_b", "vectors"),
+    [(8192, 11008, 4096, True, "bias"), (4096, 8192, 256, False, "none"), (3072, 6144, 128, True, "all_f32")],
+)
+def test_multi_round_tiles_match_single_rounds(gpu_device, m, n, k, trans_b, vectors) -> None:
+    # More 256 x 256 tiles than CUs (several rounds; config 4 first, whose
+    # last round is the 256 x 128 tail launch) against blocks of 1024 rows,
+    # each a single round of one workgroup per tile. Each output is the same
+    # K walk in either, so the results are equal bit for bit; bias, scale and
+    # shift in bf16 and f32 take the epilogue's 8- and 16-byte loads.
+    a = tensor(RNG.uniform(-1, 1, (m, k)).astype(np.float32), "bf16", gpu_device)
+    b = tensor(RNG.uniform(-1, 1, (n, k) if trans_b else (k, n)).astype(np.float32), "bf16", gpu_device)
+    vdt = torch.float32 if vectors == "all_f32" else torch.bfloat16
+    kw = {}
+    if vectors != "none":
+        kw["bias"] = torch.randn(n, device=gpu_device, dtype=vdt)
+    if vectors == "all_f32":
+        kw["scale"] = torch.rand(n, device=gpu_device, dtype=vdt) + 0.5
+        kw["shift"] = torch.randn(n, device=gpu_device, dtype=vdt)
+    fn = F.silu if vectors != "none" else None
+    if fn is not None:
+        kw["epilogue"] = fn
+    full = U.matmul(a, b, trans_b=trans_b, **kw)
+    blocks = torch.cat([U.matmul(a[r:r + 1024], b, trans_b=trans_b, **kw) for r in range(0, m, 1024)])
+    assert torch.equal(full, blocks)
+    rows = torch.from_numpy(np.sort(RNG.choice(m, 32, replace=False)))
+    an, bn = to_np(a[rows.to(gpu_device)]), to_np(b)
+    vec = {key: to_np(kw[key]) for key in ("bias", "scale", "shift") if key in kw}
+    ref = R.matmul(an, bn, False, trans_b, vec.get("bias"), vec.get("scale"), vec.get("shift"),
+                   act="silu" if fn is not None else "identity", out="bf16")
+    _check(to_np(full[rows.to(gpu_device)]), ref, k, an, bn, "bf16")
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_linear_follows_weight_updates(gpu_device, dtype) -> None:
     tdtype = torch.float32 if dtype == "f32" else torch.bfloat16
