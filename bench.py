@@ -185,23 +185,23 @@ class Gemm(Workload):
 
 
 class GemmLongK(Workload):
-    """bf16 GEMM 4096 x 4096 x 16384 through the library: the steady state of
-    the config-3 kernel (the per-launch fixed cost -- first loads, the
-    epilogue's C writes -- is a quarter as large a share as at K = 4096)."""
+    """bf16 GEMM 4096 x 4096 x K through the library: config 3's kernel at
+    other depths (K = 16384: the steady state, where the per-launch fixed
+    cost -- first loads, the epilogue's C writes -- is a quarter as large a
+    share as at K = 4096; the sweep over K separates the two)."""
 
-    def __init__(self, device) -> None:
+    def __init__(self, device, k: int = 16384) -> None:
         import torch
 
         import helion_mlir_utils as U
 
         g = torch.Generator().manual_seed(2)
         m = n = 4096
-        k = 16384
         self.a = (torch.rand(m, k, generator=g) * 2 - 1).to(torch.bfloat16).to(device)
         self.b = (torch.rand(k, n, generator=g) * 2 - 1).to(torch.bfloat16).to(device)
         self.U = U
-        self.name = "gemm_longk"
-        self.description = "bf16 GEMM 4096 x 4096 x 16384 (config 3 kernel, long K)"
+        self.name = "gemm_longk" if k == 16384 else f"gemm_k{k}"
+        self.description = f"bf16 GEMM 4096 x 4096 x {k} (config 3 kernel, K = {k})"
         self.unit, self.bound, self.peak = "TFLOP/s", "mfma", PEAK_BF16_TFLOPS
         self.work = 2.0 * m * n * k
         self.dtype = "bf16"
@@ -618,6 +618,7 @@ def make(name: str, device) -> Workload:
         "gemm_f32c": lambda: Gemm(device, "f32"),
         "gemm_prepacked": lambda: Gemm(device, prepacked=True),
         "gemm_longk": lambda: GemmLongK(device),
+        **{f"gemm_k{k}": (lambda k=k: GemmLongK(device, k)) for k in (1024, 2048, 8192)},
         "gemm_hipblaslt": lambda: VendorGemm(device),
         "gemm_longk_hipblaslt": lambda: VendorGemm(device, 16384),
         "linear": lambda: Linear(device),

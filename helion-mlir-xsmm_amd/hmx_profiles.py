@@ -5,6 +5,7 @@ launch from counter runs.
     python helion-mlir-xsmm_amd/hmx_profiles.py trace WORKLOAD TRACE_DIR BENCH_LOG OUT.md "TITLE" "COMMAND"
     python helion-mlir-xsmm_amd/hmx_profiles.py traffic PMC_ROOT OUT.json
     python helion-mlir-xsmm_amd/hmx_profiles.py clock PMC_ROOT OUT.md "TITLE" "COMMAND"
+    python helion-mlir-xsmm_amd/hmx_profiles.py kfit PMC_ROOT OUT.md "TITLE" "COMMAND"
 
 ``TRACE_DIR`` holds ``run_kernel_trace.csv`` and ``run_kernel_stats.csv`` of
 ``rocprofv3 --kernel-trace --stats -o run -f csv -- python3 bench.py
@@ -15,7 +16,11 @@ launch from counter runs.
 ``clock``, ``PMC_ROOT`` holds one directory per workload, each a counter run
 with ``GRBM_GUI_ACTIVE`` and ``SQ_VALU_MFMA_BUSY_CYCLES`` (and its
 ``run_agent_info.csv``): the clock each GEMM dispatch ran at and the share of
-SIMD cycles its MFMA unit was busy.
+SIMD cycles its MFMA unit was busy. ``kfit`` reads such runs of the 4096 x
+4096 x K GEMM workloads (``gemm_k<K>``, ``gemm`` = 4096, ``gemm_longk`` =
+16384) and fits, by least squares over K, the duration against K and each
+SIMD's cycles outside the MFMA unit against its MFMA cycles: the intercepts
+are the per-launch fixed cost.
 """
 
 from __future__ import annotations
@@ -134,39 +139,136 @@ def traffic(pmc_root: Path) -> dict:
     return out
 
 
+def _clock_rows(run: Path, last: int) -> tuple[str, float, float, float] | None:
+    """(kernel, mean duration in us, clock in GHz, MFMA-busy share) of the
+    last ``last`` dispatches of the longest-running kernel of one counter
+    run, or None without one."""
+    path = run / "run_counter_collection.csv"
+    if not path.is_file():
+        return None
+    agent = next((r for r in _rows(run / "run_agent_info.csv") if r.get("Name", "").startswith("gfx")), {})
+    xcc, simds = int(agent.get("Num_Xcc", 8)), int(agent.get("Simd_Count", 1024))
+    disp: dict[int, dict] = collections.defaultdict(dict)
+    for r in _rows(path):
+        d = disp[int(r["Dispatch_Id"])]
+        d["name"] = r["Kernel_Name"]
+        d["dur"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        d[r["Counter_Name"]] = float(r["Counter_Value"])
+    totals: dict[str, float] = collections.defaultdict(float)
+    for d in disp.values():
+        totals[d["name"]] += d["dur"]
+    name = max(totals, key=totals.get)
+    rows = [d for _, d in sorted(disp.items()) if d["name"] == name][-last:]
+    dur = sum(d["dur"] for d in rows) / len(rows)
+    clocks = [d["GRBM_GUI_ACTIVE"] / xcc / (d["dur"] * 1e3) for d in rows]
+    busy = [d["SQ_VALU_MFMA_BUSY_CYCLES"] / simds / (d["GRBM_GUI_ACTIVE"] / xcc) for d in rows]
+    return name, dur, sum(clocks) / len(rows), sum(busy) / len(rows)
+
+
+def _dispatches(run: Path, name: str) -> int:
+    """The number of dispatches of kernel ``name`` in a counter run."""
+    return len({r["Dispatch_Id"] for r in _rows(run / "run_counter_collection.csv") if r["Kernel_Name"] == name})
+
+
+def _line_fit(xs: list[float], ys: list[float]) -> tuple[float, float]:
+    """Least-squares (intercept, slope) of ys against xs."""
+    n = len(xs)
+    mx, my = sum(xs) / n, sum(ys) / n
+    sxx = sum((x - mx) ** 2 for x in xs)
+    slope = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sxx
+    return my - slope * mx, slope
+
+
+def kfit_summary(pmc_root: Path, title: str, command: str, last: int = 50) -> str:
+    """The K sweep of the 4096 x 4096 x K GEMM. Per K: the duration, and per
+    XCD the GRBM_GUI_ACTIVE cycles, per SIMD the MFMA-busy cycles. Then three
+    least-squares lines over K: duration against K (the intercept is the
+    per-launch fixed cost); GRBM cycles against duration (the slope is the
+    clock; the intercept, cycles the counter adds outside the kernel's own
+    timestamps, is why the cycles over the duration overstate the clock of
+    short kernels); and, at the fitted clock, each SIMD's cycles outside the
+    MFMA unit against its MFMA cycles."""
+    pts = _k_points(pmc_root, last)
+    ks = [p[0] for p in pts]
+    durs = [p[2] for p in pts]
+    grbm = [p[3] * p[2] * 1e3 for p in pts]  # cycles per XCD
+    mfma = [p[4] * g for p, g in zip(pts, grbm)]  # busy cycles per SIMD
+    out = [f"# {title}", "", "Command:", "", "```", command, "```", ""]
+    if len(pts) < 2:
+        return "\n".join(out + ["(fewer than two depths)"]) + "\n"
+    f0, s0 = _line_fit(ks, durs)
+    c0, ghz = _line_fit(durs, [g / 1e3 for g in grbm])  # kcycles against us: slope in GHz
+    other = [ghz * d * 1e3 - m for d, m in zip(durs, mfma)]
+    f1, s1 = _line_fit(mfma, other)
+    out += ["| K | Kernel | Duration (us) | TFLOP/s | GRBM kcycles / XCD | GRBM / duration (GHz) | MFMA kcycles / SIMD |"
+            " MFMA busy at the fitted clock |", "|---|---|---|---|---|---|---|---|"]
+    for (k, name, dur, _clk, _util), g, m in zip(pts, grbm, mfma):
+        out.append(f"| {k} | `{kernel_name(name)[:60]}` | {dur:.1f} | {2 * 4096 * 4096 * k / dur / 1e6:.0f} | "
+                   f"{g / 1e3:.1f} | {g / 1e3 / dur:.3f} | {m / 1e3:.1f} | {m / (ghz * dur * 1e3):.3f} |")
+    out += ["",
+            f"Duration = {f0:.2f} us + {s0 * 1e3:.3f} us per 1000 of K (least squares over {len(pts)} depths): "
+            f"the K-proportional part runs at {2 * 4096 * 4096 / s0 / 1e6:.0f} TFLOP/s, and the fixed {f0:.2f} us "
+            f"per launch is {100 * f0 / (f0 + s0 * 4096):.1f} % of the 4096^3 launch.",
+            f"GRBM cycles = {c0:.1f} kcycles + {ghz:.3f} GHz x duration: the clock is {ghz:.3f} GHz, and the "
+            f"counter adds {c0:.1f} kcycles per dispatch ({c0 / ghz:.1f} us at that clock) outside the kernel's "
+            f"timestamps.",
+            f"Other cycles = {f1 / 1e3:.2f} kcycles + {s1:.3f} x MFMA cycles per SIMD (at {ghz:.3f} GHz): the K "
+            f"loop spends {s1:.3f} cycles outside the MFMA unit per MFMA cycle, and each launch "
+            f"{f1 / 1e3:.2f} kcycles ({f1 / ghz / 1e3:.1f} us) more."]
+    return "\n".join(out) + "\n"
+
+
+def _k_points(pmc_root: Path, last: int) -> list[tuple]:
+    """(K, kernel, duration, GRBM cycles / duration, MFMA busy) of the 4096 x
+    4096 x K GEMM runs in ``pmc_root``, by K."""
+    names = {"gemm": 4096, "gemm_longk": 16384}
+    pts = []
+    for run in sorted(p for p in pmc_root.iterdir() if p.is_dir()):
+        k = names.get(run.name) or (int(run.name[6:]) if run.name.startswith("gemm_k") else None)
+        got = _clock_rows(run, last) if k else None
+        if got:
+            pts.append((k, *got))
+    return sorted(pts)
+
+
+def counter_window(pmc_root: Path, last: int = 50) -> tuple[float, float] | None:
+    """(kcycles per XCD the GRBM counter adds outside a kernel's timestamps,
+    the clock in GHz): the least-squares line of GRBM cycles against duration
+    over the K-sweep runs in ``pmc_root``; None with fewer than two."""
+    pts = _k_points(pmc_root, last)
+    if len(pts) < 2:
+        return None
+    return _line_fit([p[2] for p in pts], [p[3] * p[2] for p in pts])
+
+
 def clock_summary(pmc_root: Path, title: str, command: str, last: int = 50) -> str:
     """Per workload (a directory of ``pmc_root``): over the last ``last``
     dispatches of its longest-running kernel, the mean duration, the clock
-    (GRBM_GUI_ACTIVE cycles, counted once per XCD, over the duration), the
-    MFMA-busy share of SIMD cycles (SQ_VALU_MFMA_BUSY_CYCLES, summed over the
-    SIMDs, over the XCD's cycles times the SIMD count) and their product, the
-    MFMA cycles per SIMD per nanosecond."""
-    out = [f"# {title}", "", "Command:", "", "```", command, "```", "",
-           "| Workload | Kernel | Dispatches | Duration (us) | Clock (GHz) | MFMA busy | Busy x clock |",
-           "|---|---|---|---|---|---|---|"]
+    and the MFMA-busy share of SIMD cycles (SQ_VALU_MFMA_BUSY_CYCLES, summed
+    over the SIMDs, over the XCD's cycles times the SIMD count). The clock is
+    GRBM_GUI_ACTIVE cycles (counted once per XCD) over the duration, less the
+    cycles the counter adds outside the kernel's timestamps when the K-sweep
+    runs in the same root give them (``counter_window``); the raw ratio is
+    shown beside it."""
+    window = counter_window(pmc_root, last)
+    c0 = window[0] * 1e3 if window else 0.0
+    out = [f"# {title}", "", "Command:", "", "```", command, "```", ""]
+    if window:
+        out += [f"The GRBM counter adds {window[0]:.1f} kcycles per dispatch outside the kernel's timestamps "
+                f"(least squares of its cycles against the duration over the 4096 x 4096 x K runs, slope "
+                f"{window[1]:.3f} GHz); the clock column takes them off, the raw column does not.", ""]
+    out += ["| Workload | Kernel | Dispatches | Duration (us) | Clock (GHz) | MFMA busy | Busy x clock | Raw GRBM / duration (GHz) |",
+            "|---|---|---|---|---|---|---|---|"]
     for run in sorted(p for p in pmc_root.iterdir() if p.is_dir()):
-        path = run / "run_counter_collection.csv"
-        if not path.is_file():
+        got = _clock_rows(run, last)
+        if got is None:
             continue
-        agent = next((r for r in _rows(run / "run_agent_info.csv") if r.get("Name", "").startswith("gfx")), {})
-        xcc, simds = int(agent.get("Num_Xcc", 8)), int(agent.get("Simd_Count", 1024))
-        disp: dict[int, dict] = collections.defaultdict(dict)
-        for r in _rows(path):
-            d = disp[int(r["Dispatch_Id"])]
-            d["name"] = r["Kernel_Name"]
-            d["dur"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-            d[r["Counter_Name"]] = float(r["Counter_Value"])
-        totals: dict[str, float] = collections.defaultdict(float)
-        for d in disp.values():
-            totals[d["name"]] += d["dur"]
-        name = max(totals, key=totals.get)
-        rows = [d for _, d in sorted(disp.items()) if d["name"] == name][-last:]
-        dur = sum(d["dur"] for d in rows) / len(rows)
-        clocks = [d["GRBM_GUI_ACTIVE"] / xcc / (d["dur"] * 1e3) for d in rows]
-        busy = [d["SQ_VALU_MFMA_BUSY_CYCLES"] / simds / (d["GRBM_GUI_ACTIVE"] / xcc) for d in rows]
-        clk, util = sum(clocks) / len(rows), sum(busy) / len(rows)
-        out.append(f"| {run.name} | `{kernel_name(name)[:70]}` | {len(rows)} | {dur:.1f} | {clk:.3f} | "
-                   f"{util:.3f} | {clk * util:.3f} |")
+        name, dur, raw, util_raw = got
+        cycles = raw * dur * 1e3  # per XCD, raw
+        clk = (cycles - c0) / (dur * 1e3)
+        util = util_raw * cycles / (cycles - c0)
+        out.append(f"| {run.name} | `{kernel_name(name)[:70]}` | {min(last, _dispatches(run, name))} | {dur:.1f} | "
+                   f"{clk:.3f} | {util:.3f} | {clk * util:.3f} | {raw:.3f} |")
     return "\n".join(out) + "\n"
 
 
@@ -174,6 +276,9 @@ def main(argv: list[str]) -> int:
     if len(argv) >= 7 and argv[1] == "trace":
         _, _, workload, trace_dir, log, out, title, command = argv[:8]
         Path(out).write_text(trace_summary(workload, Path(trace_dir), Path(log), title, command))
+        return 0
+    if len(argv) == 6 and argv[1] == "kfit":
+        Path(argv[3]).write_text(kfit_summary(Path(argv[2]), argv[4], argv[5]))
         return 0
     if len(argv) == 6 and argv[1] == "clock":
         Path(argv[3]).write_text(clock_summary(Path(argv[2]), argv[4], argv[5]))
