@@ -13,6 +13,7 @@
 // results.
 #include <hip/hiprtc.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -112,10 +113,13 @@ std::string epilogue_key(int act, float act_arg, const hmx_program& prog) {
 }
 
 // Compiles `source` for the current device and loads it; the kernel
-// `hmx_jit_kernel`, or null (the log kept in g_jit_last_log).
+// `hmx_jit_kernel`, or null (the log kept in g_jit_last_log). A HIP call that
+// fails here leaves no error behind: the call goes on with the prebuilt
+// kernels, and their launch check must not see this one's error.
 hipFunction_t compile(const std::string& source, int device) {
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+    (void)hipGetLastError();
     g_jit_last_log = "hipGetDeviceProperties failed";
     return nullptr;
   }
@@ -148,7 +152,10 @@ hipFunction_t compile(const std::string& source, int device) {
     if (hipModuleLoadData(&module, code.data()) == hipSuccess &&
         hipModuleGetFunction(&fn, module, "hmx_jit_kernel") != hipSuccess)
       fn = nullptr;
-    if (!fn) log += "\nloading the code object failed";
+    if (!fn) {
+      (void)hipGetLastError();
+      log += "\nloading the code object failed";
+    }
   } else {
     log = std::string(hiprtcGetErrorString(rc)) + " (" + arch + ")\n" + log + "\nsource:\n" + source;
   }
@@ -174,22 +181,29 @@ hipFunction_t jit_function(const std::string& key, const std::string& source, in
 
 // Enqueues `fn` on `stream` (through hipExtModuleLaunchKernel while timing
 // events are armed on this thread, as launch() does for the library's own
-// kernels).
-int jit_launch(hipFunction_t fn, dim3 grid, unsigned block, void** params, hipStream_t stream,
-               const char* what) {
+// kernels). A launch the runtime refuses is remembered like a failed
+// compilation (key `key` is not tried again), leaves no error behind and
+// returns HMX_ERR_UNSUPPORTED: the call takes the prebuilt kernels.
+int jit_launch(const std::string& key, hipFunction_t fn, dim3 grid, unsigned block, void** params,
+               hipStream_t stream, const char* what) {
   LaunchEvents& ev = launch_events();
   hipError_t err;
   if (ev.start == nullptr && ev.stop == nullptr) {
     err = hipModuleLaunchKernel(fn, grid.x, grid.y, grid.z, block, 1, 1, 0, stream, params, nullptr);
   } else {
-    hipEvent_t start = ev.start;
-    ev.start = nullptr;
+    // The step's first kernel records the start event: taken only by a
+    // launch that happens.
     err = hipExtModuleLaunchKernel(fn, grid.x * block, grid.y, grid.z, block, 1, 1, 0, stream, params, nullptr,
-                                   start, ev.stop, 0);
+                                   ev.start, ev.stop, 0);
+    if (err == hipSuccess) ev.start = nullptr;
   }
-  return err == hipSuccess ? HMX_OK
-                           : set_error(HMX_ERR_HIP, "%s: run-time compiled kernel launch: %s", what,
-                                       hipGetErrorString(err));
+  if (err == hipSuccess) return HMX_OK;
+  (void)hipGetLastError();
+  std::lock_guard<std::mutex> guard(g_jit_lock);
+  g_jit_kernels[key] = nullptr;
+  ++g_jit_stats.failed;
+  g_jit_last_log = std::string(what) + ": run-time compiled kernel launch: " + hipGetErrorString(err);
+  return HMX_ERR_UNSUPPORTED;
 }
 
 }  // namespace
@@ -217,7 +231,7 @@ int launch_mi16_jit(const GemmArgs& g, int lb, bool bf16, bool ragged, int bm, i
   if (!fn) return HMX_ERR_UNSUPPORTED;
   GemmArgs copy = g;
   void* params[] = {&copy};
-  return jit_launch(fn, grid, (unsigned)nw * 64, params, stream, "gemm");
+  return jit_launch(key, fn, grid, (unsigned)nw * 64, params, stream, "gemm");
 }
 
 int launch_group_norm_jit(bool bf16, const void* x, void* y, const GroupNormArgs& a, int64_t rows, int tpr,
@@ -242,15 +256,18 @@ int launch_group_norm_jit(bool bf16, const void* x, void* y, const GroupNormArgs
   // As many workgroups as the GPU holds at once, each walking rows blockIdx,
   // blockIdx + grid, ... (as the library's own launch of the kernel).
   int per_cu = 0;
-  if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, (int)block, 0) != hipSuccess || per_cu < 1)
+  if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, (int)block, 0) != hipSuccess) {
+    (void)hipGetLastError();
     per_cu = 1;
+  }
+  per_cu = std::max(per_cu, 1);
   const int64_t needed = ceil_div(rows, rows_per_block);
   const dim3 grid((unsigned)std::min<int64_t>(needed, (int64_t)per_cu * cus));
   const void* xp = x;
   void* yp = y;
   GroupNormArgs copy = a;
   void* params[] = {&xp, &yp, &copy, &rows, &tpr, &gv};
-  return jit_launch(fn, grid, block, params, stream, "group_norm");
+  return jit_launch(key, fn, grid, block, params, stream, "group_norm");
 }
 
 }  // namespace hmx
@@ -264,6 +281,10 @@ extern "C" int hmx_jit_info(int64_t* compiled, int64_t* failed, int64_t* launche
 }
 
 extern "C" const char* hmx_jit_last_log(void) {
+  // A copy per thread: valid until this thread's next call, whatever other
+  // threads' compilations write meanwhile.
+  thread_local std::string copy;
   std::lock_guard<std::mutex> guard(hmx::g_jit_lock);
-  return hmx::g_jit_last_log.c_str();
+  copy = hmx::g_jit_last_log;
+  return copy.c_str();
 }
