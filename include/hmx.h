@@ -195,15 +195,18 @@ int hmx_device_check(int* compute_units);
 int hmx_time_launches(void* start_event, void* stop_event);
 
 /* Run-time compiled epilogues, as the reference reports its JIT's work
- * (helion_mlir_backend.explain(), _compiler/call_trace.py:220): GEMM kernels
- * compiled with an epilogue program or a named activation in their register
- * epilogue (hipRTC, on first use of each kernel variant and epilogue), the
- * compilations that failed (their GEMMs ran the interpreter), and the launches
- * of compiled kernels. Any pointer may be NULL. HMX_JIT=0 in the environment
- * turns run-time compilation off (read on every call). */
+ * (helion_mlir_backend.explain(), _compiler/call_trace.py:220): kernels
+ * compiled with an epilogue program or a named activation built in (the
+ * 16x16x32 GEMM's register epilogue and group_norm's whole-row kernel;
+ * hipRTC, on first use of each kernel variant and epilogue), the
+ * compilations or launches that failed (those calls ran the prebuilt
+ * kernels, and the variant is not tried again), and the launches of compiled
+ * kernels. Any pointer may be NULL. HMX_JIT=0 in the environment turns
+ * run-time compilation off (read on every call). */
 int hmx_jit_info(int64_t* compiled, int64_t* failed, int64_t* launches);
 
-/* The compiler log of the last failed run-time compilation ("" if none). */
+/* The log of the last failed run-time compilation or launch ("" if none):
+ * a copy per thread, valid until the same thread calls this again. */
 const char* hmx_jit_last_log(void);
 
 /*
