@@ -356,6 +356,31 @@ def test_jit_group_norm_programs(gpu_device, monkeypatch, dtype: str, groups: in
         assert_close(to_np(again), ref, 1e-4, 1e-4)
 
 
+@pytest.mark.parametrize("layout", ["blocked_vnni", "vnni64", "vnni512", "panels64", "blocked"])
+def test_jit_epilogues_on_packed_b(gpu_device, layout: str) -> None:
+    # Whole 256 x 256 tiles with B in each packed layout: the 16x16x32 kernel
+    # compiled with the program for that layout's loads, bit-equal to the
+    # same product with plain B (the same K walk and the same compiled
+    # epilogue), and to the oracle within the bf16 tolerance.
+    m, n, k = 512, 1024, 384
+    fn = EPILOGUES["silu_mix"]
+    a, b = _operands(m, n, k, False, False, "bf16", gpu_device)
+    bias = tensor(RNG.normal(0, 1, n).astype(np.float32), "bf16", gpu_device)
+    bt = b.t().contiguous()
+    packed = {"blocked_vnni": lambda: U.pack_b_blocked_vnni(b), "vnni64": lambda: U.pack_b_vnni_t(bt, 64),
+              "vnni512": lambda: U.pack_b_vnni_t(bt, 512), "panels64": lambda: U.pack_b_panels(b, 64),
+              "blocked": lambda: U.pack_b_blocked(b)}[layout]()
+    start = native.jit_info()
+    got = U.matmul_prepacked_b(a, packed, n, bias, fn)
+    torch.cuda.synchronize()
+    info = native.jit_info()
+    assert info["failed"] == start["failed"], info["last_failure_log"]
+    assert info["launches"] > start["launches"], "the compiled kernel did not run"
+    assert torch.equal(got, U.matmul(a, b, bias=bias, epilogue=fn))
+    ref = R.matmul(to_np(a), to_np(b), bias=to_np(bias), act=fn, out="bf16")
+    _check(to_np(got), ref, k, to_np(a), to_np(b), "bf16")
+
+
 def test_no_run_time_compilation_failed(gpu_device) -> None:
     # Every kernel the tests above compiled at run time compiled: a failure
     # would have sent its GEMM to the interpreter without an error.
