@@ -121,3 +121,15 @@ def assert_specials_close(got: np.ndarray, ref: np.ndarray, rtol: float, atol: "
             raise AssertionError(f"{int(bad.sum())} {what} elements differ: {detail}")
     fin = np.isfinite(ref)
     assert_close(got[fin], ref[fin], rtol, atol[fin])
+
+
+def tile_rows(rng: np.random.Generator, m: int, per_band: int = 2, band: int = 128) -> np.ndarray:
+    """Sorted row indices, ``per_band`` drawn from every ``band``-row slice of
+    ``m`` rows (the last, ragged slice included). Checked over all columns,
+    such a sample meets every 128- or 256-row tile of a GEMM's output, which a
+    plain random sample of rows does not promise."""
+    picks = []
+    for start in range(0, m, band):
+        stop = min(m, start + band)
+        picks.append(rng.choice(np.arange(start, stop), min(per_band, stop - start), replace=False))
+    return np.sort(np.concatenate(picks))

@@ -6,7 +6,8 @@ GEMMs over every packed layout, and the pack kernels (bit-exact).
 Tolerances (BASELINE): bf16-in / f32-accumulate rtol 1e-2 plus an atol scaled
 by sqrt(K) (``bf16_gemm_atol``); f32 rtol 1e-4, and the reference's own
 max-normalised error < 1e-5 for bmm (tests/test_cpu_utils_split_k_bmm.py:15-16).
-Full BASELINE sizes are checked on sampled rows / slices against the oracle.
+Full BASELINE sizes are checked against the oracle on rows drawn from every
+128-row band (``tile_rows``), over all columns: every output tile is sampled.
 """
 
 from __future__ import annotations
@@ -19,7 +20,7 @@ import torch.nn.functional as F
 import helion_mlir_utils as U
 import hmx_workloads as W
 from oracle import restate as R
-from tests.helpers import assert_close, bf16_gemm_atol, max_rel_error, tensor, to_np
+from tests.helpers import assert_close, bf16_gemm_atol, max_rel_error, tensor, tile_rows, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -183,7 +184,7 @@ def test_matmul_trans_a_4096(gpu_device) -> None:
     cfg = W.config3()
     at = cfg["a"].t().contiguous().to(gpu_device)  # A stored [K, M]
     c = U.matmul(at, cfg["b"].to(gpu_device), trans_a=True)
-    rows = np.sort(RNG.choice(4096, 64, replace=False))
+    rows = tile_rows(RNG, 4096)
     an, bn = to_np(cfg["a"][torch.from_numpy(rows)]), to_np(cfg["b"])
     _check(to_np(c)[rows], R.matmul(an, bn, out="bf16"), 4096, an, bn, "bf16")
 
@@ -300,7 +301,7 @@ def test_bmm_whole_tiles_split_k_direct_to_lds(gpu_device) -> None:
     c = U.bmm(a, b, splits=2)
     assert torch.equal(U.bmm(a, b, splits=2), c)
     torch.cuda.synchronize()
-    rows = np.sort(RNG.choice(4096, 64, replace=False))
+    rows = tile_rows(RNG, 4096)
     an, bn = to_np(a)[0][rows], to_np(b)[0]
     _check(to_np(c)[0][rows], R.matmul(an, bn, out="bf16"), 1024, an, bn, "bf16")
 
@@ -320,7 +321,7 @@ def test_matmul_config3_bf16_4096(gpu_device, out_dtype) -> None:
     a, b = cfg["a"].to(gpu_device), cfg["b"].to(gpu_device)
     c = U.matmul(a, b, out_dtype=out_dtype)
     torch.cuda.synchronize()
-    rows = torch.from_numpy(np.sort(RNG.choice(4096, 96, replace=False)))
+    rows = torch.from_numpy(tile_rows(RNG, 4096))
     got = to_np(c[rows.to(gpu_device)])
     an, bn = to_np(cfg["a"][rows]), to_np(cfg["b"])
     ref = R.matmul(an, bn, out="bf16" if out_dtype == torch.bfloat16 else "f32")
@@ -367,7 +368,7 @@ def test_f32_big_tile_unsplit(gpu_device, trans_b: bool, epilogue: str, out: str
         kw.update(bias=bias, epilogue=fn)
     a_pitch = torch.empty(m, k + 1, device=gpu_device)[:, :k]
     a_pitch.copy_(a)
-    rows = torch.from_numpy(np.sort(RNG.choice(m, 48, replace=False))).to(gpu_device)
+    rows = torch.from_numpy(tile_rows(RNG, m, 1)).to(gpu_device)
     an, wn = to_np(a[rows]), to_np(w)
     ref = R.matmul(an, wn, False, trans_b, to_np(bias) if fn is not None else None, act=epilogue, out=out)
     for x in (a, a_pitch):
@@ -389,7 +390,7 @@ def test_linear_config4_silu(gpu_device) -> None:
         y2, cache2 = U.linear(x, layer, F.silu, cache=cache)
     assert cache2.call is cache.call and torch.equal(y, y2)
     torch.cuda.synchronize()
-    rows = torch.from_numpy(np.sort(RNG.choice(8192, 64, replace=False)))
+    rows = torch.from_numpy(tile_rows(RNG, 8192, 1))
     got = to_np(y[rows.to(gpu_device)])
     xn, wn, bn = to_np(cfg["x"][rows]), to_np(cfg["w"]), to_np(cfg["b"])
     ref = R.matmul(xn, wn, False, True, bn, act="silu", out="bf16")
@@ -421,7 +422,7 @@ def test_multi_round_tiles_match_single_rounds(gpu_device, m, n, k, trans_b, vec
     full = U.matmul(a, b, trans_b=trans_b, **kw)
     blocks = torch.cat([U.matmul(a[r:r + 1024], b, trans_b=trans_b, **kw) for r in range(0, m, 1024)])
     assert torch.equal(full, blocks)
-    rows = torch.from_numpy(np.sort(RNG.choice(m, 32, replace=False)))
+    rows = torch.from_numpy(tile_rows(RNG, m, 1))
     an, bn = to_np(a[rows.to(gpu_device)]), to_np(b)
     vec = {key: to_np(kw[key]) for key in ("bias", "scale", "shift") if key in kw}
     ref = R.matmul(an, bn, False, trans_b, vec.get("bias"), vec.get("scale"), vec.get("shift"),
