@@ -10,8 +10,9 @@ the ``helion_mlir_utils`` hot path on hand-written gfx950 kernels
 
 from __future__ import annotations
 
-from ._compiler import native as _native
 from ._compiler import output_pool as output_pool
+from ._compiler.call_trace import CallExplanation as CallExplanation
+from ._compiler.call_trace import explain as explain
 from ._compiler.native import set_native_call as set_native_call
 from ._compiler.output_pool import set_output_pool as set_output_pool
 from ._compiler.prepared import GpuLaunch as GpuLaunch
@@ -28,20 +29,8 @@ from .language import InlineMLIRHint as InlineMLIRHint
 from .language import inline_mlir as inline_mlir
 
 
-def explain() -> dict[str, object]:
-    """What the gpu target's native path has done in this process (the
-    reference's ``explain`` reports per-call dispatch decisions of its CPU
-    path, ``_compiler/call_trace.py:220``)."""
-    return {
-        "library": str(_native.library_path()),
-        "library_built": _native.available(),
-        "native_calls": _native.native_calls(),
-        "jit": _native.jit_info() if _native.available() else None,
-        "output_pool": output_pool.output_pool_stats(),
-    }
-
-
 __all__ = [
+    "CallExplanation",
     "GpuLaunch",
     "InlineMLIRHint",
     "PreparedCall",

@@ -42,6 +42,16 @@ class GpuLaunch:
         raise NotImplementedError
 
 
+# The kinds of refusal a prepared call counts.
+REFUSALS = (
+    "native calls are off",
+    "a view changes the element count",
+    "the number of varying arguments differs",
+    "a varying argument differs from the prepared one",
+    "a bound argument changed",
+)
+
+
 def _meta(t: torch.Tensor) -> tuple[object, ...]:
     return (tuple(t.shape), tuple(t.stride()), t.dtype, t.device, t.storage_offset())
 
@@ -52,7 +62,7 @@ class PreparedCall:
     ``native_calls`` counts the calls that launched the kernel directly."""
 
     __slots__ = ("_kernel", "_args", "_varying", "_fallback", "_views", "_result_shape", "_specs",
-                 "_bound_meta", "_off", "native_calls")
+                 "_bound_meta", "_off", "native_calls", "refusals", "last_refusal")
 
     def __init__(
         self,
@@ -82,6 +92,11 @@ class PreparedCall:
         )
         self._off = False
         self.native_calls = 0
+        # Calls that took the fallback, by kind of refusal, and the last
+        # one's reason in full (what ``explain`` reports, as the reference's
+        # KernelRun.refusals / .last_refusal).
+        self.refusals: dict[str, int] = {}
+        self.last_refusal: str | None = None
 
     def disable(self) -> None:
         """Send every call to the fallback from now on."""
@@ -111,8 +126,43 @@ class PreparedCall:
                 return False
         return all(_meta(self._args[i]) == meta for i, meta in self._bound_meta)
 
+    @property
+    def kernel(self) -> GpuLaunch:
+        """The bound launch this call runs natively."""
+        return self._kernel
+
+    def refusal(self, values: Sequence[object]) -> tuple[str, str] | None:
+        """Why a call with ``values`` would take the fallback -- (kind, the
+        reason in full) -- or None when it would launch natively."""
+        if not native.enabled():
+            return REFUSALS[0], "native calls are off (set_native_call(False))"
+        if self._off:
+            return REFUSALS[1], "a view changes its argument's element count: every call takes the fallback"
+        if len(values) != len(self._specs):
+            return REFUSALS[2], f"{len(values)} varying arguments, prepared with {len(self._specs)}"
+        for k, (t, (shape, strides, dtype, device)) in enumerate(zip(values, self._specs)):
+            if not isinstance(t, torch.Tensor):
+                return REFUSALS[3], f"varying argument {k} is a {type(t).__name__}, not a tensor"
+            got = (t.dtype, t.device, tuple(t.shape))
+            if got != (dtype, device, shape):
+                return REFUSALS[3], (f"varying argument {k} is {t.dtype} of shape {tuple(t.shape)} on {t.device}, "
+                                     f"prepared {dtype} of shape {shape} on {device}")
+            if strides is None and not t.is_contiguous():
+                return REFUSALS[3], f"varying argument {k} is not contiguous (strides {tuple(t.stride())})"
+            if strides is not None and tuple(t.stride()) != strides:
+                return REFUSALS[3], f"varying argument {k} has strides {tuple(t.stride())}, prepared {strides}"
+        for i, meta in self._bound_meta:
+            if _meta(self._args[i]) != meta:
+                return REFUSALS[4], (f"bound argument {i} changed shape, strides, dtype, device or storage "
+                                     f"offset since the call was prepared")
+        return None
+
     def __call__(self, *values: object) -> object:
         if not native.enabled() or not self.matches(values):
+            why = self.refusal(values)
+            if why is not None:
+                self.refusals[why[0]] = self.refusals.get(why[0], 0) + 1
+                self.last_refusal = why[1]
             return self._fallback(*values)
         full = list(self._args)
         for i, value, view in zip(self._varying, values, self._views):

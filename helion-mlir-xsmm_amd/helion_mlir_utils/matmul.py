@@ -198,7 +198,7 @@ class GemmLaunch(GpuLaunch):
     vectors are kept alive by the launch."""
 
     __slots__ = ("_fn", "_args", "_vectors", "_ws_bytes", "_staged_ws", "_rows_ok", "_device", "_shape",
-                 "_dtype", "splits")
+                 "_dtype", "splits", "calls")
 
     def __init__(
         self, ab: int, c_dtype: torch.dtype, device: torch.device, c_shape: tuple[int, ...],
@@ -245,6 +245,12 @@ class GemmLaunch(GpuLaunch):
         self._shape = c_shape
         self._dtype = c_dtype
         self.splits = s
+        self.calls = 0  # launches made
+
+    def plan(self) -> dict[str, int]:
+        """The bound plan: K splits, workgroup tile and workspace bytes."""
+        return {"splits": self.splits, "tile_m": int(self._args[29]), "tile_n": int(self._args[30]),
+                "tile_k": int(self._args[31]), "workspace_bytes": self._ws_bytes}
 
     def unbind_vectors(self) -> None:
         """Drop the references to the bound bias, scale and shift: every later
@@ -289,6 +295,7 @@ class GemmLaunch(GpuLaunch):
         native.count_call()
         if status:
             native.check(status, "hmx_gemm")
+        self.calls += 1
         return c
 
 

@@ -97,3 +97,27 @@ def test_native_switch_sends_prepared_calls_to_the_fallback(gpu_device) -> None:
         assert prepared.native_calls == before + 1
         torch.cuda.synchronize()
     assert torch.equal(y, y_off) and torch.equal(y, y_on)
+
+
+def test_explain_on_the_gpu(gpu_device) -> None:
+    # explain (the reference's call_trace.explain) on ROCm tensors: matmul runs
+    # natively with the plan gemm_plan gives; a prepared linear reports its
+    # native calls, and a call it would refuse names the argument and why.
+    import helion_mlir_backend as B
+
+    a = tensor(RNG.normal(0, 1, (1024, 512)).astype(np.float32), "bf16", gpu_device)
+    b = tensor(RNG.normal(0, 1, (512, 768)).astype(np.float32), "bf16", gpu_device)
+    e = B.explain(U.matmul, a, b)
+    assert (e.run, e.reason) == ("native", None)
+    assert e.config == U.gemm_plan(torch.bfloat16, 1024, 768, 512)
+    assert B.explain(U.matmul, a, b.float()).run == "unsupported"
+    layer = torch.nn.Linear(512, 768).to(device=gpu_device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        _, cache = U.linear(a, layer, F.silu)
+        _, cache = U.linear(a, layer, F.silu, cache=cache)
+    prepared = cache.call[1]
+    e = B.explain(prepared, a)
+    assert e.run == "native" and e.native_calls == prepared.native_calls >= 1
+    assert e.config["splits"] >= 1 and e.config["tile_m"] in (128, 256)
+    e = B.explain(prepared, a[:512])
+    assert e.run == "general" and "varying argument 0" in e.reason

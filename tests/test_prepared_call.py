@@ -152,3 +152,48 @@ def test_switch_environment_is_read_at_import() -> None:
     env = dict(os.environ, HELION_MLIR_NATIVE_CALL="0")
     out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, check=True)
     assert out.stdout.strip() == "False"
+
+
+# ---------------------------------------------------------------------------
+# explain (the reference's _compiler/call_trace.py:220-270): what a call would
+# do, without running it, over this target's kernels.
+
+
+def test_explain_a_prepared_call_and_its_refusals(native_switch) -> None:
+    x, y = torch.randn(16, 8), torch.randn(16, 8)
+    kernel = AddRows()
+    prepared = B.prepared_call(kernel, (x, y), [0], lambda a: "fallback")
+    e = B.explain(prepared, torch.randn(16, 8))
+    assert isinstance(e, B.CallExplanation)
+    assert (e.dispatch, e.run, e.reason, e.planned, e.native_calls) == ("direct", "native", None, True, 0)
+    assert kernel.launches == 0  # explain runs nothing
+    e = B.explain(prepared, torch.randn(8, 8))
+    assert e.run == "general" and "shape (8, 8)" in e.reason and "(16, 8)" in e.reason
+    # Calls that take the fallback are counted by kind, the last in full.
+    prepared(torch.randn(8, 8))
+    prepared(torch.randn(16, 8).double())
+    prepared(torch.randn(16, 8))
+    e = B.explain(prepared, torch.randn(16, 8))
+    assert e.native_calls == 1 and e.run == "native"
+    assert e.refusals == {"a varying argument differs from the prepared one": 2}
+    assert "torch.float64" in e.last_refusal
+    native_switch(False)
+    e = B.explain(prepared, torch.randn(16, 8))
+    assert e.run == "general" and "set_native_call(False)" in e.reason
+    assert "general run" in str(e) and "took the fallback 2 times" in str(e)
+
+
+def test_explain_entry_points_and_other_objects() -> None:
+    import helion_mlir_utils as U
+
+    a, b = torch.randn(64, 32), torch.randn(32, 16)
+    e = B.explain(U.matmul, a, b)
+    assert (e.kernel, e.dispatch, e.run) == ("matmul", "bind", "unsupported")
+    assert "tensors on cpu" in e.reason
+    assert B.explain(U.softmax).reason == "no tensor arguments"
+    e = B.explain(AddRows())
+    assert (e.dispatch, e.run) == ("direct", "native")
+    info = B.explain()  # no kernel: the process report
+    assert {"library", "native_calls", "jit", "output_pool"} <= set(info)
+    with pytest.raises(TypeError, match="not a kernel of this backend"):
+        B.explain(object())
