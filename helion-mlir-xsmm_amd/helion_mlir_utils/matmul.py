@@ -344,6 +344,7 @@ def matmul(
     block_sizes: Sequence[int] | None = None,
     scale: Tensor | None = None,
     shift: Tensor | None = None,
+    *,
     out_dtype: torch.dtype | None = None,
 ) -> Tensor:
     """``epilogue((op(A) @ op(B) + bias) * scale + shift)``, ``op`` transposing
@@ -396,7 +397,7 @@ def matmul(
     )
 
 
-def bmm(a: Tensor, b: Tensor, out_dtype: torch.dtype | None = None, splits: int | None = None) -> Tensor:
+def bmm(a: Tensor, b: Tensor, *, out_dtype: torch.dtype | None = None, splits: int | None = None) -> Tensor:
     """Batched ``A @ B`` (reference ``matmul.py:1965-2006``): one kernel, the
     batch on the grid. f32 runs the f32 MFMA, bf16 the bf16 MFMA with f32
     accumulation and a bf16 result (``out_dtype`` may ask for f32). When the
