@@ -179,6 +179,30 @@ def available() -> bool:
     return library_path().is_file()
 
 
+_load_error: list[str] = []
+
+
+def module() -> ctypes.CDLL | None:
+    """The loaded library, the counterpart of the reference's native extension
+    module (``native/__init__.py:107-127``): ``None`` while native calls are
+    off, or when it cannot be loaded (:func:`load_error` says why). The
+    ``helion_mlir_utils`` entry points do not consult it: they always launch
+    the library's kernels and raise when it is missing."""
+    if not enabled():
+        return None
+    try:
+        return lib()
+    except (OSError, RuntimeError, AttributeError) as exc:
+        if not _load_error:
+            _load_error.append(str(exc))
+        return None
+
+
+def load_error() -> str | None:
+    """Why :func:`module` found no library, if loading it failed."""
+    return _load_error[0] if _load_error else None
+
+
 def last_error() -> str:
     return lib().hmx_last_error().decode(errors="replace")
 

@@ -197,3 +197,13 @@ def test_explain_entry_points_and_other_objects() -> None:
     assert {"library", "native_calls", "jit", "output_pool"} <= set(info)
     with pytest.raises(TypeError, match="not a kernel of this backend"):
         B.explain(object())
+
+
+def test_native_module_and_load_error(native_switch) -> None:
+    # native.module() / load_error() as the reference's tests use them
+    # (``native.module() is None`` to skip): the loaded library, or None
+    # while native calls are off.
+    if native.available():
+        assert native.module() is native.lib() and native.load_error() is None
+    native_switch(False)
+    assert native.module() is None
