@@ -400,6 +400,9 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
   HMX_REQUIRE(valid_dtype(ab_dtype) && valid_dtype(c_dtype), "gemm: unknown dtype");
   HMX_REQUIRE((bias == nullptr && scale == nullptr && shift == nullptr) || valid_dtype(vec_dtype),
               "gemm: unknown vector dtype %d", vec_dtype);
+  // The allocation-free entry point runs kernels compiled at run time only
+  // when an earlier call compiled them.
+  const JitCompileOff no_compile(use_scratch);
   hmx_program prog;
   const int pst = check_epilogue("gemm", epilogue, program, &prog);
   if (pst != HMX_OK) return pst;

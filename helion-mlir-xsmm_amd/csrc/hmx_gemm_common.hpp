@@ -453,6 +453,18 @@ void launch_splitk_reduce(const float* partials, int splits, int64_t batch, cons
 // (HMX_JIT=0) or failed: the caller then launches the interpreter.
 int launch_mi16_jit(const GemmArgs& g, int lb, bool bf16, bool ragged, int bm, int bn, int nw, int stages,
                     dim3 grid, hipStream_t s);
+// While a JitCompileOff lives on a thread, that thread's launches use kernels
+// already compiled but compile and load none (hipRTC and module loading
+// allocate): a kernel not yet compiled is HMX_ERR_UNSUPPORTED, the prebuilt
+// path runs, and a later call may still compile it. For hmx_gemm_noalloc.
+struct JitCompileOff {
+  explicit JitCompileOff(bool on);
+  ~JitCompileOff();
+  JitCompileOff(const JitCompileOff&) = delete;
+  JitCompileOff& operator=(const JitCompileOff&) = delete;
+  bool was;
+  bool on;
+};
 #endif  // __HIPCC_RTC__
 
 }  // namespace hmx

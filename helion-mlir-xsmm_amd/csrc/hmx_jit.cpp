@@ -57,6 +57,8 @@ struct JitStats {
 
 std::mutex g_jit_lock;
 JitStats g_jit_stats;
+// Set by JitCompileOff: this thread may not compile or load kernels.
+thread_local bool t_compile_off = false;
 // Compiled kernels by key; a null function marks a key whose compilation
 // failed (it is not tried again).
 std::map<std::string, hipFunction_t> g_jit_kernels;
@@ -165,11 +167,14 @@ hipFunction_t compile(const std::string& source, int device) {
 }
 
 // The compiled kernel for `key` (compiling `source` on first use), or null
-// when run-time compilation is off or failed. Counts a launch when found.
+// when run-time compilation is off or failed, or the kernel is not compiled
+// yet and this thread may not compile (JitCompileOff). Counts a launch when
+// found.
 hipFunction_t jit_function(const std::string& key, const std::string& source, int device) {
   std::lock_guard<std::mutex> guard(g_jit_lock);
   auto it = g_jit_kernels.find(key);
   if (it == g_jit_kernels.end()) {
+    if (t_compile_off) return nullptr;
     hipFunction_t fn = compile(source, device);
     if (fn) ++g_jit_stats.compiled;
     else ++g_jit_stats.failed;
@@ -207,6 +212,13 @@ int jit_launch(const std::string& key, hipFunction_t fn, dim3 grid, unsigned blo
 }
 
 }  // namespace
+
+JitCompileOff::JitCompileOff(bool on_) : was(t_compile_off), on(on_) {
+  if (on) t_compile_off = true;
+}
+JitCompileOff::~JitCompileOff() {
+  if (on) t_compile_off = was;
+}
 
 bool jit_enabled() {
   const char* e = getenv("HMX_JIT");

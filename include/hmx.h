@@ -6,9 +6,12 @@
  *   - Returns an int status: HMX_OK (0) on success; otherwise
  *     hmx_last_error() holds a message for the calling thread.
  *   - Pointers are device pointers owned by the caller (torch tensors on the
- *     Python side). Nothing is allocated inside: split-K partials go to the
- *     caller's `workspace` (hmx_gemm_noalloc: to the library's static
- *     per-device scratch).
+ *     Python side). No data buffer is allocated inside: split-K partials go
+ *     to the caller's `workspace` (hmx_gemm_noalloc: to the library's static
+ *     per-device scratch). The one exception is code: the first call that
+ *     needs a kernel compiled at run time compiles and loads it (hipRTC,
+ *     hipModuleLoadData), once per process (hmx_jit_info); hmx_gemm_noalloc
+ *     never does, and HMX_JIT=0 turns it off.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream)
  *     and runs asynchronously. Functions keep no mutable global state (only
  *     per-thread error messages and timing events), so they may be called
@@ -259,7 +262,9 @@ int hmx_gemm(int ab_dtype, int c_dtype,
  * launch that needs more workspace than it holds (explicit splits) is
  * refused with HMX_ERR_INVALID. Calls on one device share its scratch, so
  * calls that overlap on one device (other streams, other threads) race:
- * order them on one stream. Results equal hmx_gemm's for the same plan. */
+ * order them on one stream. Results equal hmx_gemm's for the same plan. It
+ * compiles and loads no kernel at run time: an epilogue whose compiled kernel
+ * an earlier call made uses it, any other runs the prebuilt kernels. */
 int hmx_gemm_noalloc(int ab_dtype, int c_dtype,
                      const void* a, int64_t lda, int trans_a,
                      const void* b, int64_t ldb, int b_layout, int64_t b_panel, int64_t b_kpad,

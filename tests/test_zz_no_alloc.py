@@ -156,3 +156,36 @@ def test_noalloc_program_epilogue_past_the_scratch_size(gpu_device) -> None:
         exact = R.matmul(to_np(a[0][rows]), to_np(b[0]), act="silu", out="f32") * 2.0
         assert max_rel_error(to_np(got[0][rows]), exact) < 1e-2
         del a, b, got, ref
+
+
+def test_noalloc_compiles_no_kernel(gpu_device) -> None:
+    # hmx_gemm_noalloc calls nothing that allocates, and compiling or loading
+    # a kernel at run time would: with an epilogue whose kernel no earlier
+    # call compiled it runs the prebuilt kernel (nothing compiled, no compiled
+    # launch), bit-equal to hmx_gemm, which compiles it; once compiled, the
+    # allocation-free entry point launches it too. Whole 256 x 256 tiles, so
+    # both run the 16x16x32 kernel (a program no other test uses).
+    prog = native.Program()
+    prog.count = 3
+    prog.code[0] = native.Instr(native.OP["silu"], 1, 0, 0, 0.0, 0.0)
+    prog.code[1] = native.Instr(native.OP["mul_c"], 2, 1, 0, 1.375, 0.0)
+    prog.code[2] = native.Instr(native.OP["add_c"], 3, 2, 0, 0.125, 0.0)
+    prog.result = 3
+    a, b = _operands(1, 4096, 4096, 256, "bf16", gpu_device)
+    before = native.jit_info()
+    st, got = _gemm(a, b, True, act=native.EPI_PROGRAM, program=prog)
+    assert st == native.OK, native.last_error()
+    after = native.jit_info()
+    assert (after["compiled"], after["launches"]) == (before["compiled"], before["launches"])
+    st, ref = _gemm(a, b, False, act=native.EPI_PROGRAM, program=prog)
+    assert st == native.OK, native.last_error()
+    assert torch.equal(got, ref)
+    compiled = native.jit_info()
+    if compiled["compiled"] > after["compiled"]:  # run-time compilation is on
+        st, again = _gemm(a, b, True, act=native.EPI_PROGRAM, program=prog)
+        assert st == native.OK and torch.equal(again, ref)
+        last = native.jit_info()
+        assert last["compiled"] == compiled["compiled"] and last["launches"] == compiled["launches"] + 1
+    rows = np.arange(0, 4096, 997)
+    exact = R.matmul(to_np(a[0][rows]), to_np(b[0]), act="silu", out="f32") * 1.375 + 0.125
+    assert max_rel_error(to_np(got[0][rows]), exact) < 1e-2
