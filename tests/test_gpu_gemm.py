@@ -609,6 +609,25 @@ def test_matmul_bench_panels(gpu_device, dtype) -> None:
     _check(got, R.matmul(to_np(a), to_np(b), out=dtype), k, to_np(a), to_np(b), dtype)
 
 
+@pytest.mark.parametrize("panel", [32, 64, 128, 256, 512, 768])
+@pytest.mark.parametrize(("n", "k"), [(4096, 64), (4608, 320), (4096, 4096)])
+def test_vnni_relayout_sweep(gpu_device, panel: int, n: int, k: int) -> None:
+    # The 16x16x32 kernel re-lays VNNI panels as they land (4 KiB slabs per K
+    # pair index): panels narrower than, equal to and wider than a tile, tiles
+    # at every offset in a panel, one K stage to 64. At least 256 tiles, so
+    # the product is not split (split-K runs the 32x32 kernel): bit-equal to
+    # the plain B product (the same K walk), and to the oracle on rows of
+    # every tile.
+    m = 4096
+    a = tensor(RNG.uniform(-1, 1, (m, k)).astype(np.float32), "bf16", gpu_device)
+    w = tensor(RNG.uniform(-1, 1, (n, k)).astype(np.float32), "bf16", gpu_device)
+    got = U.matmul_prepacked_b(a, U.pack_b_vnni_t(w, panel), n)
+    assert torch.equal(got, U.matmul(a, w, trans_b=True))
+    rows = tile_rows(RNG, m, 1)
+    an, wn = to_np(a)[rows], to_np(w)
+    _check(to_np(got)[rows], R.matmul(an, wn, False, True, out="bf16"), k, an, wn, "bf16")
+
+
 @pytest.mark.parametrize("panel", [32, 64, 128, 256, 512])
 def test_matmul_prepacked_vnni_whole_tiles(gpu_device, panel) -> None:
     # Whole 256 x 256 tiles with K a multiple of 64: the direct-to-LDS kernel
