@@ -389,59 +389,70 @@ __device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g) {
       }
     }
   } else if constexpr (BF16) {
-    // bf16 C goes through LDS (free once every wave is done with the last
-    // stage) as the whole tile, rows of NROWB bytes whose 16-byte chunk c sits
-    // in slot c ^ (row % 16), then leaves in whole rows: written straight
-    // from the fragments, each store would cover 32-byte pieces of 16 rows.
-    // A lane writes its four columns of a fragment row as one 8-byte word;
-    // the 16 rows x 32 bytes of one LDS write meet distinct banks.
+    // bf16 C leaves through LDS, each wave through its own region of the
+    // stage buffers (free once every wave is done with the last stage): its
+    // WM x WN outputs as rows of PB = 2 WN bytes. Fragment row block by
+    // block, a lane writes its four columns of a row as one 8-byte word, then
+    // the wave reads the block's 16 rows back as 16-byte chunks of whole row
+    // pieces (one 128-byte line each for 256-column tiles) and stores them:
+    // no wave waits for another, and a block's stores overlap the next
+    // block's writes. Written straight from the fragments, each store would
+    // cover 32-byte pieces of 16 rows. Chunk c of region row r sits in slot
+    // c ^ ((r / RPB) % CPW), RPB rows per 256 bytes, so the 16 rows x 32 bytes
+    // of one write and the rows of one read meet distinct banks.
+    constexpr int PB = WN * 2, CPW = PB / 16, RPB = 256 / PB, RPI = 64 / CPW;
+    static_assert(NW * WM * PB <= LDS_BYTES && RPB * PB == 256 && 16 % RPI == 0, "bf16 C regions");
     __syncthreads();
-    auto stage_rows = [&](auto&& finish) {
+    uint8_t* region = lds + wave * (WM * PB);
+    auto slot = [](int r, int c) { return r * PB + ((c ^ ((r / RPB) % CPW)) << 4); };
+    uint16_t* c = (uint16_t*)g.c + off;
+    const int64_t row0 = m0 + wm * WM, col0 = n0 + wn * WN;
+    auto run = [&](auto&& finish) {
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int col4 = col4_of(j);
-        float cb[4] = {0.f, 0.f, 0.f, 0.f}, cs[4] = {1.f, 1.f, 1.f, 1.f}, ch[4] = {0.f, 0.f, 0.f, 0.f};
-        if (affine) vectors4(j, cb, cs, ch);
+      for (int i = 0; i < FM; ++i) {
+        const int r = i * 16 + frow;
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
-          const int r = wm * WM + i * 16 + frow;
+        for (int j = 0; j < FN; ++j) {
           float v[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = finish(acc[i][j][e], cb[e], cs[e], ch[e]);
-          *(uint2*)(lds + r * NROWB + (((col4 >> 3) ^ frow) << 4) + (col4 & 4) * 2) =
+          for (int e = 0; e < 4; ++e) v[e] = finish(acc[i][j][e], j, e);
+          *(uint2*)(region + slot(r, 2 * j + (fg >> 1)) + (fg & 1) * 8) =
               make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        }
+        // The block's rows are read back by other lanes of this wave: the
+        // wave's LDS accesses run in order, and the compiler keeps the reads
+        // after the writes.
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int p = 0; p < 16 / RPI; ++p) {
+          const int rr = i * 16 + p * RPI + lane / CPW, ch = lane % CPW;
+          const uint4 v = *(const uint4*)(region + slot(rr, ch));
+          const int64_t row = row0 + rr, col = col0 + ch * 8;
+          if constexpr (RAGGED) {
+            // Rows past M are not stored; the chunk across N is stored
+            // element by element.
+            if (row < g.m) {
+              if (col + 8 <= g.n) {
+                store_c(c + row * g.ldc + col, v);
+              } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                  if (col + e < g.n) c[row * g.ldc + col + e] = (uint16_t)(dw(v, e >> 1) >> (16 * (e & 1)));
+              }
+            }
+          } else {
+            store_c(c + row * g.ldc + col, v);
+          }
         }
       }
     };
-    if (affine)
-      stage_rows([](float a, float b, float s, float h) { return activate<ACT>((a + b) * s + h); });
-    else
-      stage_rows([](float a, float, float, float) { return activate<ACT>(a); });
-    __syncthreads();
-    // Wave w stores tile rows RW w .. RW w + RW - 1, RPI whole rows per
-    // instruction (16 bytes per lane: two 512-byte or four 256-byte rows).
-    constexpr int RW = BM / NW, CPR = NROWB / 16, RPI = 64 / CPR;
-    uint16_t* c = (uint16_t*)g.c + off;
+    if (affine) {
+      float vb[FN][4], vs[FN][4], vh[FN][4];
 #pragma unroll
-    for (int p = 0; p < RW / RPI; ++p) {
-      const int r = wave * RW + RPI * p + lane / CPR, ch = lane % CPR;
-      const uint4 v = *(const uint4*)(lds + r * NROWB + ((ch ^ (r & 15)) << 4));
-      if constexpr (RAGGED) {
-        // Rows past M are not stored; the chunk across N is stored element
-        // by element.
-        const int64_t row = m0 + r, col = n0 + ch * 8;
-        if (row < g.m) {
-          if (col + 8 <= g.n) {
-            store_c(c + row * g.ldc + col, v);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-              if (col + e < g.n) c[row * g.ldc + col + e] = (uint16_t)(dw(v, e >> 1) >> (16 * (e & 1)));
-          }
-        }
-      } else {
-        store_c(c + (m0 + r) * g.ldc + n0 + ch * 8, v);
-      }
+      for (int j = 0; j < FN; ++j) vectors4(j, vb[j], vs[j], vh[j]);
+      run([&](float a, int j, int e) { return activate<ACT>((a + vb[j][e]) * vs[j][e] + vh[j][e]); });
+    } else {
+      run([](float a, int, int) { return activate<ACT>(a); });
     }
   } else {
     // f32 C straight from the fragments: a lane's four columns of a row are
