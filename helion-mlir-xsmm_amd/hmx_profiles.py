@@ -47,12 +47,35 @@ def _rows(path: Path) -> list[dict]:
         return list(csv.DictReader(f))
 
 
+PASSES = 3  # bench.py's event-armed passes after its timed plain pass (LAUNCH_PASSES)
+
+
+def step_spans(lib: list[dict], per_step: int) -> list[float]:
+    """First kernel start to last kernel end (us) of each step, ``per_step``
+    consecutive library kernels a step."""
+    return [(int(lib[i + per_step - 1]["End_Timestamp"]) - int(lib[i]["Start_Timestamp"])) / 1e3
+            for i in range(0, len(lib) - per_step + 1, per_step)]
+
+
+def pass_means(spans: list[float], steps: int, passes: int = PASSES) -> tuple[list[float], list[float]]:
+    """The steps of the timed plain pass and the means of the ``passes``
+    event-armed passes after it: bench.py ends with the plain pass's
+    ``steps`` steps followed by ``passes`` passes of ``steps`` steps."""
+    tail = spans[-(passes + 1) * steps:]
+    if len(tail) < (passes + 1) * steps:
+        return tail, []
+    plain, armed = tail[:steps], tail[steps:]
+    return plain, [sum(armed[i * steps:(i + 1) * steps]) / steps for i in range(passes)]
+
+
 def trace_summary(workload: str, trace_dir: Path, bench_log: Path, title: str, command: str,
                   steps: int = 20) -> str:
     """The markdown summary of one kernel-trace run: every kernel's calls and
-    durations, and the mean span (first kernel start to last kernel end) of
-    the library kernels of the last ``steps`` steps -- bench.py's second,
-    event-armed pass."""
+    durations; the mean step span (first kernel start to last kernel end) of
+    the library kernels in bench.py's timed plain pass and in each of its
+    event-armed passes, and the lowest pass mean, which is what bench.py
+    reports as ``launch_ms`` (a pass now and then runs every kernel 5-15 %
+    slower than the others)."""
     trace = sorted(_rows(trace_dir / "run_kernel_trace.csv"), key=lambda r: int(r["Start_Timestamp"]))
     stats = _rows(trace_dir / "run_kernel_stats.csv")
     log = bench_log.read_text()
@@ -61,20 +84,24 @@ def trace_summary(workload: str, trace_dir: Path, bench_log: Path, title: str, c
     # kernels per step: the distinct library kernels of the last step's pattern
     names = list(dict.fromkeys(r["Kernel_Name"] for r in lib[-8:]))
     per_step = max(1, len(names))
-    tail = lib[-steps * per_step:]
-    spans = []
-    for i in range(0, len(tail) - per_step + 1, per_step):
-        group = tail[i:i + per_step]
-        spans.append((int(group[-1]["End_Timestamp"]) - int(group[0]["Start_Timestamp"])) / 1e3)
+    spans = step_spans(lib, per_step)
+    plain, armed = pass_means(spans, steps)
     out = [f"# {title}: kernel trace", "", "Command:", "", "```", command, "```", "",
            "| Kernel | Calls | Average (us) | Min (us) | Max (us) | % of GPU time |", "|---|---|---|---|---|---|"]
     for r in stats:
         out.append(f"| `{kernel_name(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
                    f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.1f} |")
     out += ["", "Calls include the warmup and the untimed settle steps bench.py runs before its timed region.", ""]
-    if spans:
-        out.append(f"The last {len(spans)} steps ({per_step} library kernel(s) per step; first kernel start to "
-                   f"last kernel end): mean {sum(spans) / len(spans):.2f} us, min {min(spans):.2f} us per step.")
+    if armed:
+        out.append(f"Step spans ({per_step} library kernel(s) per step; first kernel start to last kernel end): "
+                   f"the timed plain pass of {len(plain)} steps, mean {sum(plain) / len(plain):.2f} us, min "
+                   f"{min(plain):.2f} us; the {len(armed)} event-armed passes after it, means "
+                   + ", ".join(f"{a:.2f}" for a in armed)
+                   + f" us. Kernel time per step (the lowest pass mean, bench.py's launch_ms): {min(armed):.2f} us.")
+        out.append("")
+    elif plain:
+        out.append(f"The last {len(plain)} steps ({per_step} library kernel(s) per step; first kernel start to "
+                   f"last kernel end): mean {sum(plain) / len(plain):.2f} us, min {min(plain):.2f} us per step.")
         out.append("")
     if bench_line:
         out += ["bench.py under the profiler (ms/step: the timed plain pass; ms/launch: the step's kernels, timed "

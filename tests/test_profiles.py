@@ -82,3 +82,48 @@ def test_clock_summary_row(tmp_path: Path) -> None:
     # No K sweep in the root: no window to take off, the clock is the raw ratio.
     assert ("| gemm | `void gemm_bf16_mi16_kernel<1, 0, true, false, 256, 256, 8, 2>(GemmArgs` | 50 | 98.0 | 2.200 | "
             "0.600 | 1.320 | 2.200 |") in text
+
+
+def _trace(root: Path, durations_us: list[float], per_step: int = 1) -> Path:
+    run = root / "kt"
+    run.mkdir(parents=True)
+    with open(run / "run_kernel_trace.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, ["Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        w.writeheader()
+        t = 1_000_000
+        for d in durations_us:
+            for q in range(per_step):
+                end = t + int(round(d * 1e3 / per_step))
+                name = KERNEL if q == 0 else KERNEL.replace("gemm_bf16_mi16_kernel", f"reduce_{q}")
+                w.writerow({"Kernel_Name": name, "Start_Timestamp": t, "End_Timestamp": end})
+                t = end
+            t += 9000
+    with open(run / "run_kernel_stats.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, ["Name", "Calls", "AverageNs", "MinNs", "MaxNs", "Percentage"])
+        w.writeheader()
+        w.writerow({"Name": KERNEL, "Calls": len(durations_us), "AverageNs": 1e5, "MinNs": 9e4, "MaxNs": 1.1e5,
+                    "Percentage": 100.0})
+    (root / "bench.log").write_text("bench: gemm 0.0990 ms/step 1388.3 TFLOP/s, 0.0960 ms/launch\n")
+    return run
+
+
+def test_pass_means_split_the_tail() -> None:
+    # settle steps, then the plain pass (20 x 96), then passes at 95, 110, 94
+    spans = [120.0] * 7 + [96.0] * 20 + [95.0] * 20 + [110.0] * 20 + [94.0] * 20
+    plain, armed = P.pass_means(spans, 20)
+    assert plain == [96.0] * 20
+    assert armed == pytest.approx([95.0, 110.0, 94.0])
+    assert P.pass_means(spans[-30:], 20) == (spans[-30:], [])
+
+
+def test_trace_summary_reports_the_lowest_pass(tmp_path: Path) -> None:
+    # one slow pass (the second) must not set the kernel time; two kernels a
+    # step are one span from the first's start to the second's end
+    durations = [130.0] * 5 + [96.0] * 20 + [95.0] * 20 + [112.0] * 20 + [94.5] * 20
+    run = _trace(tmp_path, durations, per_step=2)
+    spans = P.step_spans(P._rows(run / "run_kernel_trace.csv"), 2)
+    assert spans == pytest.approx(durations, abs=1e-3)
+    text = P.trace_summary("gemm", run, tmp_path / "bench.log", "T", "cmd")
+    assert "means 95.00, 112.00, 94.50 us" in text
+    assert "(the lowest pass mean, bench.py's launch_ms): 94.50 us" in text
+    assert "mean 96.00 us, min 96.00 us" in text
