@@ -133,6 +133,25 @@ def test_matmul_ragged_direct_to_lds(gpu_device, mnk, trans_b, act, out_dtype, t
     _check(to_np(got), ref, k, to_np(a), to_np(b), "bf16")
 
 
+@pytest.mark.parametrize(("m", "n", "k"), [(1900, 2000, 1024), (2000, 1960, 2048)])
+@pytest.mark.parametrize(("act", "out_dtype"), [("identity", torch.bfloat16), ("silu", torch.bfloat16),
+                                                ("relu", torch.float32)])
+def test_matmul_ragged_128_tiles_one_round(gpu_device, m, n, k, act, out_dtype) -> None:
+    # Ragged 128 x 128 tiles, one round (at most a tile per CU), 16 or more K
+    # stages and no split: the 16x16x32 kernel with four LDS stages, bf16 C
+    # leaving through each wave's own staging region (C rows of N = 2000 or
+    # 1960 bf16 are 16-byte aligned, which that kernel needs for bf16 C).
+    plan = U.gemm_plan(torch.bfloat16, m, n, k, trans_b=True, block_sizes=(128, 128, 64))
+    assert plan["splits"] <= 1 and (plan["tile_m"], plan["tile_n"]) == (128, 128)
+    assert -(-m // 128) * -(-n // 128) <= 256
+    a, b = _operands(m, n, k, False, True, "bf16", gpu_device, 0.3)
+    bias = tensor(RNG.normal(0, 1, n).astype(np.float32), "bf16", gpu_device)
+    got = U.matmul(a, b, trans_b=True, bias=bias, epilogue=ACTS[act], out_dtype=out_dtype, block_sizes=(128, 128, 64))
+    out = "bf16" if out_dtype == torch.bfloat16 else "f32"
+    ref = R.matmul(to_np(a), to_np(b), False, True, to_np(bias), act=act, out=out)
+    _check(to_np(got), ref, k, to_np(a), to_np(b), "bf16")
+
+
 @pytest.mark.parametrize("trans_b", [False, True])
 def test_matmul_ragged_large(gpu_device, trans_b) -> None:
     # 16 x 16 tiles of 256 x 256, the last row and column of tiles ragged
