@@ -266,7 +266,7 @@ class Linear(Workload):
         self.work = 2.0 * 8192 * 11008 * 4096
         self.dtype = "bf16"
         # 256x256 tiles over the first 10240 columns (five rounds), then 256x128 tiles over the last 768.
-        self.kernel = "gemm_bf16_mi16_kernel (256x256 head, then the 256x128 tail)"
+        self.kernel = "gemm_bf16_mi16_rounds_kernel (256x256 rounds and the 256x128 tail, one launch)"
         self.config = {"workload": self.description, "m": 8192, "n": 11008, "k": 4096, "seed": 3}
 
     def step(self):

@@ -601,7 +601,6 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
         GemmArgs head = g;
         head.n = n1 * 256;
         head.tiles_n = (int)n1;
-        launch_gemm_bf16_dma(head, lb_run, dim3((unsigned)(tiles_m * n1), 1, 1), s);
         // The rest: B rows, C columns and the column vectors from n1 * 256 on.
         const int64_t off = n1 * 256;
         GemmArgs rest = g;
@@ -616,7 +615,11 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
         if (g.bias) rest.bias = (const char*)g.bias + vb;
         if (g.scale) rest.scale = (const char*)g.scale + vb;
         if (g.shift) rest.shift = (const char*)g.shift + vb;
-        launch_gemm_bf16_dma_narrow(rest, lb_run, dim3((unsigned)(tiles_m * rest.tiles_n), 1, 1), s);
+        const unsigned head_blocks = (unsigned)(tiles_m * n1), rest_blocks = (unsigned)(tiles_m * rest.tiles_n);
+        if (!launch_gemm_bf16_dma_rounds(head, rest, lb_run, head_blocks, rest_blocks, s)) {
+          launch_gemm_bf16_dma(head, lb_run, dim3(head_blocks, 1, 1), s);
+          launch_gemm_bf16_dma_narrow(rest, lb_run, dim3(rest_blocks, 1, 1), s);
+        }
       } else {
         launch_gemm_bf16_dma(g, lb_run, grid, s);
       }

@@ -108,10 +108,11 @@ struct GemmArgs {
 // contiguous range, then walking that range in groups of kGroupM tile rows,
 // makes the tiles that share A rows and B columns run on the same XCD and its
 // L2.
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int xcds, int& tm, int& tn) {
+// `bid` is the workgroup's index in the launch's run of this tile grid (a run
+// starting at a multiple of xcds, so that bid % xcds is still its XCD).
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int xcds, int& tm, int& tn) {
   constexpr int kGroupM = 4;
   const int nb = tiles_m * tiles_n;
-  int bid = blockIdx.x;
   if (xcds > 1 && nb % xcds == 0) bid = (bid % xcds) * (nb / xcds) + bid / xcds;
   const int per_group = kGroupM * tiles_n;
   const int group = bid / per_group;
@@ -120,6 +121,10 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int xcds, 
   const int in_group = bid % per_group;
   tm = first_m + in_group % gm;
   tn = in_group / gm;
+}
+
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int xcds, int& tm, int& tn) {
+  tile_coords((int)blockIdx.x, tiles_m, tiles_n, xcds, tm, tn);
 }
 
 __device__ __forceinline__ void column_vectors(const GemmArgs& g, int64_t col, bool in,
@@ -422,6 +427,13 @@ void launch_gemm_bf16_dma(const GemmArgs& g, int lb, dim3 grid, hipStream_t s);
 // The 64-wide direct-to-LDS kernel on 256 x 128 tiles (four waves, B
 // [N, K] or [K, N]): the columns past the last whole round of 256 x 256 tiles.
 void launch_gemm_bf16_dma_narrow(const GemmArgs& g, int lb, dim3 grid, hipStream_t s);
+// Both in one launch where the 16x16x32 kernel runs both with a named
+// activation: workgroups 0 .. head_blocks - 1 take head's 256 x 256 tiles,
+// the rest rest's 256 x 128 tiles, so the tail's workgroups start as the last
+// round's free their CUs, with no kernel boundary between. False (nothing
+// launched) where it does not apply.
+bool launch_gemm_bf16_dma_rounds(const GemmArgs& head, const GemmArgs& rest, int lb, unsigned head_blocks,
+                                 unsigned rest_blocks, hipStream_t s);
 // The 64-wide direct-to-LDS kernel with A stored [K, M] (trans_a): whole
 // 256 x 256 tiles, K chunks of whole 64-element stages, B K-contiguous or
 // row-major.

@@ -552,6 +552,23 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_bf16_mi16_kernel(GemmArgs g) 
   gemm_bf16_mi16_body<LB, ACT, BF16, RAGGED, BM, BN, NW, S>(g);
 }
 
+// A product of several rounds of 256 x 256 tiles and a tail of 256 x 128
+// tiles in one launch: workgroup b < head_blocks runs head's tile b, the
+// others rest's tile b - head_blocks (head_blocks a multiple of the XCD
+// count, so the XCD-aware tile order holds for both). Both are multi-round,
+// so C is streamed.
+template <int LB, int ACT, bool BF16>
+__global__ __launch_bounds__(512, 1) void gemm_bf16_mi16_rounds_kernel(GemmArgs head, GemmArgs rest,
+                                                                        int head_blocks) {
+  constexpr int kHead = mi16_lds_bytes<ACT, 256, 256, 8, 2>(), kTail = mi16_lds_bytes<ACT, 256, 128, 8, 2>();
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kHead > kTail ? kHead : kTail];
+  const int b = (int)blockIdx.x;
+  if (b < head_blocks)
+    gemm_bf16_mi16_body<LB, ACT, BF16, false, 256, 256, 8, 2>(head, lds, b, false);
+  else
+    gemm_bf16_mi16_body<LB, ACT, BF16, false, 256, 128, 8, 2>(rest, lds, b - head_blocks, false);
+}
+
 // ---------------------------------------------------------------------------
 // f32 direct-to-LDS kernel (v_mfma_f32_32x32x2_f32) for whole 256 x 256 tiles
 // of long-K split-K products: row-major A, B [N, K] or [K, N], f32 partials
@@ -1058,6 +1075,48 @@ void launch_bf16_dma_narrow(const GemmArgs& g, dim3 grid, hipStream_t s) {
         else launch(gemm_bf16_dma64_kernel<LB, ACT_ANY, BF16, 4, 128>, grid, 256, s, g);
         break;
   }
+}
+
+// One launch for the whole rounds and the tail unless the environment sets
+// HMX_GEMM_FUSED_ROUNDS=0 (two launches, for comparison).
+bool fused_rounds_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("HMX_GEMM_FUSED_ROUNDS");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
+bool launch_gemm_bf16_dma_rounds(const GemmArgs& head, const GemmArgs& rest, int lb, unsigned head_blocks,
+                                 unsigned rest_blocks, hipStream_t s) {
+  // The conditions under which launch_gemm_bf16_dma and _narrow both take the
+  // 16x16x32 kernel with a named activation.
+  const bool k64 = head.k_chunk % 64 == 0 && head.k % 64 == 0 && dma64_enabled();
+  const bool named = head.act == HMX_EPI_IDENTITY || head.act == HMX_EPI_RELU || head.act == HMX_EPI_SILU;
+  if (!fused_rounds_enabled() || !k64 || !eight_waves() || !named || !mi16_args_ok(head) || !mi16_args_ok(rest) ||
+      (lb != L_KCONTIG && lb != L_RCONTIG) || head_blocks % (unsigned)std::max(head.xcds, 1) != 0 ||
+      head.m % 256 != 0 || head.n % 256 != 0)
+    return false;
+  const dim3 grid(head_blocks + rest_blocks);
+  const int hb = (int)head_blocks;
+  auto go = [&](auto lb_c, auto bf16_c) {
+    constexpr int LBc = decltype(lb_c)::value;
+    constexpr bool BF = decltype(bf16_c)::value;
+    switch (head.act) {
+      case HMX_EPI_RELU: launch(gemm_bf16_mi16_rounds_kernel<LBc, ACT_RELU, BF>, grid, 512, s, head, rest, hb); break;
+      case HMX_EPI_SILU: launch(gemm_bf16_mi16_rounds_kernel<LBc, ACT_SILU, BF>, grid, 512, s, head, rest, hb); break;
+      default: launch(gemm_bf16_mi16_rounds_kernel<LBc, ACT_ID, BF>, grid, 512, s, head, rest, hb); break;
+    }
+  };
+  const bool bf16 = head.c_dtype == HMX_DTYPE_BF16;
+  if (lb == L_RCONTIG) {
+    if (bf16) go(std::integral_constant<int, L_RCONTIG>{}, std::true_type{});
+    else go(std::integral_constant<int, L_RCONTIG>{}, std::false_type{});
+  } else {
+    if (bf16) go(std::integral_constant<int, L_KCONTIG>{}, std::true_type{});
+    else go(std::integral_constant<int, L_KCONTIG>{}, std::false_type{});
+  }
+  return true;
 }
 
 void launch_gemm_bf16_dma_narrow(const GemmArgs& g, int lb, dim3 grid, hipStream_t s) {

@@ -36,8 +36,21 @@ namespace {
 // S stages in LDS (4 for 128 x 128 tiles that run one workgroup per CU):
 // the loads issued in stage t are stage t + S's, so S - 1 stages are in
 // flight while one is read; the barrier waits only for stage t + 1.
+// LDS bytes of the body for these parameters: S stages of the A and B tiles,
+// or the staged epilogue's f32 rows where that is larger.
+template <int ACT, int BM, int BN, int NW, int S>
+constexpr int mi16_lds_bytes() {
+  constexpr int stage = BM * 64 * 2 + BN * 64 * 2;
+  constexpr int wm = BM / 2, wn = BN / (NW / 2);
+  constexpr int epi = NW * (wm / 2) * (wn * 4 + 16);
+  return staged_act(ACT) && epi > S * stage ? epi : S * stage;
+}
+
+// The body on tile `bid` of g's grid, with `lds` (mi16_lds_bytes, 1 KiB
+// aligned) as its LDS; `through`: C is written through to memory (a grid of
+// one round).
 template <int LB, int ACT, bool BF16, bool RAGGED = false, int BM = 256, int BN = 256, int NW = 8, int S = 2>
-__device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g) {
+__device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g, uint8_t* lds, int bid, bool through) {
   static_assert(LB == L_KCONTIG || LB == L_RCONTIG || LB == L_VNNI_PANELS || LB == L_PANELS || LB == L_BLOCKED,
                 "B [N, K], [K, N], VNNI panels, K-major panels or 32 x 32 blocks");
   static_assert(ACT == ACT_ID || ACT == ACT_RELU || ACT == ACT_SILU || ACT == ACT_JIT || staged_act(ACT),
@@ -69,13 +82,11 @@ __device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g) {
   constexpr int BAR = NS, LOAD_END = SLOTS - NF;                         // 32, 52 (16, 24)
   // ACT_ANY stages each wave's 64-row halves as f32, rows of WN * 4 + 16
   // bytes: 8 x 64 x 272 bytes, a little more than the stages.
-  constexpr int EPI_BYTES = NW * (WM / 2) * (WN * 4 + 16);
-  constexpr int LDS_BYTES = staged_act(ACT) && EPI_BYTES > S * STAGE ? EPI_BYTES : S * STAGE;
+  constexpr int LDS_BYTES = mi16_lds_bytes<ACT, BM, BN, NW, S>();
   static_assert(LDS_BYTES <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
 
   int tm, tn;
-  tile_coords(g.tiles_m, g.tiles_n, g.xcds, tm, tn);
+  tile_coords(bid, g.tiles_m, g.tiles_n, g.xcds, tm, tn);
   const int split = blockIdx.y, batch = blockIdx.z;
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int64_t k_begin = (int64_t)split * g.k_chunk;
@@ -324,13 +335,13 @@ __device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g) {
   auto vectors4 = [&](int j, float (&cb)[4], float (&cs)[4], float (&ch)[4]) {
     column_vectors4(g, n0 + col4_of(j), g.n, cb, cs, ch);
   };
-  // When the grid is one round (a workgroup per CU at most), C is written
-  // through to memory: the kernel then ends with few dirty L2 lines to write
-  // back (an f32 C of 4096 x 4096 finishes 5-6% sooner). With more rounds the
-  // streaming stores are kept: a workgroup retires only once its stores are
-  // acknowledged, and written-through stores are acknowledged later, which
-  // delays the next round's workgroups (~5% slower at 1376 tiles).
-  const bool through = gridDim.x * gridDim.y * gridDim.z <= (unsigned)g.cus;
+  // `through` (the grid is one round, a workgroup per CU at most): C is
+  // written through to memory, so the kernel ends with few dirty L2 lines to
+  // write back (an f32 C of 4096 x 4096 finishes 5-6% sooner). With more
+  // rounds the streaming stores are kept: a workgroup retires only once its
+  // stores are acknowledged, and written-through stores are acknowledged
+  // later, which delays the next round's workgroups (~5% slower at 1376
+  // tiles).
   auto store_c = [&](void* p, const uint4& v) {
     if (through) store16_through(p, v);
     else store16_stream(p, v);
@@ -483,6 +494,15 @@ __device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g) {
       }
     }
   }
+}
+
+// The body as a kernel of its own: the workgroup's tile is blockIdx.x, and C
+// is written through when the grid is one round.
+template <int LB, int ACT, bool BF16, bool RAGGED = false, int BM = 256, int BN = 256, int NW = 8, int S = 2>
+__device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[mi16_lds_bytes<ACT, BM, BN, NW, S>()];
+  gemm_bf16_mi16_body<LB, ACT, BF16, RAGGED, BM, BN, NW, S>(
+      g, lds, (int)blockIdx.x, gridDim.x * gridDim.y * gridDim.z <= (unsigned)g.cus);
 }
 
 }  // namespace

@@ -418,11 +418,13 @@ def test_linear_config4_silu(gpu_device) -> None:
 
 @pytest.mark.parametrize(
     ("m", "n", "k", "trans_b", "vectors"),
-    [(8192, 11008, 4096, True, "bias"), (4096, 8192, 256, False, "none"), (3072, 6144, 128, True, "all_f32")],
+    [(8192, 11008, 4096, True, "bias"), (4096, 8192, 256, False, "none"), (3072, 6144, 128, True, "all_f32"),
+     (4096, 4608, 512, False, "all_f32")],
 )
 def test_multi_round_tiles_match_single_rounds(gpu_device, m, n, k, trans_b, vectors) -> None:
-    # More 256 x 256 tiles than CUs (several rounds; config 4 first, whose
-    # last round is the 256 x 128 tail launch) against blocks of 1024 rows,
+    # More 256 x 256 tiles than CUs (several rounds; config 4 first, and
+    # 4096 x 4608 with row-major B, both whole rounds of 256 x 256 tiles and a
+    # tail of 256 x 128 tiles in one launch) against blocks of 1024 rows,
     # each a single round of one workgroup per tile. Each output is the same
     # K walk in either, so the results are equal bit for bit; bias, scale and
     # shift in bf16 and f32 take the epilogue's 8- and 16-byte loads.
