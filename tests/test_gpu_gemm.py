@@ -416,6 +416,25 @@ def test_linear_config4_silu(gpu_device) -> None:
     _check(got, ref, 4096, xn, wn, "bf16")
 
 
+@pytest.mark.parametrize(("trans_b", "act"), [(True, "relu"), (False, "identity")])
+def test_rounds_and_tail_f32_out(gpu_device, trans_b, act) -> None:
+    # Whole rounds of 256 x 256 tiles and a 256 x 128 tail in one launch, f32
+    # C: equal bit for bit to single rounds of 1024-row blocks, and to the
+    # oracle on rows of every tile.
+    m, n, k = 4096, 4608, 256
+    a = tensor(RNG.uniform(-1, 1, (m, k)).astype(np.float32), "bf16", gpu_device)
+    b = tensor(RNG.uniform(-1, 1, (n, k) if trans_b else (k, n)).astype(np.float32), "bf16", gpu_device)
+    bias = torch.randn(n, device=gpu_device, dtype=torch.float32)
+    kw = {"bias": bias, "epilogue": ACTS[act], "out_dtype": torch.float32}
+    full = U.matmul(a, b, trans_b=trans_b, **kw)
+    blocks = torch.cat([U.matmul(a[r:r + 1024], b, trans_b=trans_b, **kw) for r in range(0, m, 1024)])
+    assert full.dtype == torch.float32 and torch.equal(full, blocks)
+    rows = torch.from_numpy(tile_rows(RNG, m, 1))
+    an, bn = to_np(a[rows.to(gpu_device)]), to_np(b)
+    ref = R.matmul(an, bn, False, trans_b, to_np(bias), act=act, out="f32")
+    _check(to_np(full[rows.to(gpu_device)]), ref, k, an, bn, "bf16")
+
+
 @pytest.mark.parametrize(
     ("m", "n", "k", "trans_b", "vectors"),
     [(8192, 11008, 4096, True, "bias"), (4096, 8192, 256, False, "none"), (3072, 6144, 128, True, "all_f32"),
