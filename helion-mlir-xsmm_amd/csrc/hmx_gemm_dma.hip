@@ -1079,7 +1079,7 @@ void launch_bf16_dma_narrow(const GemmArgs& g, dim3 grid, hipStream_t s) {
 
 // One launch for the whole rounds and the tail unless the environment sets
 // HMX_GEMM_FUSED_ROUNDS=0 (two launches, for comparison).
-bool fused_rounds_enabled() {
+static bool fused_rounds_enabled() {
   static const bool on = [] {
     const char* e = getenv("HMX_GEMM_FUSED_ROUNDS");
     return !(e && e[0] == '0');
