@@ -35,6 +35,7 @@ OMP_NUM_THREADS) on a bounded sample of the workload, with the CPU oracle
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 from pathlib import Path
@@ -641,6 +642,22 @@ LAUNCH_PASSES = 3
 
 
 def measure(w: Workload, steps: int, warmup: int) -> dict:
+    """:func:`_measure` with Python's cyclic garbage collector paused, as
+    ``timeit`` does: a full collection in the middle of a pass stalls the host
+    for tens of milliseconds (39 ms seen between two launches of the pre-packed
+    GEMM), the GPU idles meanwhile, and the passes after it run at the lower
+    clock it comes back from."""
+    gc.collect()
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        return _measure(w, steps, warmup)
+    finally:
+        if was:
+            gc.enable()
+
+
+def _measure(w: Workload, steps: int, warmup: int) -> dict:
     """Step time (ms) over ``steps`` timed steps, and the average duration of
     one step's kernels, both from HIP events on the stream the library
     launches on (torch's current stream).
