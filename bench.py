@@ -349,7 +349,9 @@ class RowOp(Workload):
         self.unit, self.bound, self.peak = "GB/s", "hbm", PEAK_HBM_GBS
         self.work = 2.0 * m * n * esz + (n * esz if op == "rmsnorm" else 0)  # one read + one write
         self.dtype = dtype_name
-        self.kernel = "softmax_cached" if op == "softmax" else "rmsnorm_cached"
+        # bf16 RMSNorm rows run two to a workgroup (rmsnorm_cached2).
+        self.kernel = ("softmax_cached" if op == "softmax"
+                       else "rmsnorm_cached2" if dtype_name == "bf16" else "rmsnorm_cached")
         self.config = {"workload": self.description, "m": m, "n": n, "seed": 1, "values": "N(0, std 2)"}
         if op == "rmsnorm":
             self.config["eps"] = self.eps
