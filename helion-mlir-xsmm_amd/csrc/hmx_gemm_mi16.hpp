@@ -291,7 +291,13 @@ __device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g, uint8_t* 
 #pragma unroll
   for (int j = 0; j < FN; ++j) fb[0][j] = b_read(0, 0, j);
 
-  for (int t = 0; t < ktiles; ++t) {
+  // One K stage. LOADS_C: the stage issues stage t + S's loads. With two
+  // stages the last two issue none (the barrier's wait is for every load,
+  // vmcnt 0), in a copy of the stage without them rather than behind a branch
+  // per load; with four the barrier counts on S - 2 stages of loads behind
+  // the next, which clamped reloads of the last stage keep.
+  auto stage = [&](int t, auto loads_c) {
+    constexpr bool LOADS_C = decltype(loads_c)::value;
     const int cur = t & (S - 1), nxt = (t + 1) & (S - 1);
 #pragma unroll
     for (int x = 0; x < SLOTS; ++x) {
@@ -307,7 +313,7 @@ __device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g, uint8_t* 
       // next stage's fragment reads.
 #pragma unroll
       for (int q = (x - BAR) * LOADS / (LOAD_END - BAR); q < (x + 1 - BAR) * LOADS / (LOAD_END - BAR); ++q)
-        if (x >= BAR && x < LOAD_END) dma(t + S, q);
+        if (LOADS_C && x >= BAR && x < LOAD_END) dma(t + S, q);
       if (x >= SLOTS - NF) {
         const int f = x - (SLOTS - NF);
         if (f < FM) fa[0][f] = a_read(nxt, 0, f);
@@ -319,6 +325,13 @@ __device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g, uint8_t* 
       acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
+  };
+  if constexpr (S == 2) {
+    int t = 0;
+    for (; t < ktiles - S; ++t) stage(t, std::true_type{});
+    for (; t < ktiles; ++t) stage(t, std::false_type{});
+  } else {
+    for (int t = 0; t < ktiles; ++t) stage(t, std::true_type{});
   }
   wait_vmem<0>();  // no load into LDS outlives the loop
 
