@@ -438,7 +438,7 @@ def test_rounds_and_tail_f32_out(gpu_device, trans_b, act) -> None:
 @pytest.mark.parametrize(
     ("m", "n", "k", "trans_b", "vectors"),
     [(8192, 11008, 4096, True, "bias"), (4096, 8192, 256, False, "none"), (3072, 6144, 128, True, "all_f32"),
-     (4096, 4608, 512, False, "all_f32")],
+     (4096, 4608, 512, False, "all_f32"), (4096, 4352, 128, True, "bias"), (8192, 8448, 64, False, "none")],
 )
 def test_multi_round_tiles_match_single_rounds(gpu_device, m, n, k, trans_b, vectors) -> None:
     # More 256 x 256 tiles than CUs (several rounds; config 4 first, and
