@@ -465,6 +465,11 @@ void launch_splitk_reduce(const float* partials, int splits, int64_t batch, cons
 // (HMX_JIT=0) or failed: the caller then launches the interpreter.
 int launch_mi16_jit(const GemmArgs& g, int lb, bool bf16, bool ragged, int bm, int bn, int nw, int stages,
                     dim3 grid, hipStream_t s);
+// hmx_jit.cpp: launch_gemm_bf16_dma_rounds's one launch of whole rounds of
+// 256 x 256 tiles (head) and the 256 x 128 tail (rest) with g's epilogue
+// compiled in at run time; HMX_OK or HMX_ERR_UNSUPPORTED as launch_mi16_jit.
+int launch_mi16_rounds_jit(const GemmArgs& head, const GemmArgs& rest, int lb, bool bf16, unsigned head_blocks,
+                           unsigned rest_blocks, hipStream_t stream);
 // While a JitCompileOff lives on a thread, that thread's launches use kernels
 // already compiled but compile and load none (hipRTC and module loading
 // allocate): a kernel not yet compiled is HMX_ERR_UNSUPPORTED, the prebuilt

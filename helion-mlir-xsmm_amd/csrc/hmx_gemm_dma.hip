@@ -1093,10 +1093,15 @@ bool launch_gemm_bf16_dma_rounds(const GemmArgs& head, const GemmArgs& rest, int
   // 16x16x32 kernel with a named activation.
   const bool k64 = head.k_chunk % 64 == 0 && head.k % 64 == 0 && dma64_enabled();
   const bool named = head.act == HMX_EPI_IDENTITY || head.act == HMX_EPI_RELU || head.act == HMX_EPI_SILU;
-  if (!fused_rounds_enabled() || !k64 || !eight_waves() || !named || !mi16_args_ok(head) || !mi16_args_ok(rest) ||
+  if (!fused_rounds_enabled() || !k64 || !eight_waves() || !mi16_args_ok(head) || !mi16_args_ok(rest) ||
       (lb != L_KCONTIG && lb != L_RCONTIG) || head_blocks % (unsigned)std::max(head.xcds, 1) != 0 ||
       head.m % 256 != 0 || head.n % 256 != 0)
     return false;
+  // Other epilogues (programs, the other activations): the same launch with
+  // the epilogue compiled in, where run-time compilation is on.
+  if (!named)
+    return launch_mi16_rounds_jit(head, rest, lb, head.c_dtype == HMX_DTYPE_BF16, head_blocks, rest_blocks, s) ==
+           HMX_OK;
   const dim3 grid(head_blocks + rest_blocks);
   const int hb = (int)head_blocks;
   auto go = [&](auto lb_c, auto bf16_c) {

@@ -246,6 +246,30 @@ int launch_mi16_jit(const GemmArgs& g, int lb, bool bf16, bool ragged, int bm, i
   return jit_launch(key, fn, grid, (unsigned)nw * 64, params, stream, "gemm");
 }
 
+int launch_mi16_rounds_jit(const GemmArgs& head, const GemmArgs& rest, int lb, bool bf16, unsigned head_blocks,
+                           unsigned rest_blocks, hipStream_t stream) {
+  if (!jit_enabled()) return HMX_ERR_UNSUPPORTED;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return HMX_ERR_UNSUPPORTED;
+  const std::string tmpl = std::to_string(lb) + ", hmx::ACT_JIT, " + (bf16 ? "true" : "false") + ", false";
+  const std::string key = std::to_string(device) + "|gemm_rounds|" + std::to_string(lb) + "," +
+                          (bf16 ? "bf16" : "f32") + "|" + epilogue_key(head.act, head.act_arg, head.prog);
+  const std::string source =
+      "#include \"hmx_gemm_mi16.hpp\"\n" + epilogue_source(head.act, head.act_arg, head.prog) +
+      "extern \"C\" __global__ __launch_bounds__(512, 1) void hmx_jit_kernel(hmx::GemmArgs head, "
+      "hmx::GemmArgs rest, int head_blocks) {\n"
+      "  __shared__ __attribute__((aligned(1024))) uint8_t lds[hmx::mi16_lds_bytes<hmx::ACT_JIT, 256, 256, 8, 2>()];\n"
+      "  const int b = (int)blockIdx.x;\n"
+      "  if (b < head_blocks) hmx::gemm_bf16_mi16_body<" + tmpl + ", 256, 256, 8, 2>(head, lds, b, false);\n"
+      "  else hmx::gemm_bf16_mi16_body<" + tmpl + ", 256, 128, 8, 2>(rest, lds, b - head_blocks, false);\n}\n";
+  hipFunction_t fn = jit_function(key, source, device);
+  if (!fn) return HMX_ERR_UNSUPPORTED;
+  GemmArgs h = head, r = rest;
+  int hb = (int)head_blocks;
+  void* params[] = {&h, &r, &hb};
+  return jit_launch(key, fn, dim3(head_blocks + rest_blocks), 512u, params, stream, "gemm");
+}
+
 int launch_group_norm_jit(bool bf16, const void* x, void* y, const GroupNormArgs& a, int64_t rows, int tpr,
                           int gv, int epv, int vpl, bool one, bool extra, unsigned block, int rows_per_block,
                           int cus, hipStream_t stream) {
