@@ -1090,7 +1090,8 @@ static bool fused_rounds_enabled() {
 bool launch_gemm_bf16_dma_rounds(const GemmArgs& head, const GemmArgs& rest, int lb, unsigned head_blocks,
                                  unsigned rest_blocks, hipStream_t s) {
   // The conditions under which launch_gemm_bf16_dma and _narrow both take the
-  // 16x16x32 kernel with a named activation.
+  // 16x16x32 kernel (its prebuilt named activations, or any other epilogue
+  // compiled in at run time).
   const bool k64 = head.k_chunk % 64 == 0 && head.k % 64 == 0 && dma64_enabled();
   const bool named = head.act == HMX_EPI_IDENTITY || head.act == HMX_EPI_RELU || head.act == HMX_EPI_SILU;
   if (!fused_rounds_enabled() || !k64 || !eight_waves() || !mi16_args_ok(head) || !mi16_args_ok(rest) ||
