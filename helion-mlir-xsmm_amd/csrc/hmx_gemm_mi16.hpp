@@ -296,16 +296,14 @@ __device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g, uint8_t* 
   // vmcnt 0), in a copy of the stage without them rather than behind a branch
   // per load; with four the barrier counts on S - 2 stages of loads behind
   // the next, which clamped reloads of the last stage keep.
-  // LAST_C (the last stage): no barrier, which would only publish a stage
-  // t + 1 there is none of, and no reads of its fragments.
-  auto stage = [&](int t, auto loads_c, auto last_c) {
-    constexpr bool LOADS_C = decltype(loads_c)::value, LAST_C = decltype(last_c)::value;
+  auto stage = [&](int t, auto loads_c) {
+    constexpr bool LOADS_C = decltype(loads_c)::value;
     const int cur = t & (S - 1), nxt = (t + 1) & (S - 1);
 #pragma unroll
     for (int x = 0; x < SLOTS; ++x) {
       __builtin_amdgcn_sched_barrier(0);
       const int ks = x / NS, sub = x % NS;
-      if (x == BAR && !LAST_C)
+      if (x == BAR)
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(LOADS * (S - 2)) : "memory");
       if (ks == 0 && sub < NF) {
         if (sub < FM) fa[1][sub] = a_read(cur, 1, sub);
@@ -316,7 +314,7 @@ __device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g, uint8_t* 
 #pragma unroll
       for (int q = (x - BAR) * LOADS / (LOAD_END - BAR); q < (x + 1 - BAR) * LOADS / (LOAD_END - BAR); ++q)
         if (LOADS_C && x >= BAR && x < LOAD_END) dma(t + S, q);
-      if (!LAST_C && x >= SLOTS - NF) {
+      if (x >= SLOTS - NF) {
         const int f = x - (SLOTS - NF);
         if (f < FM) fa[0][f] = a_read(nxt, 0, f);
         else fb[0][f - FM] = b_read(nxt, 0, f - FM);
@@ -330,14 +328,10 @@ __device__ __forceinline__ void gemm_bf16_mi16_body(const GemmArgs& g, uint8_t* 
   };
   if constexpr (S == 2) {
     int t = 0;
-    for (; t < ktiles - S; ++t) stage(t, std::true_type{}, std::false_type{});
-    for (; t < ktiles - 1; ++t) stage(t, std::false_type{}, std::false_type{});
-    stage(ktiles - 1, std::false_type{}, std::true_type{});
+    for (; t < ktiles - S; ++t) stage(t, std::true_type{});
+    for (; t < ktiles; ++t) stage(t, std::false_type{});
   } else {
-    // (The last stage's loads would go into the buffer other waves may still
-    // be reading, with no barrier before them: it issues none.)
-    for (int t = 0; t < ktiles - 1; ++t) stage(t, std::true_type{}, std::false_type{});
-    stage(ktiles - 1, std::false_type{}, std::true_type{});
+    for (int t = 0; t < ktiles; ++t) stage(t, std::true_type{});
   }
   wait_vmem<0>();  // no load into LDS outlives the loop
 
