@@ -439,6 +439,51 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
   make_plan(ab_dtype, m, n, k, batch, trans_a, b_layout, splits,
             use_scratch ? kScratchBytes : (workspace ? workspace_bytes : 0), tile_m, tile_n, tile_k, dev.cus,
             epilogue, plan);
+  // A K-contiguous operand (row-major A, B [N, K]) spanning 2^31 bytes or
+  // more is past the 32-bit offsets of the direct-to-LDS kernels' buffer
+  // loads. Rather than run the register-staged kernel over the whole product,
+  // such a product is cut into blocks of whole 256-row tiles of that operand
+  // that each span less, every block a product of its own, unsplit, on the
+  // rows (A) or columns (B) of C it owns, in order on the stream. Unsplit
+  // products with a named epilogue only: split-K, a B transposed up front, an
+  // epilogue program and the allocation-free entry point keep the
+  // register-staged kernel.
+  if (!use_scratch && !program_epi && batch == 1 && !packed && !trans_a && plan.splits <= 1 &&
+      !plan.transpose_b && k > 0) {
+    const int64_t esz = dtype_bytes(ab_dtype), cb = dtype_bytes(c_dtype);
+    // Rows of leading dimension ld whose span ((rows - 1) ld + k) esz stays
+    // below 2^31 bytes, in whole 256-row tiles (0: not even one tile).
+    auto fit = [&](int64_t ld) {
+      const int64_t lim = (INT32_MAX - 1) / esz - k;
+      return lim < 0 ? 0 : (lim / ld + 1) / 256 * 256;
+    };
+    auto part = [&](const void* pa, const void* pb, void* pc, int64_t rows, int64_t cols, const void* vb,
+                    const void* vs, const void* vh) {
+      return gemm_impl(ab_dtype, c_dtype, pa, lda, trans_a, pb, ldb, b_layout, b_panel, b_kpad, pc, ldc, rows,
+                       cols, k, 1, 0, 0, 0, vb, vs, vh, vec_dtype, epilogue, epilogue_arg, program, 1, workspace,
+                       workspace_bytes, false, tile_m, tile_n, tile_k, stream);
+    };
+    const int64_t step_a = fit(lda);
+    if (((m - 1) * lda + k) * esz >= INT32_MAX && step_a > 0) {
+      for (int64_t r = 0; r < m; r += step_a) {
+        const int st = part((const char*)a + r * lda * esz, b, (char*)c + r * ldc * cb, std::min(step_a, m - r), n,
+                            bias, scale, shift);
+        if (st != HMX_OK) return st;
+      }
+      return HMX_OK;
+    }
+    const int64_t step_b = fit(ldb);
+    if (lb == L_KCONTIG && ((n - 1) * ldb + k) * esz >= INT32_MAX && step_b > 0) {
+      const int64_t vb = dtype_bytes(vec_dtype);
+      auto at = [&](const void* v, int64_t col) { return v ? (const void*)((const char*)v + col * vb) : nullptr; };
+      for (int64_t col = 0; col < n; col += step_b) {
+        const int st = part(a, (const char*)b + col * ldb * esz, (char*)c + col * cb, m, std::min(step_b, n - col),
+                            at(bias, col), at(scale, col), at(shift, col));
+        if (st != HMX_OK) return st;
+      }
+      return HMX_OK;
+    }
+  }
   // Workspace is checked once the launch is known (below): a B transposed up
   // front (plan.bt_bytes) and f32 partials for split-K or a staged epilogue
   // program. The transposed B is read K-contiguous from the workspace.

@@ -1,13 +1,15 @@
 """Operands past 2^31 bytes, against the CPU oracle on sampled rows.
 
 The direct-to-LDS GEMM kernels address their operands through buffer
-resources with 32-bit offsets, so a GEMM whose A or B spans 2^31 bytes or more
-takes the register-staged kernels, whose loads and stores use 64-bit offsets
-(``hmx_gemm.cpp``'s ``bytes_ok``); the row kernels index rows in 64 bits
-throughout. These tests run both past the 32-bit range: the sampled rows
-include the last ones, whose byte offsets are past 2^31 (GEMM operands) or
-2^32 (row inputs), so an offset truncated to 32 bits would read another row's
-data. Tolerances as in the other parity tests: rtol 1e-2 plus a sqrt(K)-scaled
+resources with 32-bit offsets: a row-major A or a B [N, K] that spans 2^31
+bytes or more is cut into blocks of whole tiles that each span less, one
+product per block (bf16 and f32 A, B [N, K] with the skinny kernel and the
+256 x 256 tiles, bias/scale/shift offset per block); the register-staged
+kernels, whose loads and stores use 64-bit offsets, take what cannot be cut.
+The row kernels index rows in 64 bits throughout. These tests run both past
+the 32-bit range: the sampled rows include the last ones, whose byte offsets
+are past 2^31 (GEMM operands) or 2^32 (row inputs), so an offset truncated to
+32 bits would read another row's data. Tolerances as in the other parity tests: rtol 1e-2 plus a sqrt(K)-scaled
 atol for bf16 GEMMs, rtol 1e-4 for f32; max-normalised error < 1e-2 for bf16
 softmax (the reference's, tests/test_cpu_utils_softmax.py:18-34); one bf16
 rounding for RMSNorm; column sums of integers are exact.
@@ -18,6 +20,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 import helion_mlir_utils as U
 from oracle import restate as R
@@ -68,17 +71,22 @@ def test_matmul_a_past_2gib(gpu_device, dtype: str) -> None:
     torch.cuda.empty_cache()
 
 
-def test_linear_weight_past_2gib(gpu_device) -> None:
-    # B [N, K] (a linear layer's weight) past 2^31 bytes; C's sampled columns.
-    m, n = 256, BIG_ROWS_BF16
+@pytest.mark.parametrize("m", [256, 32])
+def test_linear_weight_past_2gib(gpu_device, m: int) -> None:
+    # B [N, K] (a linear layer's weight) past 2^31 bytes, with bias, scale,
+    # shift and SiLU: C's sampled columns (each block of columns reads its own
+    # run of the vectors). 32 rows take the skinny kernel.
+    n = BIG_ROWS_BF16
     x = _uniform((m, K), torch.bfloat16, gpu_device, 13)
     w = _uniform((n, K), torch.bfloat16, gpu_device, 14)
+    bias, scale, shift = (_uniform((n,), torch.bfloat16, gpu_device, 20 + i) for i in range(3))
     assert w.numel() * 2 > 2**31
-    c = U.matmul(x, w, trans_b=True)
+    c = U.matmul(x, w, trans_b=True, bias=bias, scale=scale, shift=shift, epilogue=F.silu)
     torch.cuda.synchronize()
     cols = torch.from_numpy(_with_last(tile_rows(RNG, n, 1), n)).to(gpu_device)
     got, xn, wn = to_np(c[:, cols]), to_np(x), to_np(w[cols])
-    ref = R.matmul(xn, wn, False, True, out="bf16")
+    vb, vs, vh = (to_np(v[cols]) for v in (bias, scale, shift))
+    ref = R.matmul(xn, wn, False, True, vb, vs, vh, "silu", 0.01, out="bf16")
     _check(got, ref, K, xn, wn, "bf16")
     del x, w, c
     torch.cuda.empty_cache()
