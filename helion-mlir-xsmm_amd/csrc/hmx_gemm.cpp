@@ -1,5 +1,5 @@
 // Host side of the GEMM: the tile table and planner (hmx_gemm_plan), argument
-// checks, the up-front B transpose, kernel selection and the split-K
+// checks, the up-front A and B transposes, kernel selection and the split-K
 // reduction launch (hmx_gemm). The kernels live in hmx_gemm_bf16_*.hip,
 // hmx_gemm_dma.hip and hmx_gemm_f32.hip.
 #include <algorithm>
@@ -82,6 +82,11 @@ struct Plan {
   // kernel path then reads it without register transposes.
   bool transpose_b;
   int64_t bt_bytes;
+  // bf16 A stored [K, M] is first transposed to [M, K] in the workspace
+  // (after the transposed B, at_bytes long), and the product is planned and
+  // run as one of row-major A.
+  bool transpose_a;
+  int64_t at_bytes;
   // M <= 64 against B [N, K]: the skinny kernel (tile 32 x 32 x 64, no
   // split, no workspace).
   bool skinny;
@@ -105,6 +110,17 @@ int small_f32_splits(int64_t tiles, int64_t kt, int64_t outputs, int64_t max_ws,
 
 // Output rows from which a row-major bf16 B is transposed once up front.
 constexpr int64_t kTransposeMinRows = 512;
+
+// M, N and K from which a bf16 A stored [K, M] is transposed once up front,
+// unless the environment sets HMX_GEMM_TRANSPOSE_A=0 (for comparison).
+constexpr int64_t kTransposeAMin = 512;
+bool transpose_a_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("HMX_GEMM_TRANSPOSE_A");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
 
 // Split K while the grid holds fewer workgroups than there are CUs (bf16;
 // for f32's smaller tiles, than four per CU), each chunk keeps at least 8 K
@@ -198,10 +214,33 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
     plan.tile = kSkinny;
     plan.splits = 1;
     plan.k_chunk = k;
-    plan.transpose_b = false;
-    plan.bt_bytes = 0;
+    plan.transpose_b = plan.transpose_a = false;
+    plan.bt_bytes = plan.at_bytes = 0;
     plan.workspace_bytes = 0;
     return HMX_OK;
+  }
+  // Transposed A read in place costs the 256 x 256 kernel two transposing
+  // LDS reads per fragment (4096^3: 114-118 us against 94 for row-major A),
+  // and other shapes of it take the register-staged kernel. A transpose up
+  // front (one HBM read and write of A, ~25 us for 4096^2) is cheaper from
+  // these sizes on (same box, in place -> transposed: 8192^2 x 4096 421 ->
+  // 397 us, 2048^3 43 -> 34, 1024^3 22 -> 20, 3000^3 314 -> 212, 1000 x 4096
+  // x 4096 203 -> 55, 4096 x 1000 x 4096 105 -> 62), except for whole 256 x
+  // 256 tiles the in-place kernel takes with N up to 4096, where the
+  // transpose costs about what it saves (4096^3: 120 us).
+  const bool ta_in_place = m % 256 == 0 && n % 256 == 0 && k % 64 == 0 && (m / 256) * (n / 256) >= cus &&
+                           n <= 4096;
+  plan.transpose_a = bf16 && trans_a && !program && batch == 1 && transpose_a_enabled() &&
+                     (b_layout == HMX_B_ROW || b_layout == HMX_B_TRANS) && m >= kTransposeAMin &&
+                     n >= kTransposeAMin && k >= kTransposeAMin && m * k * 2 < INT32_MAX && !ta_in_place;
+  plan.at_bytes = plan.transpose_a ? ceil_div(m * k * 2, 256) * 256 : 0;
+  if (plan.transpose_a && max_ws >= 0 && plan.at_bytes > max_ws) {
+    plan.transpose_a = false;
+    plan.at_bytes = 0;
+  }
+  if (plan.transpose_a) {
+    trans_a = 0;
+    if (max_ws >= 0) max_ws -= plan.at_bytes;
   }
   const TileChoice* table = bf16 ? kBf16Tiles : kF32Tiles;
   const int count = bf16 ? (int)(sizeof(kBf16Tiles) / sizeof(TileChoice))
@@ -297,7 +336,7 @@ int make_plan(int ab_dtype, int64_t m, int64_t n, int64_t k, int64_t batch, int 
                      n * k * 2 < INT32_MAX &&
                      (max_ws < 0 || plan.bt_bytes + partial_bytes <= max_ws);
   if (!plan.transpose_b) plan.bt_bytes = 0;
-  plan.workspace_bytes = plan.bt_bytes + partial_bytes;
+  plan.workspace_bytes = plan.bt_bytes + plan.at_bytes + partial_bytes;
   return HMX_OK;
 }
 
@@ -386,9 +425,9 @@ Kernel select_kernel(const GemmArgs& g, const Plan& plan, int ab_dtype, int la, 
 // hmx_gemm and hmx_gemm_noalloc: checks, plan, launches. The workspace is
 // `workspace` (workspace_bytes long) or, with `use_scratch`, the library's
 // own per-device scratch array, looked up only when the plan needs workspace.
-// Every workspace byte a launch reads it has written first (the B transpose
-// and each split's whole partial tile), so nothing needs clearing between
-// calls.
+// Every workspace byte a launch reads it has written first (the A and B
+// transposes and each split's whole partial tile), so nothing needs clearing
+// between calls.
 int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a,
               const void* b, int64_t ldb, int b_layout, int64_t b_panel, int64_t b_kpad,
               void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int64_t batch,
@@ -445,11 +484,11 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
   // such a product is cut into blocks of whole 256-row tiles of that operand
   // that each span less, every block a product of its own, unsplit, on the
   // rows (A) or columns (B) of C it owns, in order on the stream. Unsplit
-  // products with a named epilogue only: split-K, a B transposed up front, an
-  // epilogue program and the allocation-free entry point keep the
+  // products with a named epilogue only: split-K, an operand transposed up
+  // front, an epilogue program and the allocation-free entry point keep the
   // register-staged kernel.
   if (!use_scratch && !program_epi && batch == 1 && !packed && !trans_a && plan.splits <= 1 &&
-      !plan.transpose_b && k > 0) {
+      !plan.transpose_b && !plan.transpose_a && k > 0) {
     const int64_t esz = dtype_bytes(ab_dtype), cb = dtype_bytes(c_dtype);
     // Rows of leading dimension ld whose span ((rows - 1) ld + k) esz stays
     // below 2^31 bytes, in whole 256-row tiles (0: not even one tile).
@@ -485,9 +524,10 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
     }
   }
   // Workspace is checked once the launch is known (below): a B transposed up
-  // front (plan.bt_bytes) and f32 partials for split-K or a staged epilogue
-  // program. The transposed B is read K-contiguous from the workspace.
-  if (use_scratch && plan.transpose_b) {
+  // front (plan.bt_bytes), then an A transposed up front (plan.at_bytes), then
+  // f32 partials for split-K or a staged epilogue program. The transposed
+  // operands are read K-contiguous from the workspace.
+  if (use_scratch && (plan.transpose_b || plan.transpose_a)) {
     const int st = scratch_of_current_device(&workspace);
     if (st != HMX_OK) return st;
     workspace_bytes = kScratchBytes;
@@ -499,6 +539,13 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
     b = workspace;
     ldb = k;
     lb_run = L_KCONTIG;
+  }
+  const void* a_given = a;
+  const int64_t lda_given = lda;
+  if (plan.transpose_a) {
+    a = workspace ? (const char*)workspace + plan.bt_bytes : nullptr;
+    lda = k;
+    trans_a = 0;
   }
   int64_t tiles_m = ceil_div(m, plan.tile.bm), tiles_n = ceil_div(n, plan.tile.bn);
   HMX_REQUIRE(tiles_m * tiles_n < ((int64_t)1 << 31) && batch < 65536 && plan.splits < 65536,
@@ -575,9 +622,11 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
   // the GEMM writes f32 partials ([splits, batch, M, N]) with the identity
   // epilogue, and the reduction applies bias, scale, shift and the epilogue.
   const bool staged = plan.splits > 1 || (program_epi && !runs_programs(kind));
-  const int64_t need = plan.bt_bytes + (staged ? (int64_t)std::max(plan.splits, 1) * batch * m * n * 4 : 0);
-  const char* what = plan.splits > 1 ? "split-K" : staged ? "an epilogue program on these operands"
-                                                           : "the B transpose";
+  const int64_t need =
+      plan.bt_bytes + plan.at_bytes + (staged ? (int64_t)std::max(plan.splits, 1) * batch * m * n * 4 : 0);
+  const char* what = plan.splits > 1 ? "split-K"
+                     : staged        ? "an epilogue program on these operands"
+                                     : "the operand transpose";
   if (use_scratch && need > 0) {
     HMX_REQUIRE(need <= kScratchBytes,
                 "gemm_noalloc: %s needs %lld bytes of workspace and the library's scratch holds %lld%s", what,
@@ -592,7 +641,13 @@ int gemm_impl(int ab_dtype, int c_dtype, const void* a, int64_t lda, int trans_a
   HMX_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need),
               "gemm: %s needs %lld workspace bytes, got %lld", what, (long long)need,
               (long long)(workspace ? workspace_bytes : 0));
-  void* partials = workspace ? (char*)workspace + plan.bt_bytes : nullptr;
+  void* partials = workspace ? (char*)workspace + plan.bt_bytes + plan.at_bytes : nullptr;
+  if (plan.transpose_a) {
+    // A [K, M] -> [M, K] in the workspace, after the transposed B.
+    launch_transpose16(a_given, (char*)workspace + plan.bt_bytes, k, m, lda_given, (hipStream_t)stream);
+    const int st = check_launch("gemm A transpose");
+    if (st != HMX_OK) return st;
+  }
   if (plan.transpose_b) {
     // B [K, N] -> B^T [N, K] in the workspace; the GEMM then reads it K-contiguous.
     launch_transpose16(b_given, workspace, k, n, ldb_given, (hipStream_t)stream);

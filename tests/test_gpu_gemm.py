@@ -208,6 +208,27 @@ def test_matmul_trans_a_4096(gpu_device) -> None:
     _check(to_np(c)[rows], R.matmul(an, bn, out="bf16"), 4096, an, bn, "bf16")
 
 
+@pytest.mark.parametrize(("m", "n", "k"), [(4096, 8192, 1024), (1000, 1500, 777), (512, 512, 512),
+                                         (2048, 520, 1024)])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_matmul_trans_a_transposed_up_front(gpu_device, m, n, k, out_dtype) -> None:
+    # From 512 rows, columns and K (but for whole 256 x 256 tiles filling the
+    # CUs with N up to 4096), bf16 A stored [K, M] is transposed once into the
+    # workspace and the product runs as one of row-major A: bit-equal to the
+    # product of the explicitly transposed A, and checked on every tile.
+    at = torch.from_numpy(RNG.uniform(-1, 1, (k, m)).astype(np.float32)).to(torch.bfloat16).to(gpu_device)
+    b = torch.from_numpy(RNG.uniform(-1, 1, (k, n)).astype(np.float32)).to(torch.bfloat16).to(gpu_device)
+    bias = torch.from_numpy(RNG.normal(0, 1, n).astype(np.float32)).to(gpu_device)
+    c = U.matmul(at, b, trans_a=True, bias=bias, epilogue=F.silu, out_dtype=out_dtype)
+    c_nn = U.matmul(at.t().contiguous(), b, bias=bias, epilogue=F.silu, out_dtype=out_dtype)
+    assert torch.equal(c, c_nn)
+    rows = tile_rows(RNG, m)
+    an, bn = to_np(at.t()[torch.from_numpy(rows).to(gpu_device)]), to_np(b)
+    ref = R.matmul(an, bn, False, False, to_np(bias), act="silu",
+                   out="bf16" if out_dtype == torch.bfloat16 else "f32")
+    _check(to_np(c)[rows], ref, k, an, bn, "bf16" if out_dtype == torch.bfloat16 else "f32")
+
+
 def _random_cases(count: int, seed: int) -> list[tuple]:
     rng = np.random.default_rng(seed)
     cases = []
