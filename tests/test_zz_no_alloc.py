@@ -1,5 +1,6 @@
 """hmx_gemm_noalloc: the GEMM entry point that allocates nothing (its split-K
-partials and transposed B live in the library's static per-device scratch),
+partials and transposed A and B live in the library's static per-device
+scratch),
 checked through the C ABI against hmx_gemm, the entry point it mirrors, on
 two calls in a row -- the second smaller, so it reads a scratch that still
 holds the first call's data -- and against the CPU oracle.
@@ -106,6 +107,40 @@ def test_noalloc_bf16_transposed_b_and_epilogue_twice(gpu_device) -> None:
     a2, b2 = _operands(1, 520, 100, 1030, "bf16", gpu_device)
     assert _plan(a2, 520, 100, 1030, 1)[4] > 0
     _check_pair(a2, b2, "bf16", bias[:100].contiguous(), native.EPI_RELU)
+
+
+def test_noalloc_bf16_transposed_a_twice(gpu_device) -> None:
+    # bf16 A stored [K, M] is transposed into the scratch first (after B^T
+    # where B is read transposed too: ragged K); then a smaller product whose
+    # A^T overwrites the start of the same scratch.
+    stream = torch.cuda.current_stream(gpu_device).cuda_stream
+    lib = native.lib()
+    for m, n, k in [(1000, 1500, 777), (600, 520, 640)]:
+        at = tensor(RNG.uniform(-1, 1, (k, m)).astype(np.float32), "bf16", gpu_device)
+        b = tensor(RNG.uniform(-1, 1, (k, n)).astype(np.float32), "bf16", gpu_device)
+        out = [ctypes.c_int() for _ in range(4)]
+        ws = ctypes.c_int64()
+        native.check(lib.hmx_gemm_plan(native.DTYPE_BF16, m, n, k, 1, 1, native.B_ROW, 0, -1, 0, 0, 0,
+                                       native.device_units(gpu_device), native.EPI_IDENTITY,
+                                       *[ctypes.byref(o) for o in out], ctypes.byref(ws)), "hmx_gemm_plan")
+        assert m * k * 2 <= ws.value <= native.GEMM_SCRATCH_BYTES
+        cs = []
+        for noalloc in (True, False):
+            c = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=gpu_device)
+            head = (native.DTYPE_BF16, native.DTYPE_BF16, at.data_ptr(), m, 1, b.data_ptr(), n, native.B_ROW, 0, 0,
+                    c.data_ptr(), n, m, n, k, 1, 0, 0, 0, None, None, None, native.DTYPE_F32,
+                    native.EPI_IDENTITY, 0.0, None, 0)
+            if noalloc:
+                st = lib.hmx_gemm_noalloc(*head, 0, 0, 0, stream)
+            else:
+                w = torch.empty(ws.value, dtype=torch.uint8, device=gpu_device)
+                st = lib.hmx_gemm(*head, w.data_ptr(), ws.value, 0, 0, 0, stream)
+            torch.cuda.synchronize()
+            assert st == native.OK, native.last_error()
+            cs.append(c)
+        assert torch.equal(cs[0], cs[1])
+        exact = R.matmul(to_np(at), to_np(b), True, False, out="bf16")
+        assert max_rel_error(to_np(cs[0]), exact) < 1e-2
 
 
 def test_noalloc_config5_fills_the_scratch(gpu_device) -> None:
