@@ -8,7 +8,7 @@
 
 #include "hmx_gemm_common.hpp"
 
-// The workspace of hmx_gemm_noalloc: split-K partials and the transposed B
+// The workspace of hmx_gemm_noalloc: split-K partials and the transposed A and B
 // of a launch, in device memory the library owns instead of memory a caller
 // allocates. One copy per device, held until the process ends. Host code
 // never uses this name as an address (on the host it names a stand-in, not

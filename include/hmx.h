@@ -230,7 +230,11 @@ const char* hmx_jit_last_log(void);
  * linear layer) with splits 0 or 1 and no tile requested (or the skinny
  * kernel's own 32 x 32 x 64) take a skinny kernel: one workgroup per 32
  * columns of C, K split over its waves and summed in a fixed order, no
- * workspace (hmx_gemm_plan reports tile 32 x 32 x 64).
+ * workspace (hmx_gemm_plan reports tile 32 x 32 x 64). The workspace also
+ * takes a bf16 operand the library transposes once before the product (a
+ * row-major B with ragged K, an A stored [K, M] of 512 or more rows, columns
+ * and K); hmx_gemm_plan counts it. A row-major A or a B [N, K] spanning 2^31
+ * bytes or more runs as one launch per block of whole tiles.
  * Stands in for matmul (helion_mlir_utils/matmul.py:1446-1570), its
  * fused-pack kernel (259-328), the f32 fused and blocked kernels (156-228,
  * 862-904, 1332-1368), split-K (1195-1300), bmm (1842-1882, 1965-2006) and the
@@ -253,7 +257,7 @@ int hmx_gemm(int ab_dtype, int c_dtype,
 #define HMX_GEMM_SCRATCH_BYTES (64ll << 20)
 
 /* hmx_gemm without a caller workspace and without allocating anything: the
- * split-K partials and a transposed B go to a workspace the library holds per
+ * split-K partials and a transposed A or B go to a workspace the library holds per
  * device (a static device array of HMX_GEMM_SCRATCH_BYTES, taken on each
  * device's first call and kept until the process ends). No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
