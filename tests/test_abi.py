@@ -5,6 +5,7 @@ refuses bad arguments before touching a device, and plans launches on the host."
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 import re
 import subprocess
@@ -370,3 +371,33 @@ def test_error_message_is_per_thread(lib: ctypes.CDLL) -> None:
     t.join()
     assert seen == [""]
     assert "unknown dtype" in native.last_error()
+
+
+def test_gemm_plan_transposes_a_up_front(lib: ctypes.CDLL) -> None:
+    # bf16 A stored [K, M] of 512 or more rows, columns and K is transposed
+    # into the workspace (M K 2 bytes, 256-byte rounded), except for whole
+    # 256 x 256 tiles that fill the CUs with N up to 4096, which the in-place
+    # kernel reads; f32, programs, small shapes and too small a workspace
+    # read it in place. The plan reproduces itself when passed back.
+    if os.environ.get("HMX_GEMM_TRANSPOSE_A", "").startswith("0"):
+        pytest.skip("HMX_GEMM_TRANSPOSE_A=0 turns the transpose off")
+    bf16, f32 = native.DTYPE_BF16, native.DTYPE_F32
+    at = lambda m, k: -(-m * k * 2 // 256) * 256  # noqa: E731
+    cases = [((3000, 3000, 3000), True), ((1000, 4096, 4096), True), ((8192, 8192, 4096), True),
+             ((2048, 2048, 2048), True), ((4096, 4096, 4096), False), ((511, 4096, 4096), False),
+             ((4096, 4096, 500), False)]
+    def as_transposed(ab, m, n, k, **kw):
+        # The plan of row-major A (same splits and tile) plus A^T's bytes.
+        plan = _plan(lib, ab, m, n, k, trans_a=1, **kw)
+        plain = _plan(lib, ab, m, n, k, **kw)
+        return plan[:4] == plain[:4] and plan[4] == plain[4] + at(m, k)
+
+    for (m, n, k), transposed in cases:
+        s, tm, tn, tk, ws = _plan(lib, bf16, m, n, k, trans_a=1)
+        assert as_transposed(bf16, m, n, k) == transposed, ((m, n, k), ws)
+        assert _plan(lib, bf16, m, n, k, splits=s, max_ws=ws, tiles=(tm, tn, tk), trans_a=1) == (s, tm, tn, tk, ws)
+        if transposed:
+            # no room for A^T: read in place
+            assert _plan(lib, bf16, m, n, k, max_ws=at(m, k) - 256, trans_a=1)[4] < at(m, k)
+    assert not as_transposed(f32, 3000, 3000, 3000)
+    assert not as_transposed(bf16, 3000, 3000, 3000, epi=native.EPI_PROGRAM)
